@@ -1,0 +1,283 @@
+"""Benchmark of the MI355X DSA path (one GPU).
+
+A step is one sparse-MLA forward over the prefill workload of BASELINE config
+C4 (B=1, Sq=Skv=16384, H=128, d_qk=576, d_v=512, topk=2048, bf16, causal
+indices with -1 padding), timed with HIP events on the launch stream.  The same
+run also measures the lightning indexer + top-k (config C2: 4096 x 32768, 64
+fp8 heads x 128, top-2048) and the paged sparse-MLA decode (config C3: B=64,
+H=128, topk=2048 over a 64K-token paged cache), each with an L2/MALL flush
+before every repetition, and times the CPU oracle on a bounded sample of the
+step workload as the reported CPU baseline.
+
+Prints one JSON line (see the keys below).  Synthetic inputs, seeded.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_FP8_TFLOPS = 5000.0
+PEAK_HBM_GBS = 8000.0
+
+
+def _log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _flush_buffer(torch, dev):
+    return torch.empty(512 * 1024 * 1024 // 4, dtype=torch.float32, device=dev)
+
+
+def _timed(torch, fn, reps, flush=None):
+    """Per-rep device time (ms) from HIP events on the current stream; optional cache flush before each rep."""
+    times = []
+    for _ in range(reps):
+        if flush is not None:
+            flush.zero_()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        e1.synchronize()
+        times.append(e0.elapsed_time(e1))
+    return times
+
+
+def _median(x):
+    s = sorted(x)
+    return s[len(s) // 2]
+
+
+def gen_prefill(torch, dev, S=16384, H=128, topk=2048, seed=20261204):
+    """C4: q, kv ~ N(0,1)*0.5 bf16; row i draws min(topk, i+1) distinct indices from [0, i], -1 padded."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    q = (torch.randn(1, S, H, 576, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    kv = (torch.randn(1, S, 1, 576, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    idx = torch.empty(1, S, 1, topk, dtype=torch.int32, device=dev)
+    cols = torch.arange(S, device=dev).view(1, -1)
+    for r0 in range(0, S, 2048):
+        r1 = min(S, r0 + 2048)
+        u = torch.rand(r1 - r0, S, generator=g, device=dev)
+        u = torch.where(cols <= torch.arange(r0, r1, device=dev).view(-1, 1), u, torch.full_like(u, -1.0))
+        v, i = torch.topk(u, topk, dim=1)
+        idx[0, r0:r1, 0] = torch.where(v >= 0, i, torch.full_like(i, -1)).to(torch.int32)
+        del u, v, i
+    return q, kv, idx
+
+
+def gen_decode(torch, dev, B=64, ctx=65536, H=128, topk=2048, bs=64, seed=20261203):
+    """C3: paged pool of B*ctx/bs blocks, seeded random block table, topk distinct indices per sequence."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    nblk = ctx // bs
+    q = (torch.randn(B, 1, H, 576, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    pool = (torch.randn(B * nblk, bs, 1, 576, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    table = torch.randperm(B * nblk, generator=g, device=dev).view(B, nblk).to(torch.int32)
+    u = torch.rand(B, ctx, generator=g, device=dev)
+    idx = torch.topk(u, topk, dim=1).indices.to(torch.int32).view(B, 1, 1, topk)
+    lens = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+    return q, pool, table, idx, lens
+
+
+def gen_indexer(torch, dev, S1=4096, S2=32768, H=64, D=128, seed=20261202):
+    """C2: q = fp8(N(0,1)); k fp8 per-token with scale absmax/448; w ~ N(0,1)/8."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    q = torch.randn(1, S1, H, D, generator=g, device=dev).to(torch.float8_e4m3fn)
+    kf = torch.randn(1, S2, D, generator=g, device=dev)
+    amax = kf.abs().amax(dim=-1)
+    ks = (amax / 448.0).to(torch.float32)
+    k = (kf / ks.unsqueeze(-1)).clamp(-448, 448).to(torch.float8_e4m3fn).unsqueeze(2).contiguous()
+    w = torch.randn(1, S1, H, generator=g, device=dev) / 8
+    return q, k, w, ks
+
+
+def cpu_baseline_prefill(torch, q, kv, idx, budget_s=12.0):
+    """The oracle (fp32) on the last query rows of the C4 workload, until ~budget_s of CPU time."""
+    from oracle import dsa_oracle as ref
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    S = q.shape[1]
+    H = q.shape[2]
+    rows = 0
+    t0 = time.perf_counter()
+    step = 4
+    while time.perf_counter() - t0 < budget_s and rows < 256:
+        r1 = S - rows
+        r0 = r1 - step
+        qs = q[:, r0:r1].cpu()
+        ids = idx[:, r0:r1].cpu()
+        kvs = kv[:, :r1].cpu()
+        ref.sparse_mla_fwd(qs, kvs, ids, 576 ** -0.5, actual_seq_lengths_query=[step],
+                           actual_seq_lengths_kv=[r1], compute_dtype=torch.float32)
+        rows += step
+    el = time.perf_counter() - t0
+    flops = 2.0 * H * idx.shape[-1] * (576 + 512) * rows
+    return {"value": flops / el / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"oracle sparse_mla_fwd (torch fp32 gather/softmax) on the last {rows} of {S} query rows "
+                      f"of the step workload, {el:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--reps", type=int, default=20, help="repetitions of the secondary (flushed) benchmarks")
+    ap.add_argument("--skip", default="", help="comma list of parts to skip: indexer,decode,cpu")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+    skip = set(filter(None, args.skip.split(",")))
+
+    import torch
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    pkg.load_library()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    # ---------------- step workload: sparse MLA prefill (C4) ----------------
+    S, H, topk = 16384, 128, 2048
+    _log("generating C4 prefill inputs")
+    q, kv, idx = gen_prefill(torch, dev, S=S, H=H, topk=topk)
+    sm_scale = 576 ** -0.5
+    fn = lambda: pkg.sparse_mla_fwd(q, kv, idx, sm_scale)  # noqa: E731
+    for _ in range(args.warmup):
+        fn()
+    torch.cuda.synchronize()
+    _log(f"C4 warmup done; timing {args.steps} steps")
+    t0 = time.perf_counter()
+    step_ms = _timed(torch, fn, args.steps)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = sum(step_ms) / len(step_ms)
+    flops = 2.0 * H * topk * (576 + 512) * S
+    tflops = flops / (ms * 1e-3) / 1e12
+    _log(f"C4 sparse MLA prefill: {ms:.3f} ms/step, {tflops:.1f} TFLOP/s")
+    result = {
+        "metric": "sparse-MLA TFLOPS (% MFMA peak) + indexer/top-k µs @H=128, topk=2048",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)*0.5 bf16 q/kv, causal uniform indices)",
+        "config": {"workload": "C4 sparse MLA prefill", "batch": 1, "seq_len_q": S, "seq_len_kv": S, "heads": H,
+                   "d_qk": 576, "d_v": 512, "topk": topk, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                     "kernel": "sparse_mla_kernel<8,false>", "flops_per_launch": flops},
+        "wall_s_timed_region": round(wall, 4),
+        "step_ms_p10_p90": [round(sorted(step_ms)[len(step_ms) // 10], 4),
+                            round(sorted(step_ms)[(len(step_ms) * 9) // 10], 4)],
+    }
+    cpu_inputs = (q, kv, idx)
+
+    flush = _flush_buffer(torch, dev)
+
+    # ---------------- indexer + top-k (C2) ----------------
+    if "indexer" not in skip:
+        _log("C2 indexer + top-k")
+        qi, ki, wi, ksi = gen_indexer(torch, dev)
+        S1, S2, Hi, K = qi.shape[1], ki.shape[1], qi.shape[2], 2048
+        logits = torch.empty(1, S1, S2, dtype=torch.float32, device=dev)
+        lib = pkg.load_library()
+        from tilelang_ascend_amd import _lib as L
+
+        stream = L.stream_handle(dev)
+        out_idx = torch.empty(S1, K, dtype=torch.int32, device=dev)
+
+        def run_logits():
+            rc = lib.dsa_indexer_logits(L.KIND_FP8_E4M3, qi.data_ptr(), ki.data_ptr(), ksi.data_ptr(), wi.data_ptr(),
+                                        1, S1, S2, Hi, 128, None, None, None, 0, 0, 3, logits.data_ptr(), S2, stream)
+            L.check(rc, "indexer")
+
+        def run_topk():
+            rc = lib.dsa_topk_select(logits.data_ptr(), S2, S1, S2, K, None, 1, out_idx.data_ptr(), None, stream)
+            L.check(rc, "topk")
+
+        def run_both():
+            run_logits()
+            run_topk()
+
+        for f in (run_logits, run_topk, run_both):
+            f()
+        torch.cuda.synchronize()
+        t_log = _median(_timed(torch, run_logits, args.reps, flush))
+        t_topk = _median(_timed(torch, run_topk, args.reps, flush))
+        t_both = _median(_timed(torch, run_both, args.reps, flush))
+        causal_pairs = sum(min(S2, S2 - S1 + t + 1) for t in range(S1))
+        idx_flops = 2.0 * Hi * 128 * S1 * S2
+        idx_tflops = idx_flops / (t_log * 1e-3) / 1e12
+        topk_bytes = S1 * S2 * 4 + S1 * K * 4
+        topk_gbs = topk_bytes / (t_topk * 1e-3) / 1e9
+        result["indexer_topk"] = {
+            "workload": "C2: Sq=4096, Skv=32768, 64 heads x 128 fp8, per-token k scale, causal, top-2048",
+            "us": round(t_both * 1e3, 1),
+            "indexer_us": round(t_log * 1e3, 1),
+            "topk_us": round(t_topk * 1e3, 1),
+            "indexer_tflops_dense": round(idx_tflops, 1),
+            "indexer_frac_fp8_peak": round(idx_tflops / PEAK_FP8_TFLOPS, 4),
+            "indexer_causal_pair_frac": round(causal_pairs / (S1 * S2), 4),
+            "topk_gbs": round(topk_gbs, 1),
+            "topk_frac_hbm": round(topk_gbs / PEAK_HBM_GBS, 4),
+            "roofline_us": round((idx_flops / (PEAK_FP8_TFLOPS * 1e12) + topk_bytes / (PEAK_HBM_GBS * 1e9)) * 1e6, 1),
+        }
+        _log(f"C2: indexer {t_log * 1e3:.1f} us, topk {t_topk * 1e3:.1f} us, both {t_both * 1e3:.1f} us")
+        del qi, ki, wi, ksi, logits, out_idx
+
+    # ---------------- decode (C3) ----------------
+    if "decode" not in skip:
+        _log("C3 paged decode")
+        qd, pool, table, idd, lens = gen_decode(torch, dev)
+        B = qd.shape[0]
+        fnd = lambda: pkg.sparse_mla_fwd(qd, pool, idd, sm_scale, block_table=table,  # noqa: E731
+                                         actual_seq_lengths_kv=lens)
+        fnd()
+        torch.cuda.synchronize()
+        t_dec = _median(_timed(torch, fnd, args.reps, flush))
+        dec_bytes = (B * topk * 576 * 2 + qd.numel() * 2 + B * H * 512 * 2 + B * H * 4 + idd.numel() * 4
+                     + table.numel() * 4)
+        dec_gbs = dec_bytes / (t_dec * 1e-3) / 1e9
+        dec_flops = 2.0 * B * H * topk * (576 + 512)
+        result["decode"] = {
+            "workload": "C3: B=64, Sq=1, H=128, topk=2048, 64K-token paged cache (64-token blocks)",
+            "us": round(t_dec * 1e3, 1),
+            "gbs": round(dec_gbs, 1),
+            "frac_hbm": round(dec_gbs / PEAK_HBM_GBS, 4),
+            "tflops": round(dec_flops / (t_dec * 1e-3) / 1e12, 1),
+            "bytes": dec_bytes,
+            "roofline_us": round(dec_bytes / (PEAK_HBM_GBS * 1e9) * 1e6, 1),
+        }
+        _log(f"C3 decode: {t_dec * 1e3:.1f} us, {dec_gbs:.0f} GB/s")
+        del qd, pool, table, idd
+
+    del flush
+    if "cpu" not in skip:
+        _log("CPU baseline (oracle, bounded sample)")
+        result["cpu_baseline"] = cpu_baseline_prefill(torch, *cpu_inputs)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

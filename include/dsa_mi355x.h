@@ -1,0 +1,127 @@
+/*
+ * C ABI of the MI355X (gfx950) DeepSeek Sparse Attention kernels:
+ * lightning indexer -> top-k selector -> sparse MLA forward.
+ *
+ * Conventions (all entry points):
+ *  - Plain device pointers and sizes; tensors are dense row-major (C order).
+ *  - The library never allocates device memory.  Outputs and workspaces are
+ *    allocated by the caller (the Python layer uses torch's caching allocator);
+ *    workspace sizes come from the *_workspace_size queries.
+ *  - `stream` is a hipStream_t passed as void* (NULL = the legacy default stream).
+ *    Work is enqueued asynchronously; the call returns once it is launched.
+ *  - Return value: 0 on success, otherwise a hipError_t code
+ *    (hipErrorInvalidValue = 1 for rejected arguments; dsa_last_error_message()
+ *    names the offending argument).  The reference's generated entry returns
+ *    void (src/target/codegen_ascend.cc:1138-1225); errors are reported here
+ *    instead of being dropped.
+ *  - Kernels are stateless and reentrant; concurrent calls on different
+ *    streams are safe.
+ */
+#ifndef DSA_MI355X_H_
+#define DSA_MI355X_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element kinds for the indexer's q/k. */
+#define DSA_KIND_FP8_E4M3 0 /* OCP float8 e4m3fn (torch.float8_e4m3fn) */
+#define DSA_KIND_BF16 1
+#define DSA_KIND_FP16 2
+
+/* Library ABI version (major * 100 + minor). */
+int dsa_abi_version(void);
+
+/* Human-readable description of the last argument error on this thread. */
+const char* dsa_last_error_message(void);
+
+/*
+ * Row-wise top-k selector.
+ * Replaces the compiled `simple_topk_selector` kernel's `call()` entry
+ * (examples/topk_selector/example_topk_selector.py:10-54, entry emitted by
+ * src/target/codegen_ascend.cc:1138-1225) and the top-k stage of the
+ * lightning indexer (examples/deepseek_v4/lightning_indexer.py:945-1033).
+ *
+ *  x        [rows, ld] fp32, the first n columns of each row are scored
+ *  row_len  [rows] int32 or NULL: columns >= row_len[r] are excluded
+ *  out_idx  [rows, k] int32; out_val [rows, k] fp32 or NULL
+ *  sorted   1: (value desc, index asc); 0: a fixed data-determined order
+ * Ties go to the lower index; scores <= -1e30, -inf and NaN never take a slot;
+ * unfilled slots hold -1 (value -inf).  1 <= k <= 8192, n < 2^31.
+ */
+int dsa_topk_select(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k, const int32_t* row_len,
+                    int sorted, int32_t* out_idx, float* out_val, void* stream);
+
+/*
+ * Lightning-indexer logits (fp32, masked positions = -inf).
+ * Replaces the QK/ReLU/weighted-head-sum stage of `make_lightning_indexer_kernel`
+ * (examples/deepseek_v4/lightning_indexer.py:338-1197, stages :756-763 and
+ * :868-937) and of `indexer` (examples/lightning_indexer/example_lightning_indexer.py:19-125).
+ *
+ *  q        [B, S1, H, D] of `kind`, D in {64, 128}
+ *  k        [B, S2, D] of `kind`, or with block_table a paged pool
+ *           [num_blocks, block_size, D]
+ *  k_scale  per-key fp32 scale ([B, S2] or [num_blocks, block_size]) or NULL
+ *  weights  [B, S1, H] fp32
+ *  actual_q_len / actual_k_len [B] int32 or NULL (= S1 / S2)
+ *  block_table [B, max_blocks] int32 or NULL
+ *  sparse_mode 0 (no mask) or 3 (causal, bottom-right aligned)
+ *  logits   [B, S1, ld] fp32, ld >= S2
+ * H % 16 == 0 and H <= 64.
+ */
+int dsa_indexer_logits(int kind, const void* q, const void* k, const float* k_scale, const float* weights,
+                       int64_t B, int64_t S1, int64_t S2, int64_t H, int64_t D, const int32_t* actual_q_len,
+                       const int32_t* actual_k_len, const int32_t* block_table, int64_t block_size,
+                       int64_t max_blocks, int sparse_mode, float* logits, int64_t ld, void* stream);
+
+/* Workspace bytes dsa_lightning_indexer needs (the fp32 logits of all rows). */
+size_t dsa_lightning_indexer_workspace_size(int64_t B, int64_t S1, int64_t S2);
+
+/*
+ * Lightning indexer: logits then top-`sparse_count` per query row.
+ * Replaces the `lightning_indexer` wrapper's kernel call
+ * (examples/deepseek_v4/lightning_indexer.py:1202-1370, BSND / PA_BSND keys).
+ *  out_idx [B, S1, sparse_count] int32 (the reference's [B, S1, 1, K])
+ *  out_val [B, S1, sparse_count] fp32 or NULL
+ * The selection is sorted by (score desc, index asc), -1 padded.
+ */
+int dsa_lightning_indexer(int kind, const void* q, const void* k, const float* k_scale, const float* weights,
+                          int64_t B, int64_t S1, int64_t S2, int64_t H, int64_t D, const int32_t* actual_q_len,
+                          const int32_t* actual_k_len, const int32_t* block_table, int64_t block_size,
+                          int64_t max_blocks, int sparse_mode, int64_t sparse_count, int32_t* out_idx,
+                          float* out_val, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes dsa_sparse_mla_fwd needs (0 when no split of the index list is used). */
+size_t dsa_sparse_mla_workspace_size(int64_t B, int64_t S, int64_t H, int64_t topk);
+
+/*
+ * Sparse MLA forward with LSE.
+ * Replaces `sparse_attention_fwd` (examples/sparse_flash_attention/example_sparse_flash_attn.py:18-243,
+ * paged variant example_sparse_flash_attn_mask_pa.py:13-333) and adds the LSE output
+ * of `sparse_flash_mla(..., return_softmax_lse=True)`
+ * (examples/deepseek_v4/sparse_flash_mla/sparse_flash_mla_api.py:94-253).
+ *
+ *  kind     DSA_KIND_BF16 or DSA_KIND_FP16 (q, kv and out share it)
+ *  q        [B, S, H, d_qk]
+ *  kv       [B, Skv, d_qk], or with block_table a paged pool
+ *           [num_blocks, block_size, d_qk]; V = kv[..., :d_v]
+ *  indices  [B, S, topk] int32, -1 = empty slot
+ *  block_table [B, max_blocks] int32 or NULL
+ *  actual_q_len / actual_kv_len [B] int32 or NULL (= S / Skv or max_blocks*block_size)
+ *  out      [B, S, H, d_v] of `kind`;  lse [B, S, H] fp32 (natural log)
+ * d_qk == 576, d_v == 512, H % 16 == 0, indices unique per row.
+ */
+int dsa_sparse_mla_fwd(int kind, const void* q, const void* kv, const int32_t* indices, const int32_t* block_table,
+                       const int32_t* actual_q_len, const int32_t* actual_kv_len, int64_t B, int64_t S,
+                       int64_t H, int64_t d_qk, int64_t d_v, int64_t Skv, int64_t block_size, int64_t max_blocks,
+                       int64_t topk, float sm_scale, int is_causal, void* out, float* lse, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSA_MI355X_H_ */

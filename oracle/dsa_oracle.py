@@ -1,0 +1,334 @@
+"""CPU oracle for the DeepSeek Sparse Attention (DSA) inference path.
+
+TEST INFRASTRUCTURE ONLY.  Nothing in the product path imports this module:
+only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` use it, and only as the checker (or the timed CPU baseline).
+
+It restates, in plain torch/numpy on the CPU, the reference's own goldens for
+the three kernels of the path (all paths relative to the reference checkout):
+
+* lightning indexer  -- ``examples/lightning_indexer/example_lightning_indexer.py:137-144``
+  (``index_golden``) and ``examples/deepseek_v4/lightning_indexer.py:199-335``
+  (``cpu_lightning_indexer``).  Superset: an optional per-key fp32 scale
+  multiplies the head-weighted ReLU sum (fp8-e4m3 keys carry one scale per
+  token); with ``k_scale=None`` it is exactly the reference formula.
+* top-k selector     -- ``examples/topk_selector/example_topk_selector.py:57-58``
+  with the tie rule of ``examples/deepseek_v4/lightning_indexer.py:317-325``
+  (stable descending sort, lower index wins, selected scores <= -1e30 -> -1).
+* sparse MLA forward -- gather form of
+  ``examples/sparse_flash_attention/sfa_golden.py:64-199`` and
+  ``examples/deepseek_v4/sparse_attention.py:171-198`` (``-1`` padding), with the
+  natural-log LSE of
+  ``examples/deepseek_v4/sparse_flash_mla/sparse_flash_mla_golden.py:149``;
+  the dense scatter-mask form of
+  ``examples/sparse_flash_attention/example_sparse_flash_attn.py:255-292`` is
+  restated too, as an independent cross-check on tiny shapes.
+
+How each function is pinned (see ``tests/test_oracle.py``):
+
+* ``topk_stable``: the reference's own known-answer tests (``arange`` sort and
+  top-k KATs, ``testing/python/language/test_tilelang_ascend_language_elementwise.py:4030-4248``),
+  ``torch.topk`` on tie-free rows, brute force on tiny integer rows full of
+  ties, constant rows and masked rows.
+* ``indexer_logits``: explicit-loop brute force on tiny shapes, one-hot
+  weights (isolates one head's ReLU(q.k)), linearity in the weights,
+  homogeneity in the key scale, causal row lengths, and a one-hot q/k probe
+  that fails on transposed operands.
+* ``sparse_mla_fwd``: the dense-mask restatement, a single valid index
+  (out = V row, lse = scale.q.k), equal scores (mean of V), permutation
+  invariance, ``-1`` padding equal to dropping the slot, LSE against
+  ``torch.logsumexp``.
+* ``fp8_quantize_per_token``: absmax maps to 448, representable values round
+  trip exactly.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Sequence, Tuple
+
+import numpy as np
+import torch
+
+NEG_INF = float("-inf")
+# examples/deepseek_v4/lightning_indexer.py:322 -- selected scores at or below
+# this threshold are reported as index -1.
+INVALID_SCORE = -1e30
+FP8_MAX = 448.0
+
+
+# ----------------------------------------------------------------------------
+# fp8 e4m3 (OCP "fn": no inf, max 448) per-token quantiser.  Not in the
+# reference (its act_quant is int8, deepseek_v4/act_quant.py:33-92); this is the
+# producer BASELINE's fp8 indexer inputs assume.
+# ----------------------------------------------------------------------------
+def fp8_quantize_per_token(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """x[..., D] float -> (x_fp8 [..., D] float8_e4m3fn, scale [...] fp32), scale = absmax/448."""
+    xf = x.to(torch.float32)
+    amax = xf.abs().amax(dim=-1)
+    scale = torch.where(amax > 0, amax / FP8_MAX, torch.ones_like(amax))
+    q = (xf / scale.unsqueeze(-1)).clamp(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn)
+    return q, scale.to(torch.float32)
+
+
+# ----------------------------------------------------------------------------
+# Lightning indexer logits
+# ----------------------------------------------------------------------------
+def causal_valid_len(aq: int, ak: int, s1: int, sparse_mode: int) -> int:
+    """Number of valid key positions for query row s1.
+
+    examples/deepseek_v4/lightning_indexer.py:308-314: with sparse_mode 3 row s1
+    sees keys s < ak - aq + s1 + 1; a non-positive bound falls back to ak.
+    """
+    if sparse_mode == 3:
+        cl = ak - aq + s1 + 1
+        return cl if cl > 0 else ak
+    return ak
+
+
+def indexer_logits(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    weights: torch.Tensor,
+    k_scale: Optional[torch.Tensor] = None,
+    *,
+    actual_q_len: Optional[Sequence[int]] = None,
+    actual_k_len: Optional[Sequence[int]] = None,
+    sparse_mode: int = 3,
+    row_chunk: int = 256,
+) -> torch.Tensor:
+    """logits[b, t, s] = k_scale[b, s] * sum_h w[b, t, h] * ReLU(q[b, t, h, :] . k[b, s, :]).
+
+    q [B, S1, H, D] (fp8/fp16/bf16/fp32), k [B, S2, D] (or [B, S2, 1, D]),
+    weights [B, S1, H], k_scale [B, S2] or None.  Returns fp32 [B, S1, S2] with
+    masked positions (causal / beyond actual lengths / padded rows) = -inf.
+    Follows examples/deepseek_v4/lightning_indexer.py:291-316 (einsum, ReLU,
+    weighted head sum, causal mask) and example_lightning_indexer.py:137-142.
+    Rows are processed in chunks so the [rows, H, S2] intermediate stays small
+    (the reference materialises it whole, 34 GB at the largest config).
+    """
+    if k.dim() == 4:
+        k = k[:, :, 0, :]
+    B, S1, H, D = q.shape
+    S2 = k.shape[1]
+    aq_l = [S1] * B if actual_q_len is None else [int(x) for x in actual_q_len]
+    ak_l = [S2] * B if actual_k_len is None else [int(x) for x in actual_k_len]
+    out = torch.full((B, S1, S2), NEG_INF, dtype=torch.float32)
+    qf = q.to(torch.float32)
+    kf = k.to(torch.float32)
+    wf = weights.to(torch.float32)
+    sc = None if k_scale is None else k_scale.to(torch.float32)
+    for b in range(B):
+        aq, ak = aq_l[b], ak_l[b]
+        if aq == 0 or ak == 0:
+            continue
+        kb = kf[b, :ak].to(torch.float64)  # [ak, D]
+        for r0 in range(0, aq, row_chunk):
+            r1 = min(aq, r0 + row_chunk)
+            qb = qf[b, r0:r1].to(torch.float64)  # [r, H, D]
+            wb = wf[b, r0:r1].to(torch.float64)  # [r, H]
+            qk = torch.relu(torch.einsum("rhd,sd->rhs", qb, kb))
+            score = torch.einsum("rhs,rh->rs", qk, wb)
+            if sc is not None:
+                score = score * sc[b, :ak].to(torch.float64)[None, :]
+            score = score.to(torch.float32)
+            for i in range(r1 - r0):
+                nv = causal_valid_len(aq, ak, r0 + i, sparse_mode)
+                score[i, nv:] = NEG_INF
+            out[b, r0:r1, :ak] = score
+    return out
+
+
+# ----------------------------------------------------------------------------
+# Top-k selector
+# ----------------------------------------------------------------------------
+def topk_stable(scores: torch.Tensor, k: int, valid_len: Optional[Sequence[int]] = None
+                ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Row-wise top-k of fp32 scores [R, N] -> (idx int32 [R, k], values fp32 [R, k]).
+
+    examples/deepseek_v4/lightning_indexer.py:317-325: a stable descending sort
+    (ties -> lower index first), the first min(k, n) taken, any selected score
+    <= -1e30 reported as index -1; slots past n hold -1 / -inf.  NaN scores
+    are treated as -inf (a documented choice of this build).  Columns at or
+    beyond ``valid_len[r]`` are excluded (equivalent to -inf).
+    """
+    x = scores.detach().to(torch.float32).cpu().clone()
+    R, N = x.shape
+    x = torch.where(torch.isnan(x), torch.full_like(x, NEG_INF), x)
+    if valid_len is not None:
+        cols = torch.arange(N)[None, :]
+        vl = torch.as_tensor([int(v) for v in valid_len]).view(-1, 1)
+        x = torch.where(cols < vl, x, torch.full_like(x, NEG_INF))
+    idx = torch.full((R, k), -1, dtype=torch.int32)
+    val = torch.full((R, k), NEG_INF, dtype=torch.float32)
+    if N == 0 or R == 0:
+        return idx, val
+    kk = min(k, N)
+    order = torch.argsort(-x, dim=1, stable=True)[:, :kk]
+    topv = x.gather(1, order)
+    topi = order.to(torch.int32)
+    topi = torch.where(topv <= INVALID_SCORE, torch.full_like(topi, -1), topi)
+    topv = torch.where(topv <= INVALID_SCORE, torch.full_like(topv, NEG_INF), topv)
+    idx[:, :kk] = topi
+    val[:, :kk] = topv
+    return idx, val
+
+
+def lightning_indexer(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    weights: torch.Tensor,
+    k_scale: Optional[torch.Tensor] = None,
+    *,
+    actual_q_len: Optional[Sequence[int]] = None,
+    actual_k_len: Optional[Sequence[int]] = None,
+    sparse_count: int = 2048,
+    sparse_mode: int = 3,
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(indices [B, S1, 1, K] int32, values [B, S1, 1, K] fp32, logits [B, S1, S2]).
+
+    examples/deepseek_v4/lightning_indexer.py:199-335 for the BSND layout.
+    """
+    logits = indexer_logits(q, k, weights, k_scale, actual_q_len=actual_q_len,
+                            actual_k_len=actual_k_len, sparse_mode=sparse_mode)
+    B, S1, S2 = logits.shape
+    idx, val = topk_stable(logits.view(B * S1, S2), sparse_count)
+    return idx.view(B, S1, 1, sparse_count), val.view(B, S1, 1, sparse_count), logits
+
+
+# ----------------------------------------------------------------------------
+# Sparse MLA forward
+# ----------------------------------------------------------------------------
+def _gather_rows(kv: torch.Tensor, b: int, idx: torch.Tensor,
+                 block_table: Optional[torch.Tensor], block_size: int) -> torch.Tensor:
+    """KV rows for batch b at logical positions idx (all >= 0)."""
+    if block_table is None:
+        return kv[b, idx.long(), 0, :]
+    blk = block_table[b, (idx // block_size).long()].long()
+    return kv[blk, (idx % block_size).long(), 0, :]
+
+
+def sparse_mla_fwd(
+    q: torch.Tensor,
+    kv: torch.Tensor,
+    indices: torch.Tensor,
+    sm_scale: Optional[float] = None,
+    *,
+    d_v: int = 512,
+    block_table: Optional[torch.Tensor] = None,
+    actual_seq_lengths_query: Optional[Sequence[int]] = None,
+    actual_seq_lengths_kv: Optional[Sequence[int]] = None,
+    is_causal: bool = True,
+    compute_dtype: torch.dtype = torch.float64,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Sparse MLA forward, gather form.  Returns (out fp32 [B,S,H,d_v], lse fp32 [B,S,H]).
+
+    q [B, S, H, Dqk]; kv [B, Skv, 1, Dqk] or, with ``block_table`` [B, nblk],
+    a paged pool [num_blocks, block_size, 1, Dqk]; indices [B, S, 1, topk]
+    int32.  V is kv[..., :d_v] (example_sparse_flash_attn.py:270-271).
+
+    Slot j of row (b, s) is valid iff idx >= 0, idx < kv_len[b] and, when
+    causal, idx <= kv_len[b] - q_len[b] + s (example_sparse_flash_attn_mask_pa.py:221-224,
+    sfa_golden.py:85-101).  Scores are scale * q.k in fp32
+    (sfa_golden.py:183-184), softmax over the valid slots, out = P V
+    (sfa_golden.py:193), lse = max + ln(sum exp) in natural log
+    (sparse_flash_mla_golden.py:149).  A row with no valid slot gives out = 0,
+    lse = -inf.  Duplicate indices in a row are a precondition violation.
+    """
+    B, S, H, Dqk = q.shape
+    if sm_scale is None:
+        sm_scale = Dqk ** -0.5  # example_sparse_flash_attn.py:36
+    paged = block_table is not None
+    if paged:
+        block_size = kv.shape[1]
+        skv_default = block_table.shape[1] * block_size
+    else:
+        block_size = 0
+        skv_default = kv.shape[1]
+    ql = [S] * B if actual_seq_lengths_query is None else [int(x) for x in actual_seq_lengths_query]
+    kl = [skv_default] * B if actual_seq_lengths_kv is None else [int(x) for x in actual_seq_lengths_kv]
+    idx_all = indices.reshape(B, S, -1).to(torch.int64).cpu()
+    out = torch.zeros((B, S, H, d_v), dtype=torch.float32)
+    lse = torch.full((B, S, H), NEG_INF, dtype=torch.float32)
+    qf = q.to(torch.float32)
+    kvf = kv.to(torch.float32)
+    for b in range(B):
+        for s in range(ql[b]):
+            row = idx_all[b, s]
+            valid = (row >= 0) & (row < kl[b])
+            if is_causal:
+                valid &= row <= kl[b] - ql[b] + s
+            sel = row[valid]
+            if sel.numel() == 0:
+                continue
+            assert torch.unique(sel).numel() == sel.numel(), "indices must be unique per row"
+            kr = _gather_rows(kvf, b, sel, block_table if paged else None, block_size).to(compute_dtype)
+            qr = qf[b, s].to(compute_dtype)  # [H, Dqk]
+            sc = (qr @ kr.T) * sm_scale  # [H, n]
+            m = sc.amax(dim=1, keepdim=True)
+            p = torch.exp(sc - m)
+            l = p.sum(dim=1, keepdim=True)
+            out[b, s] = ((p / l) @ kr[:, :d_v]).to(torch.float32)
+            lse[b, s] = (m + torch.log(l)).squeeze(1).to(torch.float32)
+    return out, lse
+
+
+def sparse_mla_dense_ref(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tensor,
+                         q_start_index_s: Optional[int] = None, sm_scale: Optional[float] = None,
+                         d_v: int = 512) -> torch.Tensor:
+    """Dense scatter-mask restatement of example_sparse_flash_attn.py:255-292 (kv_stride 1).
+
+    Builds the [B, S, Skv] boolean mask from the indices (-1 slots dropped), ANDs
+    the causal mask q_start + t >= j, and runs a dense masked softmax.  Used on
+    tiny shapes only, as an independent check of ``sparse_mla_fwd``.
+    """
+    qf = q.to(torch.float64)
+    kvf = kv.to(torch.float64)[:, :, 0, :]
+    B, S, H, Dqk = q.shape
+    Skv = kv.shape[1]
+    if q_start_index_s is None:
+        q_start_index_s = Skv - S
+    if sm_scale is None:
+        sm_scale = Dqk ** -0.5
+    idx = indices.reshape(B, S, -1).long()
+    safe = torch.where(idx < 0, torch.full_like(idx, Skv), idx)
+    mask = torch.zeros(B, S, Skv + 1, dtype=torch.bool).scatter(2, safe, True)[..., :Skv]
+    causal = torch.arange(q_start_index_s, q_start_index_s + S).view(-1, 1) >= torch.arange(Skv).view(1, -1)
+    mask &= causal.view(1, S, Skv)
+    score = torch.einsum("bshd,bnd->bshn", qf, kvf)
+    score = score.masked_fill(~mask.view(B, S, 1, Skv), float("-inf")) * sm_scale
+    p = score.softmax(dim=-1)
+    p = torch.nan_to_num(p, nan=0.0)
+    return torch.einsum("bshn,bnd->bshd", p, kvf[..., :d_v]).to(torch.float32)
+
+
+# ----------------------------------------------------------------------------
+# Seeded input generators for the benchmark configurations
+# ----------------------------------------------------------------------------
+def _gen(seed: int) -> torch.Generator:
+    return torch.Generator().manual_seed(seed)
+
+
+def causal_sparse_indices(B: int, S: int, Skv: int, topk: int, seed: int,
+                          q_start: Optional[int] = None) -> torch.Tensor:
+    """indices [B, S, 1, topk] int32: row t draws min(topk, q_start+t+1) distinct
+    positions from [0, q_start+t] without replacement, -1 padded.
+
+    Vectorised: top-k of i.i.d. uniform keys over the causal range is a uniform
+    sample without replacement.
+    """
+    if q_start is None:
+        q_start = Skv - S
+    g = _gen(seed)
+    out = torch.full((B, S, 1, topk), -1, dtype=torch.int32)
+    chunk = max(1, (1 << 24) // max(Skv, 1))
+    for b in range(B):
+        for r0 in range(0, S, chunk):
+            r1 = min(S, r0 + chunk)
+            u = torch.rand((r1 - r0, Skv), generator=g)
+            lim = torch.arange(r0, r1).view(-1, 1) + q_start + 1
+            u = torch.where(torch.arange(Skv).view(1, -1) < lim, u, torch.full_like(u, -1.0))
+            kk = min(topk, Skv)
+            v, i = torch.topk(u, kk, dim=1)
+            i = torch.where(v >= 0, i, torch.full_like(i, -1)).to(torch.int32)
+            out[b, r0:r1, 0, :kk] = i
+    return out

@@ -1,0 +1,82 @@
+"""CPU checks of the boundary: the library loads, exports every symbol declared
+in include/*.h, and rejects bad arguments (no kernel is launched)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared_functions():
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        for m in re.finditer(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\*?\s*(dsa_[A-Za-z0-9_]+)\s*\(", text, re.M):
+            names.add(m.group(1))
+    return names
+
+
+def test_header_declares_the_entry_points():
+    names = _declared_functions()
+    assert {"dsa_topk_select", "dsa_indexer_logits", "dsa_lightning_indexer", "dsa_sparse_mla_fwd",
+            "dsa_sparse_mla_workspace_size", "dsa_lightning_indexer_workspace_size"} <= names
+
+
+def test_library_exports_every_declared_symbol(dsa):
+    lib = ctypes.CDLL(str(dsa.library_path()))
+    missing = [n for n in sorted(_declared_functions()) if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_binding_signatures_cover_the_header(dsa):
+    from importlib import import_module
+    lib_mod = import_module("tilelang_ascend_amd._lib")
+    assert set(lib_mod.SIGNATURES) == _declared_functions()
+
+
+def test_abi_rejects_bad_arguments_without_launching(dsa):
+    lib = dsa.load_library()
+    assert lib.dsa_abi_version() == 100
+    # k out of range
+    assert lib.dsa_topk_select(None, 8, 1, 8, 0, None, 1, None, None, None) == 1
+    assert b"k must be" in lib.dsa_last_error_message()
+    # indexer: bad head dim
+    assert lib.dsa_indexer_logits(0, None, None, None, None, 1, 1, 1, 16, 96, None, None, None, 0, 0, 3, None, 1,
+                                  None) == 1
+    assert b"head dim" in lib.dsa_last_error_message()
+    # sparse MLA: wrong dims
+    assert lib.dsa_sparse_mla_fwd(1, None, None, None, None, None, None, 1, 1, 16, 512, 512, 16, 0, 0, 16, 1.0, 1,
+                                  None, None, None, 0, None) == 1
+    assert b"d_qk" in lib.dsa_last_error_message()
+    # sparse MLA: workspace too small when the index list is split
+    need = lib.dsa_sparse_mla_workspace_size(1, 1, 128, 2048)
+    assert need > 0
+    assert lib.dsa_sparse_mla_fwd(1, 8, 8, 8, None, None, None, 1, 1, 128, 576, 512, 4096, 0, 0, 2048, 1.0, 1,
+                                  8, 8, None, need - 1, None) == 1
+    assert b"workspace" in lib.dsa_last_error_message()
+
+
+def test_python_layer_refuses_cpu_tensors(dsa):
+    x = torch.randn(4, 64)
+    with pytest.raises(ValueError, match="HIP"):
+        dsa.topk_selector(x, 8)
+    q = torch.zeros(1, 2, 16, 576, dtype=torch.bfloat16)
+    kv = torch.zeros(1, 8, 1, 576, dtype=torch.bfloat16)
+    idx = torch.zeros(1, 2, 1, 4, dtype=torch.int32)
+    with pytest.raises(ValueError, match="HIP"):
+        dsa.sparse_mla_fwd(q, kv, idx)
+
+
+def test_python_layer_validation_messages(dsa):
+    q = torch.zeros(1, 2, 16, 128, dtype=torch.float16)
+    with pytest.raises(ValueError, match="sparse_count"):
+        dsa.lightning_indexer(q, q, torch.zeros(1, 2, 16), sparse_count=3000)
+    with pytest.raises(ValueError, match="sparse_mode"):
+        dsa.lightning_indexer(q, q, torch.zeros(1, 2, 16), sparse_mode=1)
+    with pytest.raises(ValueError, match="dtype"):
+        dsa.lightning_indexer(q, q.to(torch.bfloat16), torch.zeros(1, 2, 16))
+    with pytest.raises(ValueError, match="non-casual|non-causal"):
+        dsa.sparse_attention_fwd(128, 512, 64, 2048, is_causal=False)

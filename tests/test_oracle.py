@@ -1,0 +1,243 @@
+"""Pins the CPU oracle (oracle/dsa_oracle.py) against the reference's known-answer
+tests, brute force and closed forms.  CPU only."""
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import dsa_oracle as ref
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+# --------------------------------------------------------------------------- top-k
+def test_topk_kat_sort_arange131():
+    d = np.load(GOLDEN / "kat_sort_arange131.npz")
+    idx, val = ref.topk_stable(torch.from_numpy(d["x"]), d["x"].shape[1])
+    assert np.array_equal(idx.numpy(), d["idx"])
+    assert np.array_equal(val.numpy(), d["val"])
+
+
+def test_topk_kat_topk_arange51():
+    d = np.load(GOLDEN / "kat_topk_arange51_k10.npz")
+    idx, val = ref.topk_stable(torch.from_numpy(d["x"]), int(d["k"]))
+    assert np.array_equal(idx.numpy(), d["idx"])
+    assert np.array_equal(val.numpy(), d["val"])
+
+
+def test_topk_ties_brute_force():
+    d = np.load(GOLDEN / "ties_topk.npz")
+    idx, val = ref.topk_stable(torch.from_numpy(d["x"]), int(d["k"]))
+    assert np.array_equal(idx.numpy(), d["idx"])
+    assert np.array_equal(val.numpy(), d["val"])
+
+
+def test_topk_matches_torch_topk_without_ties():
+    g = torch.Generator().manual_seed(0)
+    x = torch.stack([torch.randperm(4096, generator=g) for _ in range(64)]).float() * 0.37 - 700.0
+    assert all(torch.unique(r).numel() == r.numel() for r in x)
+    idx, val = ref.topk_stable(x, 2048)
+    tv, ti = torch.topk(x, 2048, dim=1, largest=True, sorted=True)
+    assert torch.equal(idx, ti.to(torch.int32))
+    assert torch.equal(val, tv)
+
+
+def test_topk_constant_rows_take_lowest_indices():
+    x = torch.full((3, 100), 1.5)
+    idx, _ = ref.topk_stable(x, 10)
+    assert torch.equal(idx, torch.arange(10, dtype=torch.int32).expand(3, 10))
+
+
+def test_topk_valid_len_and_padding():
+    x = torch.arange(20, dtype=torch.float32).view(1, 20)
+    idx, _ = ref.topk_stable(x, 8, valid_len=[5])
+    assert idx.tolist() == [[4, 3, 2, 1, 0, -1, -1, -1]]
+
+
+# --------------------------------------------------------------------------- fp8 quantiser
+def test_fp8_quantiser_absmax_and_roundtrip():
+    x = torch.tensor([[1.0, -2.0, 0.5, 4.0], [0.0, 0.0, 0.0, 0.0]])
+    q, s = ref.fp8_quantize_per_token(x)
+    assert s[0].item() == pytest.approx(4.0 / 448.0)
+    assert q[0, 3].float().item() == 448.0
+    # Values that are exact multiples of the scale by e4m3-representable numbers round-trip.
+    assert torch.equal((q[0].float() * s[0]), x[0])
+    assert torch.equal(q[1].float(), torch.zeros(4)) and s[1].item() == 1.0
+
+
+# --------------------------------------------------------------------------- indexer logits
+def _brute_logits(q, k, w, scale, sparse_mode):
+    B, S1, H, D = q.shape
+    S2 = k.shape[1]
+    out = torch.full((B, S1, S2), float("-inf"))
+    for b in range(B):
+        for t in range(S1):
+            lim = ref.causal_valid_len(S1, S2, t, sparse_mode)
+            for s in range(lim):
+                acc = 0.0
+                for h in range(H):
+                    dot = sum(float(q[b, t, h, d]) * float(k[b, s, d]) for d in range(D))
+                    acc += float(w[b, t, h]) * max(dot, 0.0)
+                out[b, t, s] = acc * (1.0 if scale is None else float(scale[b, s]))
+    return out
+
+
+@pytest.mark.parametrize("sparse_mode", [0, 3])
+def test_indexer_logits_brute_force(sparse_mode):
+    g = torch.Generator().manual_seed(1)
+    B, S1, S2, H, D = 2, 3, 7, 4, 5
+    q = torch.randn(B, S1, H, D, generator=g)
+    k = torch.randn(B, S2, D, generator=g)
+    w = torch.randn(B, S1, H, generator=g)
+    sc = torch.rand(B, S2, generator=g) + 0.5
+    got = ref.indexer_logits(q, k, w, sc, sparse_mode=sparse_mode)
+    want = _brute_logits(q, k, w, sc, sparse_mode)
+    assert torch.equal(torch.isinf(got), torch.isinf(want))
+    fin = torch.isfinite(want)
+    torch.testing.assert_close(got[fin], want[fin], rtol=1e-5, atol=1e-5)
+
+
+def test_indexer_logits_one_hot_probe_catches_transposes():
+    # q nonzero only at (t=1, h=2, d=3); k only at (s=4, d=3): the single positive
+    # logit must land at [t=1, s=4] and carry w[1, 2] * q * k * scale[4].
+    B, S1, S2, H, D = 1, 3, 6, 4, 8
+    q = torch.zeros(B, S1, H, D)
+    k = torch.zeros(B, S2, D)
+    q[0, 1, 2, 3] = 2.0
+    k[0, 4, 3] = 3.0
+    w = torch.zeros(B, S1, H)
+    w[0, 1, 2] = 0.5
+    sc = torch.arange(1, S2 + 1, dtype=torch.float32).view(1, S2)
+    got = ref.indexer_logits(q, k, w, sc, sparse_mode=0)
+    want = torch.zeros(B, S1, S2)
+    want[0, 1, 4] = 0.5 * 6.0 * 5.0
+    assert torch.equal(got, want)
+
+
+def test_indexer_logits_linear_in_weights_and_homogeneous_in_scale():
+    g = torch.Generator().manual_seed(2)
+    B, S1, S2, H, D = 1, 8, 32, 16, 16
+    q = torch.randn(B, S1, H, D, generator=g)
+    k = torch.randn(B, S2, D, generator=g)
+    w1 = torch.randn(B, S1, H, generator=g)
+    w2 = torch.randn(B, S1, H, generator=g)
+    sc = torch.rand(B, S2, generator=g) + 0.1
+    a = ref.indexer_logits(q, k, w1 + w2, sc, sparse_mode=0)
+    b = ref.indexer_logits(q, k, w1, sc, sparse_mode=0) + ref.indexer_logits(q, k, w2, sc, sparse_mode=0)
+    torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5)
+    c = ref.indexer_logits(q, k, w1, 3.0 * sc, sparse_mode=0)
+    torch.testing.assert_close(c, 3.0 * ref.indexer_logits(q, k, w1, sc, sparse_mode=0), rtol=1e-5, atol=1e-5)
+
+
+def test_indexer_logits_one_hot_weight_is_relu_gemm():
+    g = torch.Generator().manual_seed(3)
+    B, S1, S2, H, D = 1, 5, 9, 4, 8
+    q = torch.randn(B, S1, H, D, generator=g)
+    k = torch.randn(B, S2, D, generator=g)
+    w = torch.zeros(B, S1, H)
+    w[..., 1] = 1.0
+    got = ref.indexer_logits(q, k, w, sparse_mode=0)
+    want = torch.relu(q[0, :, 1, :].double() @ k[0].double().T).float()
+    torch.testing.assert_close(got[0], want, rtol=1e-6, atol=1e-6)
+
+
+def test_indexer_causal_row_lengths():
+    B, S1, S2 = 1, 4, 10
+    out = ref.indexer_logits(torch.ones(B, S1, 16, 8), torch.ones(B, S2, 8), torch.ones(B, S1, 16), sparse_mode=3)
+    finite = torch.isfinite(out[0]).sum(dim=1).tolist()
+    assert finite == [S2 - S1 + t + 1 for t in range(S1)]
+
+
+# --------------------------------------------------------------------------- sparse MLA
+def _mla_inputs(B=1, S=6, Skv=64, H=16, topk=16, seed=5):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, S, H, 576, generator=g) * 0.5
+    kv = torch.randn(B, Skv, 1, 576, generator=g) * 0.5
+    idx = ref.causal_sparse_indices(B, S, Skv, topk, seed=seed)
+    return q, kv, idx
+
+
+def test_mla_gather_equals_dense_mask_restatement():
+    q, kv, idx = _mla_inputs()
+    idx[0, 2, 0, 5:] = -1  # padded slots drop out
+    out, _ = ref.sparse_mla_fwd(q, kv, idx)
+    dense = ref.sparse_mla_dense_ref(q, kv, idx)
+    torch.testing.assert_close(out, dense, rtol=1e-5, atol=1e-5)
+
+
+def test_mla_single_index_closed_form():
+    q, kv, _ = _mla_inputs(S=1)
+    idx = torch.full((1, 1, 1, 8), -1, dtype=torch.int32)
+    idx[0, 0, 0, 3] = 17
+    out, lse = ref.sparse_mla_fwd(q, kv, idx)
+    torch.testing.assert_close(out[0, 0], kv[0, 17, 0, :512].expand(16, 512), rtol=1e-6, atol=1e-6)
+    want = (q[0, 0].double() @ kv[0, 17, 0].double()) / math.sqrt(576)
+    torch.testing.assert_close(lse[0, 0].double(), want, rtol=1e-6, atol=1e-6)
+
+
+def test_mla_equal_scores_give_mean_and_log_n():
+    B, S, Skv, H, topk = 1, 1, 32, 16, 8
+    q = torch.zeros(B, S, H, 576)
+    kv = torch.randn(B, Skv, 1, 576)
+    idx = torch.arange(topk, dtype=torch.int32).view(1, 1, 1, topk)
+    out, lse = ref.sparse_mla_fwd(q, kv, idx)
+    torch.testing.assert_close(out[0, 0], kv[0, :topk, 0, :512].mean(0).expand(H, 512), rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(lse, torch.full((1, 1, H), math.log(topk)), rtol=1e-6, atol=1e-6)
+
+
+def test_mla_permutation_invariance_and_lse():
+    q, kv, idx = _mla_inputs(S=3, topk=32)
+    out, lse = ref.sparse_mla_fwd(q, kv, idx)
+    perm = torch.randperm(32, generator=torch.Generator().manual_seed(9))
+    out2, lse2 = ref.sparse_mla_fwd(q, kv, idx[..., perm].contiguous())
+    torch.testing.assert_close(out, out2, rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(lse, lse2, rtol=1e-6, atol=1e-6)
+    # LSE against torch.logsumexp on the gathered scores of one row.
+    rows = idx[0, 1, 0].long()
+    sc = (q[0, 1].double() @ kv[0, rows, 0].double().T) / math.sqrt(576)
+    torch.testing.assert_close(lse[0, 1].double(), torch.logsumexp(sc, dim=1), rtol=1e-6, atol=1e-6)
+
+
+def test_mla_paged_equals_contiguous():
+    q, kv, idx = _mla_inputs(B=2, S=4, Skv=64, topk=16)
+    bs = 8
+    nblk = 64 // bs
+    perm = torch.randperm(2 * nblk, generator=torch.Generator().manual_seed(4))
+    pool = torch.empty(2 * nblk, bs, 1, 576)
+    table = perm.view(2, nblk).to(torch.int32)
+    for b in range(2):
+        for j in range(nblk):
+            pool[table[b, j]] = kv[b, j * bs:(j + 1) * bs]
+    o1, l1 = ref.sparse_mla_fwd(q, kv, idx)
+    o2, l2 = ref.sparse_mla_fwd(q, pool, idx, block_table=table)
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+
+
+def test_mla_causal_mask_drops_future_indices():
+    q, kv, _ = _mla_inputs(S=4, Skv=16, topk=4)
+    idx = torch.tensor([[[[0, 15, 3, -1]], [[1, 2, 14, 13]], [[5, 6, 7, 8]], [[15, 14, 0, 1]]]], dtype=torch.int32)
+    out, lse = ref.sparse_mla_fwd(q, kv, idx)
+    # Row s may use indices <= Skv - S + s = 12 + s.
+    kept = torch.tensor([[[[0, -1, 3, -1]], [[1, 2, -1, 13]], [[5, 6, 7, 8]], [[15, 14, 0, 1]]]], dtype=torch.int32)
+    out2, lse2 = ref.sparse_mla_fwd(q, kv, kept, is_causal=False)
+    assert torch.equal(out, out2) and torch.equal(lse, lse2)
+
+
+def test_mla_empty_row():
+    q, kv, _ = _mla_inputs(S=1)
+    idx = torch.full((1, 1, 1, 4), -1, dtype=torch.int32)
+    out, lse = ref.sparse_mla_fwd(q, kv, idx)
+    assert torch.all(out == 0) and torch.all(torch.isneginf(lse))
+
+
+def test_causal_sparse_indices_are_unique_and_in_range():
+    idx = ref.causal_sparse_indices(1, 64, 256, 128, seed=1)
+    for t in range(64):
+        row = idx[0, t, 0]
+        valid = row[row >= 0]
+        assert valid.numel() == min(128, 256 - 64 + t + 1)
+        assert torch.unique(valid).numel() == valid.numel()
+        assert int(valid.max()) <= 256 - 64 + t
+        assert torch.all(row[valid.numel():] == -1)

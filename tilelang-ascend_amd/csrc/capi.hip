@@ -1,0 +1,136 @@
+// C ABI entry points: argument validation, then the kernel launchers.
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/dsa_mi355x.h"
+#include "common.hpp"
+
+namespace dsa {
+hipError_t launch_topk(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k, const int32_t* row_len,
+                       int sorted, int32_t* out_idx, float* out_val, hipStream_t stream);
+hipError_t launch_indexer_logits(int kind, const void* q, const void* k, const float* k_scale, const float* w,
+                                 int64_t B, int64_t S1, int64_t S2, int64_t H, int64_t D, const int32_t* aq_len,
+                                 const int32_t* ak_len, const int32_t* block_table, int64_t block_size,
+                                 int64_t max_blocks, int sparse_mode, float* logits, int64_t ld, hipStream_t stream);
+hipError_t launch_sparse_mla(int is_fp16, const void* q, const void* kv, const int32_t* indices, const int32_t* block_table,
+                             const int32_t* q_len, const int32_t* kv_len, int64_t B, int64_t S, int64_t H,
+                             int64_t Skv, int64_t block_size, int64_t max_blocks, int64_t topk, float sm_scale,
+                             int causal, void* out, float* lse, void* workspace, hipStream_t stream);
+size_t mla_workspace_bytes(int64_t tokens, int64_t H, int64_t topk);
+}  // namespace dsa
+
+namespace {
+thread_local char g_msg[256] = "";
+
+int reject(const char* what) {
+  std::snprintf(g_msg, sizeof(g_msg), "%s", what);
+  return (int)hipErrorInvalidValue;
+}
+
+int ok(hipError_t e) {
+  if (e != hipSuccess) std::snprintf(g_msg, sizeof(g_msg), "launch failed: %s", hipGetErrorString(e));
+  return (int)e;
+}
+
+constexpr int64_t kMaxInt = 0x7fffffff;
+}  // namespace
+
+extern "C" {
+
+int dsa_abi_version(void) { return 100; }
+
+const char* dsa_last_error_message(void) { return g_msg; }
+
+int dsa_topk_select(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k, const int32_t* row_len,
+                    int sorted, int32_t* out_idx, float* out_val, void* stream) {
+  if (rows < 0 || n < 0 || rows > kMaxInt || n >= kMaxInt) return reject("topk: rows/n out of range");
+  if (k < 1 || k > 8192) return reject("topk: k must be in [1, 8192]");
+  if (ld < n) return reject("topk: ld < n");
+  if (rows > 0 && (!out_idx || (n > 0 && !x))) return reject("topk: null pointer");
+  return ok(dsa::launch_topk(x, ld, rows, n, k, row_len, sorted ? 1 : 0, out_idx, out_val,
+                             static_cast<hipStream_t>(stream)));
+}
+
+static int check_indexer(int kind, const void* q, const void* k, const float* weights, int64_t B, int64_t S1,
+                         int64_t S2, int64_t H, int64_t D, const int32_t* block_table, int64_t block_size,
+                         int64_t max_blocks, int sparse_mode) {
+  if (kind != DSA_KIND_FP8_E4M3 && kind != DSA_KIND_BF16 && kind != DSA_KIND_FP16) return reject("indexer: bad kind");
+  if (D != 128 && D != 64) return reject("indexer: head dim D must be 64 or 128");
+  if (H < 16 || H > 64 || H % 16 != 0) return reject("indexer: H must be 16, 32, 48 or 64");
+  if (B < 0 || S1 < 0 || S2 < 0 || B > 65535 || S1 > kMaxInt || S2 > kMaxInt) return reject("indexer: bad sizes");
+  if (sparse_mode != 0 && sparse_mode != 3) return reject("indexer: sparse_mode must be 0 or 3");
+  if (block_table && (block_size <= 0 || max_blocks <= 0 || block_size * max_blocks < S2))
+    return reject("indexer: paged key needs block_size > 0 and max_blocks * block_size >= S2");
+  if (B * S1 * S2 > 0 && (!q || !k || !weights)) return reject("indexer: null pointer");
+  return 0;
+}
+
+int dsa_indexer_logits(int kind, const void* q, const void* k, const float* k_scale, const float* weights,
+                       int64_t B, int64_t S1, int64_t S2, int64_t H, int64_t D, const int32_t* actual_q_len,
+                       const int32_t* actual_k_len, const int32_t* block_table, int64_t block_size,
+                       int64_t max_blocks, int sparse_mode, float* logits, int64_t ld, void* stream) {
+  int rc = check_indexer(kind, q, k, weights, B, S1, S2, H, D, block_table, block_size, max_blocks, sparse_mode);
+  if (rc) return rc;
+  if (ld < S2) return reject("indexer: ld < S2");
+  if (B * S1 * S2 > 0 && !logits) return reject("indexer: null logits");
+  return ok(dsa::launch_indexer_logits(kind, q, k, k_scale, weights, B, S1, S2, H, D, actual_q_len, actual_k_len,
+                                       block_table, block_size, max_blocks, sparse_mode, logits, ld,
+                                       static_cast<hipStream_t>(stream)));
+}
+
+size_t dsa_lightning_indexer_workspace_size(int64_t B, int64_t S1, int64_t S2) {
+  if (B <= 0 || S1 <= 0 || S2 <= 0) return 0;
+  const int64_t ld = (S2 + 3) & ~int64_t(3);
+  return (size_t)(B * S1 * ld) * sizeof(float);
+}
+
+int dsa_lightning_indexer(int kind, const void* q, const void* k, const float* k_scale, const float* weights,
+                          int64_t B, int64_t S1, int64_t S2, int64_t H, int64_t D, const int32_t* actual_q_len,
+                          const int32_t* actual_k_len, const int32_t* block_table, int64_t block_size,
+                          int64_t max_blocks, int sparse_mode, int64_t sparse_count, int32_t* out_idx,
+                          float* out_val, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_indexer(kind, q, k, weights, B, S1, S2, H, D, block_table, block_size, max_blocks, sparse_mode);
+  if (rc) return rc;
+  if (sparse_count < 1 || sparse_count > 8192) return reject("indexer: sparse_count must be in [1, 8192]");
+  if (workspace_bytes < dsa_lightning_indexer_workspace_size(B, S1, S2)) return reject("indexer: workspace too small");
+  if (B * S1 > 0 && !out_idx) return reject("indexer: null out_idx");
+  if (B * S1 == 0) return 0;
+  const int64_t ld = (S2 + 3) & ~int64_t(3);
+  float* logits = static_cast<float*>(workspace);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e = dsa::launch_indexer_logits(kind, q, k, k_scale, weights, B, S1, S2, H, D, actual_q_len, actual_k_len,
+                                            block_table, block_size, max_blocks, sparse_mode, logits, ld, st);
+  if (e != hipSuccess) return ok(e);
+  return ok(dsa::launch_topk(logits, ld, B * S1, S2, sparse_count, nullptr, 1, out_idx, out_val, st));
+}
+
+size_t dsa_sparse_mla_workspace_size(int64_t B, int64_t S, int64_t H, int64_t topk) {
+  if (B <= 0 || S <= 0 || H <= 0 || topk <= 0) return 0;
+  return dsa::mla_workspace_bytes(B * S, H, topk);
+}
+
+int dsa_sparse_mla_fwd(int kind, const void* q, const void* kv, const int32_t* indices,
+                       const int32_t* block_table, const int32_t* actual_q_len, const int32_t* actual_kv_len,
+                       int64_t B, int64_t S, int64_t H, int64_t d_qk, int64_t d_v, int64_t Skv, int64_t block_size,
+                       int64_t max_blocks, int64_t topk, float sm_scale, int is_causal, void* out, float* lse,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+  if (kind != DSA_KIND_BF16 && kind != DSA_KIND_FP16) return reject("sparse_mla: kind must be bf16 or fp16");
+  if (d_qk != 576 || d_v != 512) return reject("sparse_mla: d_qk must be 576 and d_v 512");
+  if (H < 16 || H % 16 != 0 || H > 1024) return reject("sparse_mla: H must be a multiple of 16 in [16, 1024]");
+  if (B < 0 || S < 0 || topk < 1 || B * S > kMaxInt || topk > kMaxInt) return reject("sparse_mla: bad sizes");
+  if (block_table) {
+    if (block_size <= 0 || max_blocks <= 0 || block_size * max_blocks > kMaxInt)
+      return reject("sparse_mla: paged kv needs block_size > 0 and max_blocks > 0");
+  } else if (Skv < 0 || Skv > kMaxInt) {
+    return reject("sparse_mla: bad Skv");
+  }
+  if (!(sm_scale == sm_scale)) return reject("sparse_mla: sm_scale is NaN");
+  if (workspace_bytes < dsa_sparse_mla_workspace_size(B, S, H, topk)) return reject("sparse_mla: workspace too small");
+  if (B * S > 0 && (!q || !kv || !indices || !out || !lse)) return reject("sparse_mla: null pointer");
+  const int64_t skv_eff = block_table ? block_size * max_blocks : Skv;
+  return ok(dsa::launch_sparse_mla(kind == DSA_KIND_FP16, q, kv, indices, block_table, actual_q_len, actual_kv_len, B, S, H, skv_eff,
+                                   block_size, max_blocks, topk, sm_scale, is_causal ? 1 : 0, out, lse, workspace,
+                                   static_cast<hipStream_t>(stream)));
+}
+
+}  // extern "C"

@@ -1,0 +1,347 @@
+// Lightning-indexer logits on gfx950 MFMA.
+//
+//   logits[b, t, s] = k_scale[b, s] * sum_h w[b, t, h] * ReLU(q[b, t, h, :] . k[b, s, :]),  D in {64, 128}
+//
+// (examples/deepseek_v4/lightning_indexer.py:291-316; example_lightning_indexer.py:137-142;
+// k_scale is the per-token scale of fp8 keys, 1 when absent.)  Masked positions
+// -- beyond the causal bound of sparse_mode 3 (lightning_indexer.py:308-314),
+// beyond actual_k_len, or on padded query rows -- are written as -inf, so the
+// logits feed the top-k selector directly.
+//
+// Work split.  A 256-thread workgroup (4 waves) owns kTok query tokens (kTokPW
+// per wave) and one chunk of keys.  q is stationary: every wave keeps its
+// tokens' [H, D] rows in VGPRs as MFMA A operands (16 heads per operand).  k
+// streams through a double-buffered LDS tile of 64 keys; each 16-key slice is
+// one MFMA B operand.  fp8 e4m3 inputs use one v_mfma_f32_16x16x128_f8f6f4 per
+// 16 heads x 16 keys (K = D = 128 in a single instruction); fp16/bf16 inputs use
+// D/32 16x16x32 MFMAs.  The K dimension is read with the same lane -> byte
+// mapping for A and B, so the dot products do not depend on the hardware's
+// internal K order.  Epilogue in registers: ReLU, multiply by w[t, h], sum the
+// lane's 4 head rows, then two cross-lane adds over the 4 row groups; after
+// four 16-key slices lane l holds key l of the 64-key tile, so each token's
+// logits go out as one coalesced 256-byte store.
+#include "common.hpp"
+
+namespace dsa {
+
+constexpr int kIdxThreads = 256;
+constexpr int kIdxWaves = kIdxThreads / kWave;
+constexpr int kIdxKeyTile = 64;
+
+enum ElemKind : int { kFp8 = 0, kBf16 = 1, kFp16 = 2 };
+
+// Row bytes and the bytes each lane feeds one 16-row MFMA operand: the 64
+// lanes split a key/query row into 4 K-slices (lane group g = lane / 16 takes
+// bytes [g * row / 4, (g + 1) * row / 4)).
+template <int kKind, int kD>
+struct IdxTraits {
+  static constexpr int kElem = kKind == kFp8 ? 1 : 2;
+  static constexpr int kRowBytes = kD * kElem;
+  static constexpr int kLaneBytes = kRowBytes / 4;
+};
+
+// LDS row pitch: 16 bytes of padding per key row spreads the 16 rows one
+// MFMA operand reads over different banks.
+template <int kKind, int kD>
+constexpr int lds_pitch() { return IdxTraits<kKind, kD>::kRowBytes + 16; }
+
+template <int kKind, int kD>
+struct Operand {
+  static constexpr int kWords = IdxTraits<kKind, kD>::kLaneBytes / 4;
+  uint32_t w[kWords];
+};
+
+template <int kKind, int kD>
+__device__ __forceinline__ void load_operand_global(Operand<kKind, kD>& op, const uint8_t* p, bool valid) {
+  constexpr int n16 = IdxTraits<kKind, kD>::kLaneBytes / 16;
+#pragma unroll
+  for (int c = 0; c < n16; ++c) {
+    u32x4 v = valid ? *reinterpret_cast<const u32x4*>(p + 16 * c) : u32x4{0, 0, 0, 0};
+    op.w[4 * c + 0] = v.x; op.w[4 * c + 1] = v.y; op.w[4 * c + 2] = v.z; op.w[4 * c + 3] = v.w;
+  }
+}
+
+template <int kKind, int kD>
+__device__ __forceinline__ void load_operand_lds(Operand<kKind, kD>& op, const uint8_t* p) {
+  constexpr int n16 = IdxTraits<kKind, kD>::kLaneBytes / 16;
+#pragma unroll
+  for (int c = 0; c < n16; ++c) {
+    u32x4 v = *reinterpret_cast<const u32x4*>(p + 16 * c);
+    op.w[4 * c + 0] = v.x; op.w[4 * c + 1] = v.y; op.w[4 * c + 2] = v.z; op.w[4 * c + 3] = v.w;
+  }
+}
+
+template <int kKind, int kD>
+__device__ __forceinline__ f32x4 mfma_qk(const Operand<kKind, kD>& a, const Operand<kKind, kD>& b) {
+  constexpr int kW = Operand<kKind, kD>::kWords;
+  f32x4 c = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (kKind == kFp8) {
+    // One 16x16x128 fp8 MFMA; a D = 64 row leaves half of each lane's K-slice zero.
+    i32x8 av, bv;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      av[i] = i < kW ? (int)a.w[i] : 0;
+      bv[i] = i < kW ? (int)b.w[i] : 0;
+    }
+    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 0, 0, 0, 0, 0, 0);
+  } else {
+#pragma unroll
+    for (int s = 0; s < kW / 4; ++s) {
+      u32x4 au = {a.w[4 * s], a.w[4 * s + 1], a.w[4 * s + 2], a.w[4 * s + 3]};
+      u32x4 bu = {b.w[4 * s], b.w[4 * s + 1], b.w[4 * s + 2], b.w[4 * s + 3]};
+      if constexpr (kKind == kBf16) {
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, au), __builtin_bit_cast(bf16x8, bu), c, 0, 0, 0);
+      } else {
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, au), __builtin_bit_cast(f16x8, bu), c, 0, 0, 0);
+      }
+    }
+  }
+  return c;
+}
+
+struct IdxArgs {
+  const uint8_t* q;        // [B, S1, H, 128]
+  const uint8_t* k;        // [B, S2, 128] or paged [blocks, block_size, 128]
+  const float* k_scale;    // [B, S2] or paged [blocks, block_size]; nullable
+  const float* w;          // [B, S1, H] fp32
+  const int32_t* aq_len;   // [B] nullable
+  const int32_t* ak_len;   // [B] nullable
+  const int32_t* block_table;  // [B, max_blocks] nullable (non-paged)
+  float* logits;           // [B, S1, ld]
+  int64_t ld;
+  int S1, S2, H;
+  int block_size, max_blocks;
+  int sparse_mode;
+  int key_chunk;
+};
+
+template <int kKind, int kD, int kTokPW>
+__global__ __launch_bounds__(kIdxThreads) void indexer_logits_kernel(IdxArgs a) {
+  constexpr int kRB = IdxTraits<kKind, kD>::kRowBytes;
+  constexpr int kLB = IdxTraits<kKind, kD>::kLaneBytes;
+  constexpr int kPitch = lds_pitch<kKind, kD>();
+  constexpr int kTok = kTokPW * kIdxWaves;
+  constexpr int kTileBytes = kIdxKeyTile * kRB;
+  constexpr int kLoads = kTileBytes / 16 / kIdxThreads;  // 16-byte loads per thread per tile
+  static_assert(kLoads >= 1, "tile too small");
+  __shared__ __align__(16) uint8_t ktile[2][kIdxKeyTile * kPitch];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int r = lane & 15;   // MFMA operand row / output column
+  const int g = lane >> 4;   // K-slice of the operand, output row group
+  const int b = blockIdx.z;
+  const int t_base = blockIdx.y * kTok;
+  const int key0 = blockIdx.x * a.key_chunk;
+  const int key1 = min(a.S2, key0 + a.key_chunk);
+  const int aq = a.aq_len ? a.aq_len[b] : a.S1;
+  const int ak = a.ak_len ? a.ak_len[b] : a.S2;
+  const int nhb = a.H >> 4;
+
+  // Valid key count per token of this wave (0 for padded rows).
+  int nvalid[kTokPW];
+  int max_valid = 0;
+#pragma unroll
+  for (int j = 0; j < kTokPW; ++j) {
+    const int t = t_base + wave * kTokPW + j;
+    int nv = 0;
+    if (t < aq && t < a.S1 && ak > 0) {
+      if (a.sparse_mode == 3) {
+        const int cl = ak - aq + t + 1;
+        nv = cl > 0 ? cl : ak;
+      } else {
+        nv = ak;
+      }
+      nv = min(nv, ak);
+    }
+    nvalid[j] = nv;
+  }
+  // Workgroup-wide bound for skipping whole key tiles.
+  {
+    const int tl = min(t_base + kTok, min(aq, a.S1)) - 1;  // last real token
+    if (tl >= t_base && ak > 0) {
+      if (a.sparse_mode == 3) {
+        const int cl = ak - aq + tl + 1;
+        max_valid = min(cl > 0 ? cl : ak, ak);
+      } else {
+        max_valid = ak;
+      }
+    }
+  }
+
+  // Stationary q operands and head weights.
+  Operand<kKind, kD> qa[kTokPW][4];
+  f32x4 wv[kTokPW][4];
+#pragma unroll
+  for (int j = 0; j < kTokPW; ++j) {
+    const int t = t_base + wave * kTokPW + j;
+    const bool tv = t < a.S1;
+    const int64_t trow = (int64_t)b * a.S1 + (tv ? t : 0);
+#pragma unroll
+    for (int hb = 0; hb < 4; ++hb) {
+      const bool hv = tv && hb < nhb;
+      const uint8_t* p = a.q + (trow * a.H + hb * 16 + r) * kRB + g * kLB;
+      load_operand_global<kKind, kD>(qa[j][hb], p, hv);
+      wv[j][hb] = hv ? *reinterpret_cast<const f32x4*>(a.w + trow * a.H + hb * 16 + 4 * g) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+
+  const int tile_end = min(key1, max_valid);  // keys at or past this are -inf for every token
+  const int ntiles = tile_end > key0 ? (tile_end - key0 + kIdxKeyTile - 1) / kIdxKeyTile : 0;
+
+  // Global -> register staging for one key tile.
+  u32x4 stage[kLoads];
+  auto fetch = [&](int tile) {
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int e = tid + i * kIdxThreads;      // 16-byte element of the tile
+      const int kr = e / (kRB / 16);            // key row in tile
+      const int kc = e % (kRB / 16);            // 16-byte column
+      const int s = key0 + tile * kIdxKeyTile + kr;
+      u32x4 v = {0, 0, 0, 0};
+      if (s < tile_end) {
+        int64_t rowi;
+        if (a.block_table) {
+          const int blk = a.block_table[(int64_t)b * a.max_blocks + s / a.block_size];
+          rowi = (int64_t)blk * a.block_size + s % a.block_size;
+        } else {
+          rowi = (int64_t)b * a.S2 + s;
+        }
+        v = *reinterpret_cast<const u32x4*>(a.k + rowi * kRB + kc * 16);
+      }
+      stage[i] = v;
+    }
+  };
+  auto commit = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int e = tid + i * kIdxThreads;
+      const int kr = e / (kRB / 16);
+      const int kc = e % (kRB / 16);
+      *reinterpret_cast<u32x4*>(&ktile[buf][kr * kPitch + kc * 16]) = stage[i];
+    }
+  };
+
+  if (ntiles > 0) {
+    fetch(0);
+    commit(0);
+  }
+  __syncthreads();
+
+  for (int tile = 0; tile < ntiles; ++tile) {
+    const int buf = tile & 1;
+    if (tile + 1 < ntiles) fetch(tile + 1);
+
+    float res[kTokPW];
+#pragma unroll
+    for (int j = 0; j < kTokPW; ++j) res[j] = 0.f;
+#pragma unroll
+    for (int sub = 0; sub < kIdxKeyTile / 16; ++sub) {
+      Operand<kKind, kD> kb;
+      load_operand_lds<kKind, kD>(kb, &ktile[buf][(sub * 16 + r) * kPitch + g * kLB]);
+#pragma unroll
+      for (int j = 0; j < kTokPW; ++j) {
+        float acc = 0.f;
+#pragma unroll
+        for (int hb = 0; hb < 4; ++hb) {
+          if (hb < nhb) {
+            const f32x4 c = mfma_qk<kKind, kD>(qa[j][hb], kb);
+            acc = fmaf(wv[j][hb].x, fmaxf(c.x, 0.f), acc);
+            acc = fmaf(wv[j][hb].y, fmaxf(c.y, 0.f), acc);
+            acc = fmaf(wv[j][hb].z, fmaxf(c.z, 0.f), acc);
+            acc = fmaf(wv[j][hb].w, fmaxf(c.w, 0.f), acc);
+          }
+        }
+        acc += __shfl_xor(acc, 16, kWave);
+        acc += __shfl_xor(acc, 32, kWave);
+        res[j] = (g == sub) ? acc : res[j];
+      }
+    }
+    // Lane l now holds key (tile*64 + l) for each token.
+    const int s = key0 + tile * kIdxKeyTile + lane;
+    float sc = 1.f;
+    if (a.k_scale && s < tile_end) {
+      if (a.block_table) {
+        const int blk = a.block_table[(int64_t)b * a.max_blocks + s / a.block_size];
+        sc = a.k_scale[(int64_t)blk * a.block_size + s % a.block_size];
+      } else {
+        sc = a.k_scale[(int64_t)b * a.S2 + s];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kTokPW; ++j) {
+      const int t = t_base + wave * kTokPW + j;
+      if (t < a.S1 && s < key1) {
+        const float v = (s < nvalid[j]) ? res[j] * sc : -__builtin_huge_valf();
+        __builtin_nontemporal_store(v, &a.logits[((int64_t)b * a.S1 + t) * a.ld + s]);
+      }
+    }
+    if (tile + 1 < ntiles) {
+      __syncthreads();
+      commit(buf ^ 1);
+      __syncthreads();
+    }
+  }
+
+  // Keys of this chunk past every token's bound: -inf.
+  const int masked0 = key0 + ntiles * kIdxKeyTile;
+#pragma unroll
+  for (int j = 0; j < kTokPW; ++j) {
+    const int t = t_base + wave * kTokPW + j;
+    if (t < a.S1) {
+      float* row = a.logits + ((int64_t)b * a.S1 + t) * a.ld;
+      for (int s = masked0 + lane; s < key1; s += kWave) __builtin_nontemporal_store(-__builtin_huge_valf(), &row[s]);
+    }
+  }
+}
+
+template <int kKind, int kD>
+static hipError_t launch_indexer_kind(const IdxArgs& a, int B, hipStream_t stream) {
+  constexpr int kTokPW = 2;
+  constexpr int kTok = kTokPW * kIdxWaves;
+  const dim3 grid((unsigned)((a.S2 + a.key_chunk - 1) / a.key_chunk), (unsigned)((a.S1 + kTok - 1) / kTok), (unsigned)B);
+  hipLaunchKernelGGL((indexer_logits_kernel<kKind, kD, kTokPW>), grid, dim3(kIdxThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+// kind: 0 fp8 e4m3fn, 1 bf16, 2 fp16.  Caller validated: D in {64, 128}, H % 16 == 0, H <= 64.
+hipError_t launch_indexer_logits(int kind, const void* q, const void* k, const float* k_scale, const float* w,
+                                 int64_t B, int64_t S1, int64_t S2, int64_t H, int64_t D,
+                                 const int32_t* aq_len, const int32_t* ak_len,
+                                 const int32_t* block_table, int64_t block_size, int64_t max_blocks,
+                                 int sparse_mode, float* logits, int64_t ld, hipStream_t stream) {
+  if (B == 0 || S1 == 0 || S2 == 0) return hipSuccess;
+  IdxArgs a;
+  a.q = static_cast<const uint8_t*>(q);
+  a.k = static_cast<const uint8_t*>(k);
+  a.k_scale = k_scale;
+  a.w = w;
+  a.aq_len = aq_len;
+  a.ak_len = ak_len;
+  a.block_table = block_table;
+  a.logits = logits;
+  a.ld = ld;
+  a.S1 = (int)S1;
+  a.S2 = (int)S2;
+  a.H = (int)H;
+  a.block_size = (int)block_size;
+  a.max_blocks = (int)max_blocks;
+  a.sparse_mode = sparse_mode;
+  // Enough workgroups to fill 256 CUs several times over.
+  const int64_t tok_groups = B * ((S1 + 7) / 8);
+  int64_t chunks = (2048 + tok_groups - 1) / tok_groups;
+  int64_t chunk = (S2 + chunks - 1) / chunks;
+  chunk = ((chunk + kIdxKeyTile - 1) / kIdxKeyTile) * kIdxKeyTile;
+  if (chunk < 1024) chunk = 1024;
+  a.key_chunk = (int)chunk;
+  const bool d128 = (D == 128);
+  switch (kind) {
+    case kFp8: return d128 ? launch_indexer_kind<kFp8, 128>(a, (int)B, stream) : launch_indexer_kind<kFp8, 64>(a, (int)B, stream);
+    case kBf16: return d128 ? launch_indexer_kind<kBf16, 128>(a, (int)B, stream) : launch_indexer_kind<kBf16, 64>(a, (int)B, stream);
+    case kFp16: return d128 ? launch_indexer_kind<kFp16, 128>(a, (int)B, stream) : launch_indexer_kind<kFp16, 64>(a, (int)B, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace dsa

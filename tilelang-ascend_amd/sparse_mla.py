@@ -1,0 +1,142 @@
+"""Sparse MLA forward on gfx950: gathered latent-KV attention with LSE.
+
+``sparse_mla_fwd(q, kv, indices, sm_scale)`` returns ``(out, lse)``:
+
+* q       [B, S, H, 576] bf16/fp16 (512 latent + 64 rope dims)
+* kv      [B, Skv, 1, 576] (one shared latent head), or a paged pool
+          [num_blocks, block_size, 1, 576] with ``block_table`` [B, max_blocks]
+* indices [B, S, 1, topk] int32 (or [B, S, topk]), -1 = empty slot
+* out     [B, S, H, 512] (V = kv[..., :512]), lse [B, S, H] fp32, natural log
+
+Semantics follow examples/sparse_flash_attention/example_sparse_flash_attn.py:18-292
+(sm_scale default 1/sqrt(576), causal) and the paged variant
+example_sparse_flash_attn_mask_pa.py:13-333 (``actual_seq_lengths``, block table,
+``-1`` slots); the LSE convention is the V4 golden's
+(examples/deepseek_v4/sparse_flash_mla/sparse_flash_mla_golden.py:149).  The
+builder ``sparse_attention_fwd(heads, dim, tail_dim, topk, ...)`` keeps the
+reference's builder signature (example_sparse_flash_attn.py:19-29) and returns a
+callable that yields ``out`` only, as the reference kernel does.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+D_QK = 576
+D_V = 512
+
+_KINDS = {torch.bfloat16: _lib.KIND_BF16, torch.float16: _lib.KIND_FP16}
+
+
+def _lens(x: Optional[torch.Tensor], B: int, dev) -> Optional[torch.Tensor]:
+    if x is None:
+        return None
+    t = torch.as_tensor(x).to(device=dev, dtype=torch.int32).reshape(-1).contiguous()
+    if t.numel() != B:
+        raise ValueError(f"actual sequence lengths must have B={B} entries, got {t.numel()}")
+    return t
+
+
+def sparse_mla_fwd(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tensor, sm_scale: Optional[float] = None, *,
+                   block_table: Optional[torch.Tensor] = None,
+                   actual_seq_lengths_query: Optional[torch.Tensor] = None,
+                   actual_seq_lengths_kv: Optional[torch.Tensor] = None,
+                   is_causal: bool = True) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Sparse MLA forward; returns ``(out [B, S, H, 512], lse [B, S, H] fp32)``."""
+    if q.dtype not in _KINDS:
+        raise ValueError(f"q must be bfloat16 or float16, got {q.dtype}")
+    if kv.dtype != q.dtype:
+        raise ValueError(f"kv dtype {kv.dtype} must equal q dtype {q.dtype}")
+    if indices.dtype != torch.int32:
+        raise ValueError(f"indices must be int32, got {indices.dtype}")
+    dev = _lib.require_device(q, kv, indices, block_table)
+    if q.dim() != 4 or q.shape[-1] != D_QK:
+        raise ValueError(f"q must be [B, S, H, {D_QK}], got {tuple(q.shape)}")
+    B, S, H, _ = q.shape
+    if H % 16 != 0 or H > 1024:
+        raise ValueError(f"heads must be a multiple of 16 (<= 1024), got {H}")
+    if kv.dim() != 4 or kv.shape[2] != 1 or kv.shape[3] != D_QK:
+        raise ValueError(f"kv must be [*, *, 1, {D_QK}] (one shared latent head), got {tuple(kv.shape)}")
+    if indices.dim() == 4:
+        if indices.shape[2] != 1:
+            raise ValueError("indices must have kv_group = 1")
+        idx = indices.reshape(B, S, indices.shape[3])
+    elif indices.dim() == 3:
+        idx = indices
+    else:
+        raise ValueError(f"indices must be [B, S, 1, topk] or [B, S, topk], got {tuple(indices.shape)}")
+    if tuple(idx.shape[:2]) != (B, S):
+        raise ValueError(f"indices batch/seq dims {tuple(idx.shape[:2])} do not match q {(B, S)}")
+    topk = idx.shape[2]
+    for name, t in (("q", q), ("kv", kv), ("indices", idx)):
+        _lib.require_contiguous(name, t)
+    if block_table is not None:
+        bt = block_table.to(torch.int32).contiguous()
+        if bt.dim() != 2 or bt.shape[0] != B:
+            raise ValueError(f"block_table must be [B, max_blocks], got {tuple(bt.shape)}")
+        block_size, max_blocks = kv.shape[1], bt.shape[1]
+        skv = max_blocks * block_size
+    else:
+        bt = None
+        if kv.shape[0] != B:
+            raise ValueError(f"kv batch {kv.shape[0]} does not match q batch {B}")
+        block_size, max_blocks = 0, 0
+        skv = kv.shape[1]
+    if sm_scale is None:
+        sm_scale = D_QK ** -0.5
+    ql = _lens(actual_seq_lengths_query, B, dev)
+    kl = _lens(actual_seq_lengths_kv, B, dev)
+    # The kernel trusts these bounds for its address arithmetic: check them here.
+    if kl is not None and B > 0 and (int(kl.max().item()) > skv or int(kl.min().item()) < 0):
+        raise ValueError(f"actual_seq_lengths_kv must lie in [0, {skv}]")
+    if ql is not None and B > 0 and (int(ql.max().item()) > S or int(ql.min().item()) < 0):
+        raise ValueError(f"actual_seq_lengths_query must lie in [0, {S}]")
+    out = torch.empty((B, S, H, D_V), dtype=q.dtype, device=dev)
+    lse = torch.empty((B, S, H), dtype=torch.float32, device=dev)
+    lib = _lib.load_library()
+    ws_bytes = lib.dsa_sparse_mla_workspace_size(B, S, H, topk)
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    rc = lib.dsa_sparse_mla_fwd(_KINDS[q.dtype], _lib.ptr(q), _lib.ptr(kv), _lib.ptr(idx), _lib.ptr(bt),
+                                _lib.ptr(ql), _lib.ptr(kl), B, S, H, D_QK, D_V, skv, block_size, max_blocks, topk,
+                                float(sm_scale), 1 if is_causal else 0, _lib.ptr(out), _lib.ptr(lse), _lib.ptr(ws),
+                                ws_bytes, _lib.stream_handle(dev))
+    _lib.check(rc, "dsa_sparse_mla_fwd")
+    return out, lse
+
+
+def sparse_attention_fwd(heads: int, dim: int, tail_dim: int, topk: int, kv_stride: int = 1, kv_group: int = 1,
+                         sm_scale: Optional[float] = None, is_causal: bool = True, block_I: int = 64, **_tuning):
+    """Builder with the signature of example_sparse_flash_attn.py:19-29; returns ``kernel(q, kv, indices) -> out``.
+
+    The paged form ``kernel(q, kv, indices, actual_q_len, actual_kv_len, block_table)``
+    (example_sparse_flash_attn_mask_pa.py:440) is accepted too; paged indices may
+    omit the batch dimension ([S, 1, topk]) as in that example (batch 1).
+    """
+    if dim + tail_dim != D_QK or dim != D_V:
+        raise ValueError(f"dim + tail_dim must be {D_V} + {D_QK - D_V}, got {dim} + {tail_dim}")
+    if kv_stride != 1:
+        raise ValueError("kv_stride must be 1")
+    if kv_group != 1:
+        raise ValueError("kv_group must be 1 (one shared latent head)")
+    if not is_causal:
+        raise ValueError("non-causal is not supported")  # example_sparse_flash_attn.py:32
+    if topk % block_I != 0:
+        raise ValueError("topk must be a multiple of block_I")  # example_sparse_flash_attn.py:33
+
+    def kernel(q, kv, indices, actual_q_len=None, actual_kv_len=None, block_table=None):
+        if q.shape[2] != heads:
+            raise ValueError(f"q has {q.shape[2]} heads, builder expects {heads}")
+        idx = indices
+        if block_table is not None and idx.dim() == 3:
+            idx = idx.unsqueeze(0)
+        if idx.shape[-1] != topk:
+            raise ValueError(f"indices last dim {idx.shape[-1]} != topk {topk}")
+        out, _ = sparse_mla_fwd(q, kv, idx, sm_scale, block_table=block_table,
+                                actual_seq_lengths_query=actual_q_len, actual_seq_lengths_kv=actual_kv_len,
+                                is_causal=True)
+        return out
+
+    return kernel
