@@ -127,44 +127,10 @@ def cpu_baseline_prefill(torch, q, kv, idx, budget_s=12.0):
                       f"of the step workload, {el:.1f} s"}
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--reps", type=int, default=20, help="repetitions of the secondary (flushed) benchmarks")
-    ap.add_argument("--skip", default="", help="comma list of parts to skip: indexer,decode,cpu")
-    ap.add_argument("--copy-calibration", action="store_true",
-                    help="only run a 1 GiB device-to-device copy (HBM byte-counter calibration for rocprof)")
-    args = ap.parse_args()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
-              file=sys.stderr)
-        sys.exit(2)
-    skip = set(filter(None, args.skip.split(",")))
-
-    import torch
-    import __graft_entry__
-
-    pkg = __graft_entry__.load_package()
-    pkg.load_library()
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-
-    if args.copy_calibration:
-        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_calibration_bytes_each_way": src.numel() * 4, "reps": 5}), flush=True)
-        return
-
-    # ---------------- step workload: sparse MLA prefill (C4) ----------------
-    S, H, topk = 16384, 128, 2048
+def run_step(torch, pkg, dev, args, S, H, topk, sm_scale):
+    """C4 sparse MLA prefill: the timed step.  Returns (result dict, inputs for the CPU baseline)."""
     _log("generating C4 prefill inputs")
     q, kv, idx = gen_prefill(torch, dev, S=S, H=H, topk=topk)
-    sm_scale = 576 ** -0.5
     fn = lambda: pkg.sparse_mla_fwd(q, kv, idx, sm_scale)  # noqa: E731
     for _ in range(args.warmup):
         fn()
@@ -195,14 +161,57 @@ def main():
                    "d_qk": 576, "d_v": 512, "topk": topk, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                     "kernel": "sparse_mla_kernel<8,false>", "flops_per_launch": flops},
+                     "kernel": "sparse_mla_kernel<4,false>", "flops_per_launch": flops},
         "wall_s_timed_region": round(wall, 4),
         "step_ms_p10_p90": [round(sorted(step_ms)[len(step_ms) // 10], 4),
                             round(sorted(step_ms)[(len(step_ms) * 9) // 10], 4)],
     }
-    cpu_inputs = (q, kv, idx)
+    return result, (q, kv, idx)
 
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--reps", type=int, default=20, help="repetitions of the secondary (flushed) benchmarks")
+    ap.add_argument("--skip", default="", help="comma list of parts to skip: step,indexer,decode,cpu")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 1 GiB device-to-device copy (HBM byte-counter calibration for rocprof)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+    skip = set(filter(None, args.skip.split(",")))
+
+    import torch
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    pkg.load_library()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    if args.copy_calibration:
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_each_way": src.numel() * 4, "reps": 5}), flush=True)
+        return
+
+    # ---------------- step workload: sparse MLA prefill (C4) ----------------
+    S, H, topk = 16384, 128, 2048
+    sm_scale = 576 ** -0.5
+    result = {}
+    cpu_inputs = None
+    if "step" not in skip:
+        result, cpu_inputs = run_step(torch, pkg, dev, args, S, H, topk, sm_scale)
     flush = _flush_buffer(torch, dev)
+
 
     # ---------------- indexer + top-k (C2) ----------------
     if "indexer" not in skip:
@@ -282,7 +291,7 @@ def main():
         del qd, pool, table, idd
 
     del flush
-    if "cpu" not in skip:
+    if "cpu" not in skip and cpu_inputs is not None:
         _log("CPU baseline (oracle, bounded sample)")
         result["cpu_baseline"] = cpu_baseline_prefill(torch, *cpu_inputs)
     else:

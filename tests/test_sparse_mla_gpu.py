@@ -32,7 +32,7 @@ def test_config1_parity(dsa, dev):
     _check(out, lse, *ref.sparse_mla_fwd(q, kv, idx))
 
 
-@pytest.mark.parametrize("H", [32, 64, 128, 256])
+@pytest.mark.parametrize("H", [32, 48, 64, 128, 160, 256])
 def test_head_counts(dsa, dev, H):
     q, kv, idx = _inputs(1, 4, 2048, H, 256, seed=H)
     out, lse = dsa.sparse_mla_fwd(q.to(dev), kv.to(dev), idx.to(dev))
@@ -106,3 +106,32 @@ def test_builder_signature(dsa, dev):
     out = kern(q.to(dev), kv.to(dev), idx.to(dev))
     ro, _ = ref.sparse_mla_fwd(q, kv, idx)
     torch.testing.assert_close(out.float().cpu(), ro, atol=2e-2, rtol=2e-2)
+
+
+def _ramp_inputs(jump_log2, H=128, S=2, topk=256, Skv=1024, seed=12):
+    """Scores of later index slots exceed the first tile's by ~jump_log2 (base 2)."""
+    g = torch.Generator().manual_seed(seed)
+    q = torch.zeros(1, S, H, 576)
+    q[..., :64] = 1.0
+    q += torch.randn(1, S, H, 576, generator=g) * 0.01
+    kv = torch.randn(1, Skv, 1, 576, generator=g) * 0.5
+    # t = sm_scale * log2(e) * q.k ~= 64 * c / 24 * 1.4427 for a row with c in its first 64 dims
+    c = jump_log2 / (64 / 24 * 1.4426950408889634)
+    kv[0, 512:, 0, :64] = c
+    idx = torch.empty(1, S, 1, topk, dtype=torch.int32)
+    for s in range(S):
+        low = torch.randperm(512, generator=g)[:topk // 2]
+        high = 512 + torch.randperm(Skv - 512 - S, generator=g)[:topk // 2]
+        idx[0, s, 0] = torch.cat([low, high]).to(torch.int32)  # first tiles all low
+    return q.to(torch.bfloat16), kv.to(torch.bfloat16), idx
+
+
+@pytest.mark.parametrize("jump", [40.0, 200.0])  # within the fast path's headroom / beyond it (exact fallback)
+@pytest.mark.parametrize("S", [1, 300])          # split index list (+combine) / one workgroup per row
+def test_large_score_jumps(dsa, dev, jump, S):
+    q, kv, idx = _ramp_inputs(jump, S=S)
+    out, lse = dsa.sparse_mla_fwd(q.to(dev), kv.to(dev), idx.to(dev))
+    ro, rl = ref.sparse_mla_fwd(q, kv, idx)
+    assert torch.isfinite(out.float()).all() and torch.isfinite(lse).all()
+    torch.testing.assert_close(out.float().cpu(), ro, atol=2e-2, rtol=2e-2)
+    torch.testing.assert_close(lse.cpu(), rl, atol=1e-3, rtol=1e-3)

@@ -101,3 +101,18 @@ def test_builder_signature(dsa, dev):
     kern = dsa.simple_topk_selector(4, 2048, 512, 128)
     got = kern(x.to(dev)).cpu()
     assert torch.equal(got, ref.topk_stable(x, 512)[0])
+
+
+def test_mixed_fast_and_exact_rows(dsa, dev):
+    # Rows the register fast path cannot bound (constant rows, few distinct values,
+    # a huge outlier) go to the exact radix pass; the others must be left untouched.
+    g = torch.Generator().manual_seed(10)
+    x = torch.randn(12, 30000, generator=g)
+    x[1] = 0.5
+    x[4] = torch.randint(0, 3, (30000,), generator=g).float()
+    x[7, 123] = 3.0e38
+    x[7, 5000] = -3.0e38
+    x[10, :] = float("-inf")
+    x[10, 17] = 1.0
+    _check(dsa, dev, x, 2048)
+    _check(dsa, dev, x, 100, sorted=False)

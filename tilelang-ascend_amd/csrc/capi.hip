@@ -124,7 +124,7 @@ int dsa_sparse_mla_fwd(int kind, const void* q, const void* kv, const int32_t* i
   } else if (Skv < 0 || Skv > kMaxInt) {
     return reject("sparse_mla: bad Skv");
   }
-  if (!(sm_scale == sm_scale)) return reject("sparse_mla: sm_scale is NaN");
+  if (!(sm_scale > 0.f) || !(sm_scale < 3.0e38f)) return reject("sparse_mla: sm_scale must be positive and finite");
   if (workspace_bytes < dsa_sparse_mla_workspace_size(B, S, H, topk)) return reject("sparse_mla: workspace too small");
   if (B * S > 0 && (!q || !kv || !indices || !out || !lse)) return reject("sparse_mla: null pointer");
   const int64_t skv_eff = block_table ? block_size * max_blocks : Skv;

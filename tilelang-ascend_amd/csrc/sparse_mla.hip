@@ -13,18 +13,29 @@
 // examples/deepseek_v4/sparse_flash_mla/sparse_flash_mla_golden.py:149.
 //
 // Work split.  One workgroup per (query row, split of the index list, group
-// of up to 128 heads); a wave owns 16 heads.  Per 32-slot tile the workgroup
-// gathers the selected KV rows from HBM with 16-byte loads into LDS twice: a
-// row-major copy (the A operand of S^T = K Q^T, K = 576 over 18 MFMAs
-// 16x16x32 bf16) and a column-major copy of the first 512 dims (the B operand
-// of O += P V).  Q stays in VGPRs for the whole row.  Because S^T puts the
-// keys on the MFMA M axis, each lane's 8 softmax probabilities are exactly the
-// 8 K-values its lane must feed the PV MFMA, so P goes to bf16 and into the
-// MFMA with no cross-lane shuffle.  Online softmax in base 2 (scale folded
-// with log2 e), fp32 row max / row sum, P rounded to bf16 only as the MFMA
-// operand (as the V4 golden does, sparse_flash_mla_golden.py:143).  The two
-// LDS buffers alternate so the next tile's gather (staged in VGPRs) overlaps
-// this tile's MFMAs.  With more than one split the workgroup writes a
+// of up to 128 heads); a wave owns 32 heads (two 16-head MFMA blocks that share
+// every K and V operand read from LDS) and keeps their Q rows in registers, the
+// O accumulators (32 x 512 fp32) in AGPRs: one wave per SIMD.
+//
+// Gather.  The workgroup first turns its slots into physical KV row numbers
+// (index -> validity -> block table) in LDS, once.  Tiles of 32 slots then
+// stream HBM -> LDS with global_load_lds_dwordx4 (no VGPR staging) through a
+// 4-stage ring, three tiles ahead of the MFMAs; each wave waits on its own
+// vmcnt, then a barrier publishes the tile.  A tile is chunk-major: the
+// 16-byte chunk c of all 32 slots is contiguous (slot index XOR-swizzled by
+// 4*(c & 1)), so a lane always serves the same slot, and both the 16-slot MFMA
+// operand reads and the transposed V reads are bank-conflict free.  Empty /
+// masked slots re-load a valid row of the same workgroup and get probability 0.
+//
+// Math per tile and wave: S^T = K Q^T with the 32 keys on the MFMA M axis
+// (18 x 2 v_mfma_f32_16x16x32_bf16 over d = 576), so each lane ends up with 8
+// scores of one head; softmax in base 2 against a reference max fixed by the
+// first valid tile (plus a bias: 2^60 for bf16), so O is never rescaled in the loop (a
+// score beyond the representable headroom sends the workgroup to an exact
+// two-pass fallback); P to bf16 is the
+// lane's own A operand of O += P V, and V comes straight from the row-major
+// tile through ds_read_b64_tr_b16 (4x4 transposes across lane quads), two
+// reads per 16 output columns.  With more than one split a workgroup writes a
 // normalised bf16 partial and its LSE; a combine kernel merges them.
 #include "common.hpp"
 
@@ -32,24 +43,34 @@ namespace dsa {
 
 constexpr int kMlaD = 576;
 constexpr int kMlaDV = 512;
-constexpr int kMlaTile = 32;
-constexpr int kKPitch = kMlaD * 2 + 16;       // bytes per key row, row-major copy
-constexpr int kVtPitch = kMlaTile * 2 + 8;    // bytes per value column, column-major copy
-constexpr int kKBytes = kMlaTile * kKPitch;   // 37376
-constexpr int kVtBytes = kMlaDV * kVtPitch;   // 36864
-constexpr int kBufBytes = kKBytes + kVtBytes + kMlaTile * 4;
-constexpr int kMlaLds = 2 * kBufBytes;        // 148736 bytes
+constexpr int kMlaTile = 32;                       // slots per tile
+constexpr int kRowBytes = kMlaD * 2;               // 1152
+constexpr int kRowChunks = kRowBytes / 16;         // 72
+constexpr int kStages = 4;
+constexpr int kAhead = kStages - 1;                // tiles in flight ahead of compute
+constexpr int kStageBytes = kMlaTile * kRowBytes;  // 36864
+constexpr int kTileInstr = kStageBytes / 1024;     // 36 wave-wide 16-byte DMA loads per tile
+constexpr int kSlotsCap = 2048;                    // slots per workgroup (physical rows kept in LDS)
+constexpr int kRowsOffset = kStages * kStageBytes; // 147456
+constexpr int kMlaLds = kRowsOffset + kSlotsCap * 4 + 16;  // rows + overflow flag + first valid slot
+// Reference max = first valid tile's max + kRefBias (log2); the fast path accepts
+// P up to 2^kOverflowGuard.  bf16 shares fp32's exponent range; fp16 P must stay
+// within [2^-14, 65504].
+template <bool kF16> struct PRange;
+template <> struct PRange<false> { static constexpr float kRefBias = 60.f, kOverflowGuard = 60.f; };
+template <> struct PRange<true> { static constexpr float kRefBias = 8.f, kOverflowGuard = 15.f; };
+constexpr int kHeadsPerWave = 32;                  // two 16-head MFMA blocks share every K / V operand
 
 struct MlaArgs {
-  const uint16_t* q;          // [B, S, H, 576] bf16
-  const uint16_t* kv;         // [B, Skv, 576] or paged [blocks, block_size, 576] bf16
+  const uint16_t* q;          // [B, S, H, 576] bf16 / fp16
+  const uint16_t* kv;         // [B, Skv, 576] or paged [blocks, block_size, 576]
   const int32_t* indices;     // [B, S, topk]
   const int32_t* block_table; // [B, max_blocks] or null
   const int32_t* q_len;       // [B] or null
   const int32_t* kv_len;      // [B] or null
-  uint16_t* out;              // [B, S, H, 512] bf16
+  uint16_t* out;              // [B, S, H, 512]
   float* lse;                 // [B, S, H]
-  uint16_t* part_o;           // [splits, B*S, H, 512] bf16 (splits > 1)
+  uint16_t* part_o;           // [splits, B*S, H, 512] (splits > 1)
   float* part_lse;            // [splits, B*S, H]
   int B, S, H, Skv, topk;
   int block_size, max_blocks;
@@ -58,129 +79,67 @@ struct MlaArgs {
   float scale_log2;           // sm_scale * log2(e)
 };
 
-__device__ __forceinline__ const uint16_t* kv_row(const MlaArgs& a, int b, int idx) {
-  int64_t r;
-  if (a.block_table) {
-    const int blk = a.block_table[(int64_t)b * a.max_blocks + idx / a.block_size];
-    r = (int64_t)blk * a.block_size + idx % a.block_size;
-  } else {
-    r = (int64_t)b * a.Skv + idx;
-  }
-  return a.kv + r * kMlaD;
+typedef __attribute__((address_space(3))) void lds_void;
+typedef const __attribute__((address_space(1))) void gbl_void;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// Workgroup barrier that the compiler may not move memory accesses across; it
+// emits no waitcnt of its own (the DMA pipeline manages vmcnt explicitly).
+__device__ __forceinline__ void raw_barrier() {
+  __asm__ __volatile__("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  __asm__ __volatile__("" ::: "memory");
 }
 
-// Interleave the bf16 halves of two words: lo16(x), lo16(y) and hi16(x), hi16(y).
-__device__ __forceinline__ uint32_t pair_lo(uint32_t x, uint32_t y) { return (x & 0xffffu) | (y << 16); }
-__device__ __forceinline__ uint32_t pair_hi(uint32_t x, uint32_t y) { return (x >> 16) | (y & 0xffff0000u); }
-
-__device__ __forceinline__ bool slot_valid(int idx, int kl, int lim) { return idx >= 0 && idx < kl && idx <= lim; }
-
-// One gather task of the value part: key pair kp (keys 2kp, 2kp+1 of the tile),
-// 16-byte column chunk c (value dims 8c .. 8c+7).
-__device__ __forceinline__ void vtask_load(const MlaArgs& a, const int32_t* irow, int slot0, int slot_end, int b,
-                                           int kl, int lim, int e, u32x4& x, u32x4& y) {
-  const int kp = e & 15;
-  const int c = e >> 4;
-  u32x4 v[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int slot = slot0 + 2 * kp + h;
-    const int idx = slot < slot_end ? irow[slot] : -1;
-    v[h] = u32x4{0, 0, 0, 0};
-    if (slot < slot_end && slot_valid(idx, kl, lim)) v[h] = *reinterpret_cast<const u32x4*>(kv_row(a, b, idx) + c * 8);
-  }
-  x = v[0];
-  y = v[1];
+// s_waitcnt with only vmcnt constrained (expcnt, lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-__device__ __forceinline__ void vtask_store(uint8_t* buf, int e, const u32x4& x, const u32x4& y) {
-  const int kp = e & 15;
-  const int c = e >> 4;
-  uint8_t* krow = buf;
-  *reinterpret_cast<u32x4*>(krow + (2 * kp) * kKPitch + c * 16) = x;
-  *reinterpret_cast<u32x4*>(krow + (2 * kp + 1) * kKPitch + c * 16) = y;
-  // Columns 8c .. 8c+7 of the column-major copy, keys 2kp and 2kp+1 packed per word.
-  uint8_t* col = buf + kKBytes + (8 * c) * kVtPitch + 4 * kp;
-  *reinterpret_cast<uint32_t*>(col + 0 * kVtPitch) = pair_lo(x.x, y.x);
-  *reinterpret_cast<uint32_t*>(col + 1 * kVtPitch) = pair_hi(x.x, y.x);
-  *reinterpret_cast<uint32_t*>(col + 2 * kVtPitch) = pair_lo(x.y, y.y);
-  *reinterpret_cast<uint32_t*>(col + 3 * kVtPitch) = pair_hi(x.y, y.y);
-  *reinterpret_cast<uint32_t*>(col + 4 * kVtPitch) = pair_lo(x.z, y.z);
-  *reinterpret_cast<uint32_t*>(col + 5 * kVtPitch) = pair_hi(x.z, y.z);
-  *reinterpret_cast<uint32_t*>(col + 6 * kVtPitch) = pair_lo(x.w, y.w);
-  *reinterpret_cast<uint32_t*>(col + 7 * kVtPitch) = pair_hi(x.w, y.w);
-}
-
-// One gather task of the rope tail (dims 512..575): key e/8, chunk 64 + e%8.
-__device__ __forceinline__ u32x4 ttask_load(const MlaArgs& a, const int32_t* irow, int slot0, int slot_end, int b,
-                                            int kl, int lim, int e) {
-  const int key = e >> 3;
-  const int c = 64 + (e & 7);
-  const int slot = slot0 + key;
-  const int idx = slot < slot_end ? irow[slot] : -1;
-  if (slot < slot_end && slot_valid(idx, kl, lim)) return *reinterpret_cast<const u32x4*>(kv_row(a, b, idx) + c * 8);
-  return u32x4{0, 0, 0, 0};
-}
-
-__device__ __forceinline__ void ttask_store(uint8_t* buf, int e, const u32x4& v) {
-  *reinterpret_cast<u32x4*>(buf + (e >> 3) * kKPitch + (64 + (e & 7)) * 16) = v;
-}
-
-__device__ __forceinline__ void bias_store(uint8_t* buf, const int32_t* irow, int slot0, int slot_end, int kl,
-                                           int lim) {
-  const int t = threadIdx.x;
-  if (t < kMlaTile) {
-    const int slot = slot0 + t;
-    const int idx = slot < slot_end ? irow[slot] : -1;
-    reinterpret_cast<float*>(buf + kKBytes + kVtBytes)[t] =
-        (slot < slot_end && slot_valid(idx, kl, lim)) ? 0.f : -__builtin_huge_valf();
+// Wait until at most `ahead` tiles (of L loads each) issued after the current one are pending.
+template <int L>
+__device__ __forceinline__ void wait_tiles(int ahead) {
+  switch (ahead) {
+    case 0: wait_vmcnt<0>(); break;
+    case 1: wait_vmcnt<L>(); break;
+    case 2: wait_vmcnt<(2 * L < 64 ? 2 * L : 0)>(); break;
+    default: wait_vmcnt<(3 * L < 64 ? 3 * L : 0)>(); break;
   }
 }
 
-// Register-staged gather (8-wave workgroups): loads for the next tile are in
-// flight while the current tile computes.
 template <int kNW>
-struct Staged {
+struct MlaCfg {
   static constexpr int kThreads = kNW * kWave;
-  static constexpr int kV = 1024 / kThreads;                     // value tasks per thread
-  static constexpr int kT = (kMlaTile * 8 + kThreads - 1) / kThreads;  // tail tasks per thread
-  u32x4 x[kV], y[kV], t[kT];
-
-  __device__ __forceinline__ void load(const MlaArgs& a, const int32_t* irow, int slot0, int slot_end, int b, int kl,
-                                       int lim) {
-#pragma unroll
-    for (int i = 0; i < kV; ++i) vtask_load(a, irow, slot0, slot_end, b, kl, lim, threadIdx.x + i * kThreads, x[i], y[i]);
-#pragma unroll
-    for (int i = 0; i < kT; ++i) {
-      const int e = threadIdx.x + i * kThreads;
-      t[i] = e < kMlaTile * 8 ? ttask_load(a, irow, slot0, slot_end, b, kl, lim, e) : u32x4{0, 0, 0, 0};
-    }
-  }
-  __device__ __forceinline__ void store(uint8_t* buf, const int32_t* irow, int slot0, int slot_end, int kl,
-                                        int lim) const {
-#pragma unroll
-    for (int i = 0; i < kV; ++i) vtask_store(buf, threadIdx.x + i * kThreads, x[i], y[i]);
-#pragma unroll
-    for (int i = 0; i < kT; ++i) {
-      const int e = threadIdx.x + i * kThreads;
-      if (e < kMlaTile * 8) ttask_store(buf, e, t[i]);
-    }
-    bias_store(buf, irow, slot0, slot_end, kl, lim);
-  }
+  // DMA instructions per tile for wave w: I = w, w + kNW, ... < kTileInstr.
+  static constexpr int kMaxPerWave = (kTileInstr + kNW - 1) / kNW;
+  static_assert(kTileInstr % kNW == 0, "every wave issues the same number of DMA loads per tile");
+  // Tiles kept in flight: bounded by the 6-bit vmcnt.
+  static constexpr int kDepth = (kAhead * kMaxPerWave < 64) ? kAhead : (63 / kMaxPerWave);
 };
 
-// Direct gather (smaller workgroups): load and store task by task.
+// Issue the DMA of tile `tile` (slots tile*32 .. +31 of this workgroup) into `stage_base`.
+// Stage layout, in 16-byte units: chunk c (dims 8c .. 8c+7) of slot r sits at
+// position 32*c + (r ^ 4*(c & 1)).  DMA instruction I fills positions
+// 64*I .. 64*I + 63, i.e. chunks 2I and 2I+1 of all 32 slots, so a lane always
+// serves the same slot (a fixed function of the lane) and only its row base
+// changes per tile.  Empty / masked slots re-load `safe_row` (a valid row of
+// this workgroup; its probability is forced to 0), so every load stays inside
+// the KV cache.
 template <int kNW>
-__device__ __forceinline__ void gather_direct(const MlaArgs& a, uint8_t* buf, const int32_t* irow, int slot0,
-                                              int slot_end, int b, int kl, int lim) {
-  constexpr int kThreads = kNW * kWave;
-  for (int e = threadIdx.x; e < 1024; e += kThreads) {
-    u32x4 x, y;
-    vtask_load(a, irow, slot0, slot_end, b, kl, lim, e, x, y);
-    vtask_store(buf, e, x, y);
+__device__ __forceinline__ void issue_tile(const uint8_t* kv, const int32_t* rows, int safe_row, int tile,
+                                           uint8_t* stage_base, int wave, int lane) {
+  const int r = (lane & 31) ^ (4 * ((lane >> 5) & 1));
+  int row = rows[tile * kMlaTile + r];
+  row = row >= 0 ? row : safe_row;
+  const uint8_t* src = kv + (int64_t)row * kRowBytes + 16 * (lane >> 5) + 32 * wave;
+#pragma unroll
+  for (int i = 0; i < MlaCfg<kNW>::kMaxPerWave; ++i) {
+    const int I = wave + i * kNW;
+    __builtin_amdgcn_global_load_lds((gbl_void*)(src + 32 * kNW * i), (lds_void*)(stage_base + I * 1024), 16, 0, 0);
   }
-  for (int e = threadIdx.x; e < kMlaTile * 8; e += kThreads) ttask_store(buf, e, ttask_load(a, irow, slot0, slot_end, b, kl, lim, e));
-  bias_store(buf, irow, slot0, slot_end, kl, lim);
 }
 
 template <bool kF16>
@@ -222,10 +181,175 @@ __device__ __forceinline__ float unpack_hi(uint32_t v) {
   else return __uint_as_float(v & 0xffff0000u);
 }
 
+// ds_read_b64_tr_b16 as inline asm: through the builtin the compiler waits for
+// every outstanding DMA before each read.  Completion is tracked explicitly
+// with lgkm_wait below.
+template <int kOff>
+__device__ __forceinline__ void tr_read(u32x2& out, uint32_t lds_addr) {
+  __asm__ __volatile__("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(out) : "v"(lds_addr), "i"(kOff));
+}
+
+// Wait until at most N LDS operations are outstanding; the four values pass
+// through the asm so no use of them can be scheduled before the wait.
+template <int N>
+__device__ __forceinline__ void lgkm_wait(u32x2 (&v)[4]) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  __asm__ __volatile__("s_waitcnt lgkmcnt(%4)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]) : "i"(N));
+}
+
+// The four transposed reads of one pair of 16-column blocks 2*kGrp, 2*kGrp + 1:
+// v[2j], v[2j+1] = keys 4g..4g+3 and 16+4g..16+4g+3 of block 2*kGrp + j, at
+// bytes pa + 1024*cb (+256 for the second key group).
+template <int kGrp>
+__device__ __forceinline__ void pv_group_reads(u32x2 (&v)[4], uint32_t pa) {
+  tr_read<1024 * (2 * kGrp)>(v[0], pa);
+  tr_read<1024 * (2 * kGrp) + 256>(v[1], pa);
+  tr_read<1024 * (2 * kGrp + 1)>(v[2], pa);
+  tr_read<1024 * (2 * kGrp + 1) + 256>(v[3], pa);
+}
+
+template <bool kF16, int kGrp>
+__device__ __forceinline__ void pv_group_mfma(f32x4 (&o)[2][kMlaDV / 16], const u32x4 (&pa)[2], const u32x2 (&v)[4]) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const u32x4 vb = {v[2 * j].x, v[2 * j].y, v[2 * j + 1].x, v[2 * j + 1].y};
+    o[0][2 * kGrp + j] = mfma16<kF16>(pa[0], vb, o[0][2 * kGrp + j]);
+    o[1][2 * kGrp + j] = mfma16<kF16>(pa[1], vb, o[1][2 * kGrp + j]);
+  }
+}
+
+// O += P V over one tile: 16 pairs of 16-column blocks, the reads of pair k+1
+// in flight while pair k runs on the matrix cores.
+template <bool kF16, int kGrp>
+__device__ __forceinline__ void pv_pipeline(f32x4 (&o)[2][kMlaDV / 16], const u32x4 (&pa)[2], uint32_t vaddr,
+                                            u32x2 (&cur)[4]) {
+  if constexpr (kGrp + 1 < kMlaDV / 32) {
+    u32x2 nxt[4];
+    pv_group_reads<kGrp + 1>(nxt, vaddr);
+    lgkm_wait<4>(cur);
+    pv_group_mfma<kF16, kGrp>(o, pa, cur);
+    pv_pipeline<kF16, kGrp + 1>(o, pa, vaddr, nxt);
+  } else {
+    lgkm_wait<0>(cur);
+    pv_group_mfma<kF16, kGrp>(o, pa, cur);
+  }
+}
+
+template <int kOff>
+__device__ __forceinline__ void b128_read(u32x4& out, uint32_t lds_addr) {
+  __asm__ __volatile__("ds_read_b128 %0, %1 offset:%2" : "=v"(out) : "v"(lds_addr), "i"(kOff));
+}
+
+template <int N>
+__device__ __forceinline__ void lgkm_wait2(u32x4& a, u32x4& b) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  __asm__ __volatile__("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
+}
+
+// S^T += K Q^T over d = 576: 18 steps of 32 dims; the two K reads of step
+// st + 1 are in flight while step st runs on the matrix cores.  Lane (g, r)
+// reads chunk 4*st + g of slots r and 16 + r: bytes qa + 2048*st (+256).
+template <bool kF16, int kSt>
+__device__ __forceinline__ void qk_pipeline(f32x4 (&c)[2][2], const u32x4 (&qb)[2][kMlaD / 32], uint32_t qa,
+                                            u32x4& k0, u32x4& k1) {
+  constexpr int kSteps = kMlaD / 32;
+  if constexpr (kSt + 1 < kSteps) {
+    u32x4 n0, n1;
+    b128_read<2048 * (kSt + 1)>(n0, qa);
+    b128_read<2048 * (kSt + 1) + 256>(n1, qa);
+    lgkm_wait2<2>(k0, k1);
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+      c[hb][0] = mfma16<kF16>(k0, qb[hb][kSt], c[hb][0]);
+      c[hb][1] = mfma16<kF16>(k1, qb[hb][kSt], c[hb][1]);
+    }
+    qk_pipeline<kF16, kSt + 1>(c, qb, qa, n0, n1);
+  } else {
+    lgkm_wait2<0>(k0, k1);
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+      c[hb][0] = mfma16<kF16>(k0, qb[hb][kSt], c[hb][0]);
+      c[hb][1] = mfma16<kF16>(k1, qb[hb][kSt], c[hb][1]);
+    }
+  }
+}
+
+__device__ __forceinline__ uint32_t lds_u32(const void* p) {
+  return (uint32_t)(uintptr_t)(const lds_void*)p;
+}
+
+// Exact two-pass fallback for a workgroup whose scores outgrew the fast
+// path's fixed reference: per head, the scores of all slots go to LDS, then
+// max, sum and P V from them.  Slow (VALU, KV re-read per head) and only taken
+// for pathological score ranges.  Writes the same outputs as the fast path.
+// Arguments are passed by value (a reference to the kernel's argument block
+// would force that block into scratch memory for the whole kernel).
+template <bool kF16>
+__device__ __attribute__((noinline)) void mla_exact_fallback(const uint16_t* q, const uint8_t* kvb,
+                                                             uint16_t* obase, float* lbase, int H,
+                                                             float scale_log2, const int32_t* rows, int nslots,
+                                                             int token, int head_begin, int nheads, float* sc,
+                                                             int threads) {
+  const int tid = threadIdx.x;
+  float* red = sc + kSlotsCap;  // per-wave partials
+  for (int hl = 0; hl < nheads; ++hl) {
+    const int h = head_begin + hl;
+    if (h >= H) break;
+    const uint16_t* qh = q + ((int64_t)token * H + h) * kMlaD;
+    float mx = -__builtin_huge_valf();
+    for (int j = tid; j < nslots; j += threads) {
+      const int row = rows[j];
+      float sj = -__builtin_huge_valf();
+      if (row >= 0) {
+        const uint16_t* kr = reinterpret_cast<const uint16_t*>(kvb + (int64_t)row * kRowBytes);
+        float acc = 0.f;
+        for (int d = 0; d < kMlaD; d += 2) {
+          const uint32_t qv = *reinterpret_cast<const uint32_t*>(qh + d);
+          const uint32_t kv = *reinterpret_cast<const uint32_t*>(kr + d);
+          acc = fmaf(unpack_lo<kF16>(qv), unpack_lo<kF16>(kv), acc);
+          acc = fmaf(unpack_hi<kF16>(qv), unpack_hi<kF16>(kv), acc);
+        }
+        sj = acc * scale_log2;
+      }
+      sc[j] = sj;
+      mx = fmaxf(mx, sj);
+    }
+    mx = wave_max(mx);
+    if ((tid & (kWave - 1)) == 0) red[tid / kWave] = mx;
+    __syncthreads();
+    mx = -__builtin_huge_valf();
+    for (int w = 0; w < threads / kWave; ++w) mx = fmaxf(mx, red[w]);
+    __syncthreads();
+    const float m_use = mx == -__builtin_huge_valf() ? 0.f : mx;
+    float l = 0.f;
+    for (int j = tid; j < nslots; j += threads) l += fast_exp2(sc[j] - m_use);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, kWave);
+    if ((tid & (kWave - 1)) == 0) red[tid / kWave] = l;
+    __syncthreads();
+    l = 0.f;
+    for (int w = 0; w < threads / kWave; ++w) l += red[w];
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    for (int c = tid; c < kMlaDV; c += threads) {
+      float acc = 0.f;
+      for (int j = 0; j < nslots; ++j) {
+        const int row = rows[j];
+        if (row < 0) continue;
+        const uint16_t v = reinterpret_cast<const uint16_t*>(kvb + (int64_t)row * kRowBytes)[c];
+        acc = fmaf(fast_exp2(sc[j] - m_use), unpack_lo<kF16>(v), acc);
+      }
+      obase[((int64_t)token * H + h) * kMlaDV + c] = cvt1<kF16>(acc * inv);
+    }
+    if (tid == 0) lbase[(int64_t)token * H + h] = l > 0.f ? (mx + fast_log2(l)) * 0.69314718055994531f : -__builtin_huge_valf();
+    __syncthreads();
+  }
+}
+
 template <int kNW, bool kF16>
 __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
-  constexpr bool kStaged = (kNW == 8);
+  using Cfg = MlaCfg<kNW>;
   extern __shared__ __align__(16) uint8_t lds[];
+  int32_t* rows = reinterpret_cast<int32_t*>(lds + kRowsOffset);
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
@@ -237,8 +361,11 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   const int split = blockIdx.x / T;
   const int b = token / a.S;
   const int s = token % a.S;
-  const int head0 = blockIdx.y * (kNW * 16) + wave * 16;
-  const bool wave_active = head0 < a.H;
+  // A wave owns two 16-head blocks: heads head0 + 16*hb + r.
+  const int head0 = blockIdx.y * (kNW * kHeadsPerWave) + wave * kHeadsPerWave;
+  bool hb_on[2];
+  hb_on[0] = head0 < a.H;
+  hb_on[1] = head0 + 16 < a.H;
 
   const int ql = a.q_len ? a.q_len[b] : a.S;
   const int kl = a.kv_len ? a.kv_len[b] : a.Skv;
@@ -247,140 +374,197 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   const int32_t* irow = a.indices + (int64_t)token * a.topk;
   const int slot_begin = split * a.keys_per_split;
   const int slot_end = min(a.topk, slot_begin + a.keys_per_split);
-  const int ntiles = row_active && slot_end > slot_begin ? (slot_end - slot_begin + kMlaTile - 1) / kMlaTile : 0;
+  const int nslots = slot_end > slot_begin ? slot_end - slot_begin : 0;
+  int ntiles = row_active ? (nslots + kMlaTile - 1) / kMlaTile : 0;
 
-  // Q operand (B of S^T = K Q^T): head head0 + r, dims 32*st + 8*g .. +8.
-  u32x4 qb[kMlaD / 32];
-  {
-    const uint16_t* qp = a.q + ((int64_t)token * a.H + head0 + r) * kMlaD + 8 * g;
+  // Q operands (B of S^T = K Q^T): head head0 + 16*hb + r, dims 32*st + 8*g .. +8.
+  u32x4 qb[2][kMlaD / 32];
+#pragma unroll
+  for (int hb = 0; hb < 2; ++hb) {
+    const uint16_t* qp = a.q + ((int64_t)token * a.H + head0 + 16 * hb + r) * kMlaD + 8 * g;
+    const bool on = hb_on[hb] && row_active;
 #pragma unroll
     for (int st = 0; st < kMlaD / 32; ++st) {
-      qb[st] = (wave_active && row_active) ? *reinterpret_cast<const u32x4*>(qp + 32 * st) : u32x4{0, 0, 0, 0};
+      qb[hb][st] = on ? *reinterpret_cast<const u32x4*>(qp + 32 * st) : u32x4{0, 0, 0, 0};
     }
   }
-
-  f32x4 o[kMlaDV / 16];
+  // Q must be resident before the DMA ring starts: vmcnt then only counts DMA.
+  wait_vmcnt<0>();
 #pragma unroll
-  for (int i = 0; i < kMlaDV / 16; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m2 = -__builtin_huge_valf();  // running max (base-2 units) of head head0 + r
-  float lsum = 0.f;                   // this lane's share of the running sum
-
-  Staged<kNW> gs;
-  if (ntiles > 0) {
-    if constexpr (kStaged) {
-      gs.load(a, irow, slot_begin, slot_end, b, kl, lim);
-      gs.store(lds, irow, slot_begin, slot_end, kl, lim);
-    } else {
-      gather_direct<kNW>(a, lds, irow, slot_begin, slot_end, b, kl, lim);
+  for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+    for (int st = 0; st < kMlaD / 32; ++st) __asm__ __volatile__("" : "+v"(qb[hb][st]));
+  // Slots -> physical rows (-1: empty or masked); the lowest valid slot's row
+  // doubles as the DMA source of the empty ones.
+  int32_t* first_valid = rows + kSlotsCap + 1;
+  if (tid == 0) *first_valid = 0x7fffffff;
+  __syncthreads();
+  for (int i = tid; i < ntiles * kMlaTile; i += Cfg::kThreads) {
+    int row = -1;
+    if (i < nslots) {
+      const int idx = irow[slot_begin + i];
+      if (idx >= 0 && idx < kl && idx <= lim) {
+        if (a.block_table) {
+          const int blk = a.block_table[(int64_t)b * a.max_blocks + idx / a.block_size];
+          row = blk * a.block_size + idx % a.block_size;
+        } else {
+          row = b * a.Skv + idx;
+        }
+      }
     }
+    rows[i] = row;
+    if (row >= 0) atomicMin(first_valid, i);
   }
   __syncthreads();
+  const int fv = *first_valid;
+  const int safe_row = fv < kSlotsCap ? rows[fv] : -1;
+  if (safe_row < 0) ntiles = 0;  // no valid slot: out = 0, lse = -inf
 
-  for (int tile = 0; tile < ntiles; ++tile) {
-    uint8_t* buf = lds + (tile & 1) * kBufBytes;
-    const int next0 = slot_begin + (tile + 1) * kMlaTile;
-    if constexpr (kStaged) {
-      if (tile + 1 < ntiles) gs.load(a, irow, next0, slot_end, b, kl, lim);
-    }
-
-    if (wave_active) {
-      const uint8_t* krow = buf;
-      const uint8_t* vt = buf + kKBytes;
-      const float* bias = reinterpret_cast<const float*>(buf + kKBytes + kVtBytes);
-      // S^T[key][head] for keys 0-15 (c0) and 16-31 (c1).
-      f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+  const uint8_t* kvb = reinterpret_cast<const uint8_t*>(a.kv);
+  const int depth = Cfg::kDepth;
 #pragma unroll
-      for (int st = 0; st < kMlaD / 32; ++st) {
-        const u32x4 k0 = *reinterpret_cast<const u32x4*>(krow + r * kKPitch + (32 * st + 8 * g) * 2);
-        const u32x4 k1 = *reinterpret_cast<const u32x4*>(krow + (16 + r) * kKPitch + (32 * st + 8 * g) * 2);
-        c0 = mfma16<kF16>(k0, qb[st], c0);
-        c1 = mfma16<kF16>(k1, qb[st], c1);
-      }
-      // Lane (g, r) holds keys 4g+i and 16+4g+i of head head0 + r.
-      float t[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        t[i] = c0[i] * a.scale_log2 + bias[4 * g + i];
-        t[4 + i] = c1[i] * a.scale_log2 + bias[16 + 4 * g + i];
-      }
-      float tmax = t[0];
-#pragma unroll
-      for (int i = 1; i < 8; ++i) tmax = fmaxf(tmax, t[i]);
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
-      const float m_new = fmaxf(m2, tmax);
-      const float m_use = (m_new == -__builtin_huge_valf()) ? 0.f : m_new;
-      const float alpha = fast_exp2(m2 - m_use);
-      float p[8];
-      float psum = 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        p[i] = fast_exp2(t[i] - m_use);
-        psum += p[i];
-      }
-      lsum = lsum * alpha + psum;
-      m2 = m_new;
-      // Rows of the PV accumulator are heads 4g+i: fetch their alpha.
-      float al[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * g + i, kWave);
-      const u32x4 pa = {pack2<kF16>(p[0], p[1]), pack2<kF16>(p[2], p[3]), pack2<kF16>(p[4], p[5]), pack2<kF16>(p[6], p[7])};
-#pragma unroll
-      for (int cb = 0; cb < kMlaDV / 16; ++cb) {
-        const uint8_t* col = vt + (16 * cb + r) * kVtPitch;
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(col + 8 * g);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(col + 32 + 8 * g);
-        const u32x4 vb = {lo.x, lo.y, hi.x, hi.y};
-        f32x4 acc = o[cb];
-        acc[0] *= al[0]; acc[1] *= al[1]; acc[2] *= al[2]; acc[3] *= al[3];
-        o[cb] = mfma16<kF16>(pa, vb, acc);
-      }
-    }
-    if (tile + 1 < ntiles) {
-      __syncthreads();  // everyone is done reading the other buffer (tile - 1)
-      uint8_t* nbuf = lds + ((tile + 1) & 1) * kBufBytes;
-      if constexpr (kStaged) {
-        gs.store(nbuf, irow, next0, slot_end, kl, lim);
-      } else {
-        gather_direct<kNW>(a, nbuf, irow, next0, slot_end, b, kl, lim);
-      }
-    }
-    __syncthreads();
+  for (int t = 0; t < Cfg::kDepth; ++t) {
+    if (t < ntiles) issue_tile<kNW>(kvb, rows, safe_row, t, lds + (t % kStages) * kStageBytes, wave, lane);
   }
 
-  // Epilogue: normalise, write out (or the split partial) and the LSE.
-  float l_tot = lsum;
-  l_tot += __shfl_xor(l_tot, 16, kWave);
-  l_tot += __shfl_xor(l_tot, 32, kWave);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  float inv_i[4];
+  f32x4 o[2][kMlaDV / 16];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) inv_i[i] = __shfl(inv, 4 * g + i, kWave);
+  for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+    for (int i = 0; i < kMlaDV / 16; ++i) o[hb][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_ref[2] = {-__builtin_huge_valf(), -__builtin_huge_valf()};  // reference max (base 2)
+  float lsum[2] = {0.f, 0.f};  // this lane's share of sum exp2(t - m_ref)
+  int32_t* overflow_flag = rows + kSlotsCap;
+  bool overflow = false;
 
+  // Per-lane LDS byte offsets in a stage (see issue_tile for the layout).
+  // QK A operand: chunk 4*st + g of slots r, 16 + r -> 512*g + 16*(r ^ 4*(g & 1)) + 2048*st (+256).
+  const uint32_t qk_lane = 512 * g + 16 * (r ^ (4 * (g & 1)));
+  // PV B operand through transposed reads: lane (g, s = r) addresses slot
+  // 4g + (r >> 2) (+16), columns 16*cb + 4*(r & 3), i.e. chunk 2*cb + h with
+  // h = (r >> 1) & 1 -> 512*h + 16*((4g + (r >> 2)) ^ 4h) + 8*(r & 1) + 1024*cb (+256).
+  const int hh = (r >> 1) & 1;
+  const uint32_t pv_lane = 512 * hh + 16 * ((4 * g + (r >> 2)) ^ (4 * hh)) + 8 * (r & 1);
+
+  for (int tile = 0; tile < ntiles; ++tile) {
+    uint8_t* buf = lds + (tile % kStages) * kStageBytes;
+    if (tile + depth < ntiles) {
+      issue_tile<kNW>(kvb, rows, safe_row, tile + depth, lds + ((tile + depth) % kStages) * kStageBytes, wave, lane);
+    }
+    wait_tiles<Cfg::kMaxPerWave>(min(depth, ntiles - 1 - tile));
+    raw_barrier();
+
+    // S^T[key][head] for keys 0-15 (kb 0) and 16-31 (kb 1), both head blocks.
+    f32x4 c[2][2];
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) c[hb][0] = c[hb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    {
+      // K rows come through inline-asm LDS reads (see tr_read) with explicit waits.
+      const uint32_t qa = lds_u32(buf) + qk_lane;
+      u32x4 k0, k1;
+      b128_read<0>(k0, qa);
+      b128_read<256>(k1, qa);
+      qk_pipeline<kF16, 0>(c, qb, qa, k0, k1);
+    }
+    // Lane (g, r) holds keys 4g+i and 16+4g+i of heads head0 + 16*hb + r.
+    const i32x4 v0 = *reinterpret_cast<const i32x4*>(rows + tile * kMlaTile + 4 * g);
+    const i32x4 v1 = *reinterpret_cast<const i32x4*>(rows + tile * kMlaTile + 16 + 4 * g);
+    bool valid[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      valid[i] = v0[i] >= 0;
+      valid[4 + i] = v1[i] >= 0;
+    }
+    u32x4 pa[2];
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+      // Raw scores with empty slots at -inf; sm_scale > 0, so the max commutes with it.
+      float cm[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        cm[i] = valid[i] ? c[hb][0][i] : -__builtin_huge_valf();
+        cm[4 + i] = valid[4 + i] ? c[hb][1][i] : -__builtin_huge_valf();
+      }
+      float cmax = fmaxf(fmaxf(fmaxf(cm[0], cm[1]), fmaxf(cm[2], cm[3])), fmaxf(fmaxf(cm[4], cm[5]), fmaxf(cm[6], cm[7])));
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 16, kWave));
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 32, kWave));
+      const float tmax = cmax * a.scale_log2;
+      // The reference max is fixed by the first tile with a valid score, biased
+      // up by 2^kRefBias so later scores may exceed it by 2^(kRefBias +
+      // kOverflowGuard) without a rescale of O (scaling by a power of two is
+      // exact; for bf16, contributions more than 2^66 below the first tile's
+      // max underflow, negligibly).  A larger jump flags the workgroup for the
+      // exact fallback after the loop.
+      if (m_ref[hb] == -__builtin_huge_valf()) {
+        if (tmax != -__builtin_huge_valf()) m_ref[hb] = tmax + PRange<kF16>::kRefBias;
+      } else if (tmax > m_ref[hb] + PRange<kF16>::kOverflowGuard) {
+        overflow = true;
+      }
+      const float neg_m = (m_ref[hb] == -__builtin_huge_valf()) ? 0.f : -m_ref[hb];
+      float p[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) p[i] = fast_exp2(fmaf(cm[i], a.scale_log2, neg_m));
+      lsum[hb] += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+      pa[hb] = u32x4{pack2<kF16>(p[0], p[1]), pack2<kF16>(p[2], p[3]), pack2<kF16>(p[4], p[5]), pack2<kF16>(p[6], p[7])};
+    }
+    {
+      const uint32_t va = lds_u32(buf) + pv_lane;
+      u32x2 first[4];
+      pv_group_reads<0>(first, va);
+      pv_pipeline<kF16, 0>(o, pa, va, first);
+    }
+    // All reads of this stage retire before anyone refills it.
+    __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
+    raw_barrier();
+  }
+
+  // Any wave whose scores outgrew the biased reference: recompute exactly.
+  if (tid == 0) *overflow_flag = 0;
+  __syncthreads();
+  if (__any(overflow) && lane == 0) *overflow_flag = 1;
+  __syncthreads();
   const bool final_out = (a.splits == 1);
   uint16_t* obase = final_out ? a.out : a.part_o + (int64_t)split * T * a.H * kMlaDV;
   float* lbase = final_out ? a.lse : a.part_lse + (int64_t)split * T * a.H;
-  // Stage the wave's 16 x 512 tile in LDS, then store 16-byte row chunks.
-  uint16_t* stage = reinterpret_cast<uint16_t*>(lds) + wave * 16 * (kMlaDV + 8);
+  if (*overflow_flag) {
+    mla_exact_fallback<kF16>(a.q, reinterpret_cast<const uint8_t*>(a.kv), obase, lbase, a.H, a.scale_log2, rows,
+                             ntiles * kMlaTile, token, blockIdx.y * (kNW * kHeadsPerWave), kNW * kHeadsPerWave,
+                             reinterpret_cast<float*>(lds), kNW * kWave);
+    return;
+  }
+
+  // Epilogue: normalise, write out (or the split partial) and the LSE.
+  __syncthreads();  // the ring is free: reuse it to stage the output rows
+  uint16_t* stage = reinterpret_cast<uint16_t*>(lds) + wave * kHeadsPerWave * (kMlaDV + 8);
 #pragma unroll
-  for (int cb = 0; cb < kMlaDV / 16; ++cb) {
+  for (int hb = 0; hb < 2; ++hb) {
+    float l_tot = lsum[hb];
+    l_tot += __shfl_xor(l_tot, 16, kWave);
+    l_tot += __shfl_xor(l_tot, 32, kWave);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    float inv_i[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) stage[(4 * g + i) * (kMlaDV + 8) + 16 * cb + r] = cvt1<kF16>(o[cb][i] * inv_i[i]);
+    for (int i = 0; i < 4; ++i) inv_i[i] = __shfl(inv, 4 * g + i, kWave);
+#pragma unroll
+    for (int cb = 0; cb < kMlaDV / 16; ++cb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        stage[(16 * hb + 4 * g + i) * (kMlaDV + 8) + 16 * cb + r] = cvt1<kF16>(o[hb][cb][i] * inv_i[i]);
+    }
+    if (hb_on[hb] && g == 0) {
+      const float lse = l_tot > 0.f ? (m_ref[hb] + fast_log2(l_tot)) * 0.69314718055994531f : -__builtin_huge_valf();
+      lbase[(int64_t)token * a.H + head0 + 16 * hb + r] = lse;
+    }
   }
   __syncthreads();
-  if (wave_active) {
-    uint16_t* orow = obase + ((int64_t)token * a.H + head0) * kMlaDV;
+  uint16_t* orow = obase + ((int64_t)token * a.H + head0) * kMlaDV;
 #pragma unroll
-    for (int it = 0; it < 16 * kMlaDV / 8 / kWave; ++it) {
-      const int e = lane + it * kWave;  // 16-byte chunk: head e / 64, cols 8*(e % 64)
-      const int h = e >> 6;
-      const int c = (e & 63) * 8;
+  for (int it = 0; it < kHeadsPerWave * kMlaDV / 8 / kWave; ++it) {
+    const int e = lane + it * kWave;  // 16-byte chunk: head e / 64, cols 8*(e % 64)
+    const int h = e >> 6;
+    const int c = (e & 63) * 8;
+    if (head0 + h < a.H)
       *reinterpret_cast<u32x4*>(orow + h * kMlaDV + c) = *reinterpret_cast<const u32x4*>(stage + h * (kMlaDV + 8) + c);
-    }
-    if (g == 0) {
-      const float lse = l_tot > 0.f ? (m2 + fast_log2(l_tot)) * 0.69314718055994531f : -__builtin_huge_valf();
-      lbase[(int64_t)token * a.H + head0 + r] = lse;
-    }
   }
 }
 
@@ -426,10 +610,15 @@ __global__ __launch_bounds__(256) void sparse_mla_combine_kernel(const uint16_t*
 
 int mla_choose_splits(int64_t tokens, int64_t head_groups, int64_t topk) {
   const int64_t wgs = tokens * head_groups;
-  int splits = 1;
   const int max_splits = (int)((topk + kMlaTile - 1) / kMlaTile);
+  int splits = (int)((topk + kSlotsCap - 1) / kSlotsCap);  // each split's slots must fit in LDS
   while (wgs * splits < 256 && splits * 2 <= max_splits) splits *= 2;
   return splits;
+}
+
+static int64_t mla_keys_per_split(int64_t topk, int splits) {
+  const int64_t per = (topk + splits - 1) / splits;
+  return ((per + kMlaTile - 1) / kMlaTile) * kMlaTile;
 }
 
 size_t mla_workspace_bytes(int64_t tokens, int64_t H, int64_t topk) {
@@ -455,9 +644,8 @@ static hipError_t launch_mla_nw(const MlaArgs& a, int head_groups, hipStream_t s
 template <bool kF16>
 static hipError_t launch_mla_dtype(const MlaArgs& a, int head_groups, int hpg, hipStream_t stream) {
   hipError_t e;
-  if (hpg > 64) e = launch_mla_nw<8, kF16>(a, head_groups, stream);
-  else if (hpg > 32) e = launch_mla_nw<4, kF16>(a, head_groups, stream);
-  else if (hpg > 16) e = launch_mla_nw<2, kF16>(a, head_groups, stream);
+  if (hpg > 64) e = launch_mla_nw<4, kF16>(a, head_groups, stream);
+  else if (hpg > 32) e = launch_mla_nw<2, kF16>(a, head_groups, stream);
   else e = launch_mla_nw<1, kF16>(a, head_groups, stream);
   if (e != hipSuccess || a.splits == 1) return e;
   const int64_t rows = (int64_t)a.B * a.S * a.H;
@@ -467,7 +655,8 @@ static hipError_t launch_mla_dtype(const MlaArgs& a, int head_groups, int hpg, h
   return hipGetLastError();
 }
 
-// Caller validated: d_qk 576, d_v 512, H % 16 == 0, 16-bit inputs, workspace >= mla_workspace_bytes.
+// Caller validated: d_qk 576, d_v 512, H % 16 == 0, 16-bit inputs, workspace >= mla_workspace_bytes,
+// physical KV rows < 2^31.
 hipError_t launch_sparse_mla(int is_fp16, const void* q, const void* kv, const int32_t* indices,
                              const int32_t* block_table, const int32_t* q_len, const int32_t* kv_len, int64_t B,
                              int64_t S, int64_t H, int64_t Skv, int64_t block_size, int64_t max_blocks, int64_t topk,
@@ -494,8 +683,7 @@ hipError_t launch_sparse_mla(int is_fp16, const void* q, const void* kv, const i
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   const int head_groups = (int)((H + 127) / 128);
   a.splits = mla_choose_splits(T, head_groups, topk);
-  const int64_t per = (topk + a.splits - 1) / a.splits;
-  a.keys_per_split = (int)(((per + kMlaTile - 1) / kMlaTile) * kMlaTile);
+  a.keys_per_split = (int)mla_keys_per_split(topk, a.splits);
   a.part_o = nullptr;
   a.part_lse = nullptr;
   if (a.splits > 1) {

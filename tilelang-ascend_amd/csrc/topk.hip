@@ -27,6 +27,7 @@ constexpr int kTopkWaves = kTopkThreads / kWave;
 constexpr int kHistBins = 2048;
 constexpr int kRedWords = 64;
 constexpr int kLdsBytes = 160 * 1024;
+constexpr int32_t kFallbackFlag = (int32_t)0x80000000;  // out_idx[row][0] marker: row needs the exact radix path
 
 // Block-wide exclusive scan of one uint32 per thread; `total` receives the sum.
 // Uses red[0..kTopkWaves) and ends with a barrier so red can be reused.
@@ -62,7 +63,7 @@ __device__ __forceinline__ uint32_t load_key(const float* __restrict__ xr, const
 template <bool kCached>
 __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(
     const float* __restrict__ x, int64_t ld, int n, int k, const int32_t* __restrict__ row_len,
-    int sorted, int kpad, int32_t* __restrict__ out_idx, float* __restrict__ out_val) {
+    int sorted, int kpad, int32_t* __restrict__ out_idx, float* __restrict__ out_val, int only_flagged) {
   extern __shared__ __align__(16) uint32_t lds[];
   uint32_t* hist = lds;                                     // kHistBins
   uint32_t* red = hist + kHistBins;                         // kRedWords
@@ -74,6 +75,9 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(
   const float* __restrict__ xr = x + (int64_t)row * ld;
   int32_t* __restrict__ oi = out_idx + (int64_t)row * k;
   float* __restrict__ ov = out_val ? out_val + (int64_t)row * k : nullptr;
+  // Second pass behind topk_reg_kernel: only the rows it handed over.
+  if (only_flagged && oi[0] != kFallbackFlag) return;
+  __syncthreads();  // every thread has read the flag before any overwrites it
   int nv = n;
   if (row_len) nv = min(max(row_len[row], 0), n);
 
@@ -214,6 +218,181 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(
   }
 }
 
+
+// ----------------------------------------------------------------------------
+// Register-resident fast path (rows of up to 4096 * kChunks scores).
+//
+// The row is loaded once into VGPRs (kChunks 16-byte loads per thread, all in
+// flight together).  Present scores (> -1e30, not NaN) are bucketed into 2048
+// bins linear in value between the row's min and max -- a monotone map, so
+// every score in a higher bin is strictly larger -- which spreads the
+// histogram atomics far better than key-bit radix digits do.  A descending
+// scan finds the bin b* holding the k-th largest; every score in bins >= b*
+// goes, as a (key << 32 | ~index) word, into an LDS list grouped by bin.  Each
+// list entry then counts the entries of its own bin that beat it: bin offset
+// + that rank is its final sorted position (value desc, index asc), exact
+// with ties, and entries landing below k are written out directly.  Rows the
+// fast path cannot bound (all-equal scores, a list over kListCap, a bin over
+// kBinCap, non-finite range) are flagged in out_idx[row][0] for the exact
+// radix kernel, launched right after on the same stream.
+// ----------------------------------------------------------------------------
+constexpr int kListCap = 4096;
+constexpr int kBinCap = 512;
+
+template <int kChunks>
+__global__ __launch_bounds__(kTopkThreads) void topk_reg_kernel(const float* __restrict__ x, int64_t ld, int n, int k,
+                                                                const int32_t* __restrict__ row_len,
+                                                                int32_t* __restrict__ out_idx,
+                                                                float* __restrict__ out_val) {
+  __shared__ uint32_t cnt[kHistBins];
+  __shared__ uint32_t offs[kHistBins];
+  __shared__ uint32_t fill[kHistBins];
+  __shared__ uint32_t red[kRedWords];
+  __shared__ uint64_t list[kListCap];
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const float* __restrict__ xr = x + (int64_t)row * ld;
+  int32_t* __restrict__ oi = out_idx + (int64_t)row * k;
+  float* __restrict__ ov = out_val ? out_val + (int64_t)row * k : nullptr;
+  int nv = n;
+  if (row_len) nv = min(max(row_len[row], 0), n);
+
+  // 1. Load: thread t holds elements 4*(t + c*1024) .. +3 of chunk c.
+  float v[kChunks][4];
+  const bool vec = ((reinterpret_cast<uintptr_t>(xr) & 15) == 0);
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c) {
+    const int e0 = 4 * (tid + c * kTopkThreads);
+    if (vec && e0 + 3 < nv) {
+      const f32x4 t = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(xr) + (tid + c * kTopkThreads));
+      v[c][0] = t[0]; v[c][1] = t[1]; v[c][2] = t[2]; v[c][3] = t[3];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[c][j] = (e0 + j < nv) ? xr[e0 + j] : -__builtin_huge_valf();
+    }
+  }
+  for (int b = tid; b < kHistBins; b += kTopkThreads) { cnt[b] = 0; fill[b] = 0; }
+
+  // 2. Count, min and max of the present scores.
+  uint32_t present = 0;
+  float vmin = __builtin_huge_valf(), vmax = -__builtin_huge_valf();
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool p = v[c][j] > -1e30f;  // false for NaN too
+      present += p;
+      if (p) { vmin = fminf(vmin, v[c][j]); vmax = fmaxf(vmax, v[c][j]); }
+    }
+  present = (uint32_t)wave_sum_i((int)present);
+  vmin = -wave_max(-vmin);
+  vmax = wave_max(vmax);
+  if (lane == 0) {
+    red[wave] = present;
+    red[16 + wave] = __float_as_uint(vmin);
+    red[32 + wave] = __float_as_uint(vmax);
+  }
+  __syncthreads();
+  uint32_t m_total = 0;
+  vmin = __builtin_huge_valf();
+  vmax = -__builtin_huge_valf();
+#pragma unroll
+  for (int w = 0; w < kTopkWaves; ++w) {
+    m_total += red[w];
+    vmin = fminf(vmin, __uint_as_float(red[16 + w]));
+    vmax = fmaxf(vmax, __uint_as_float(red[32 + w]));
+  }
+  const int kk = min((int)m_total, k);
+  const float inv = 2048.f / (vmax - vmin);
+  // Degenerate ranges go to the exact path (a single distinct value, or a
+  // range whose width or inverse is not a normal finite number).
+  if (kk > 0 && !(vmax > vmin && inv < 3.0e38f && inv > 0.f)) {
+    if (tid == 0) oi[0] = kFallbackFlag;
+    return;  // block-uniform
+  }
+  __syncthreads();
+
+  // 3. Histogram of bin(v) = min(2047, (int)((v - vmin) * inv)).
+  if (kk > 0) {
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (v[c][j] > -1e30f) atomicAdd(&cnt[min(kHistBins - 1, (int)((v[c][j] - vmin) * inv))], 1u);
+  }
+  __syncthreads();
+
+  // 4. Descending scan: offs[b] = number of present scores in bins above b.
+  const int bhi = kHistBins - 1 - 2 * tid, blo = bhi - 1;
+  const uint32_t chi = cnt[bhi], clo = cnt[blo];
+  uint32_t tot;
+  const uint32_t excl = block_excl_scan(chi + clo, red, tot);
+  offs[bhi] = excl;
+  offs[blo] = excl + chi;
+  if (excl < (uint32_t)kk && excl + chi + clo >= (uint32_t)kk) red[kTopkWaves] = (excl + chi >= (uint32_t)kk) ? bhi : blo;
+  // Largest bin at or above b* bounds the rank work; find it after b* is known.
+  __syncthreads();
+  const int bstar = kk > 0 ? (int)red[kTopkWaves] : kHistBins;
+  const uint32_t list_n = kk > 0 ? offs[bstar] + cnt[bstar] : 0;
+  uint32_t bigbin = 0;
+  if (bhi >= bstar) bigbin = max(bigbin, chi);
+  if (blo >= bstar) bigbin = max(bigbin, clo);
+  {
+    uint32_t bm = bigbin;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) bm = max(bm, (uint32_t)__shfl_xor((int)bm, o, kWave));
+    if (lane == 0) red[kTopkWaves + 1 + wave] = bm;
+  }
+  __syncthreads();
+  uint32_t maxbin = 0;
+#pragma unroll
+  for (int w = 0; w < kTopkWaves; ++w) maxbin = max(maxbin, red[kTopkWaves + 1 + w]);
+  if (kk > 0 && (list_n > (uint32_t)kListCap || maxbin > (uint32_t)kBinCap)) {
+    if (tid == 0) oi[0] = kFallbackFlag;
+    return;  // block-uniform
+  }
+
+  // 5. Scatter the bins >= b* into the list, grouped by bin.
+  if (kk > 0) {
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float val = v[c][j];
+        if (val > -1e30f) {
+          const int b = min(kHistBins - 1, (int)((val - vmin) * inv));
+          if (b >= bstar) {
+            const uint32_t pos = offs[b] + atomicAdd(&fill[b], 1u);
+            const int idx = 4 * (tid + c * kTopkThreads) + j;
+            list[pos] = ((uint64_t)float_key(val) << 32) | (uint32_t)(~(uint32_t)idx);
+          }
+        }
+      }
+  }
+  __syncthreads();
+
+  // 6. Rank inside the bin; final position = bin offset + rank.
+  for (uint32_t p = tid; p < list_n; p += kTopkThreads) {
+    const uint64_t e = list[p];
+    const float val = key_to_float((uint32_t)(e >> 32));
+    const int b = min(kHistBins - 1, (int)((val - vmin) * inv));
+    const uint32_t lo = offs[b], nb = cnt[b];
+    uint32_t rank = 0;
+    for (uint32_t j = 0; j < nb; ++j) rank += list[lo + j] > e;
+    const uint32_t pos = lo + rank;
+    if (pos < (uint32_t)kk) {
+      oi[pos] = (int32_t)(~(uint32_t)e);
+      if (ov) ov[pos] = val;
+    }
+  }
+  for (int i = kk + tid; i < k; i += kTopkThreads) {
+    oi[i] = -1;
+    if (ov) ov[i] = -__builtin_huge_valf();
+  }
+}
+
 static int next_pow2(int v) {
   int p = 1;
   while (p < v) p <<= 1;
@@ -221,10 +400,32 @@ static int next_pow2(int v) {
 }
 
 // Launch on `stream`.  Caller has validated shapes (rows, n >= 0; 1 <= k <= 8192).
+template <int kChunks>
+static hipError_t launch_reg(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k, const int32_t* row_len,
+                             int32_t* out_idx, float* out_val, hipStream_t stream) {
+  hipLaunchKernelGGL((topk_reg_kernel<kChunks>), dim3((unsigned)rows), dim3(kTopkThreads), 0, stream, x, ld, (int)n,
+                     (int)k, row_len, out_idx, out_val);
+  return hipGetLastError();
+}
+
+// Launch on `stream`.  Caller has validated shapes (rows, n >= 0; 1 <= k <= 8192).
 hipError_t launch_topk(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k,
                        const int32_t* row_len, int sorted, int32_t* out_idx, float* out_val,
                        hipStream_t stream) {
   if (rows == 0) return hipSuccess;
+  // Fast path for rows that fit in registers; the exact radix kernel then
+  // takes only the rows the fast path flagged (its output is sorted either way).
+  int only_flagged = 0;
+  if (n <= 4 * kTopkThreads * 8 && k <= kListCap) {
+    hipError_t e;
+    if (n <= 4 * kTopkThreads) e = launch_reg<1>(x, ld, rows, n, k, row_len, out_idx, out_val, stream);
+    else if (n <= 8 * kTopkThreads) e = launch_reg<2>(x, ld, rows, n, k, row_len, out_idx, out_val, stream);
+    else if (n <= 16 * kTopkThreads) e = launch_reg<4>(x, ld, rows, n, k, row_len, out_idx, out_val, stream);
+    else e = launch_reg<8>(x, ld, rows, n, k, row_len, out_idx, out_val, stream);
+    if (e != hipSuccess) return e;
+    only_flagged = 1;
+    sorted = 1;
+  }
   const int kpad = sorted ? next_pow2((int)(k < 2 ? 2 : k)) : 0;
   const size_t base = (size_t)(kHistBins + kRedWords) * 4 + (size_t)kpad * 8;
   const size_t cached = base + (size_t)n * 4;
@@ -238,7 +439,7 @@ hipError_t launch_topk(const float* x, int64_t ld, int64_t rows, int64_t n, int6
       attr = true;
     }
     hipLaunchKernelGGL(topk_rows_kernel<true>, grid, block, lds, stream, x, ld, (int)n, (int)k, row_len,
-                       sorted, kpad, out_idx, out_val);
+                       sorted, kpad, out_idx, out_val, only_flagged);
   } else {
     static bool attr = false;
     if (!attr) {
@@ -246,7 +447,7 @@ hipError_t launch_topk(const float* x, int64_t ld, int64_t rows, int64_t n, int6
       attr = true;
     }
     hipLaunchKernelGGL(topk_rows_kernel<false>, grid, block, lds, stream, x, ld, (int)n, (int)k, row_len,
-                       sorted, kpad, out_idx, out_val);
+                       sorted, kpad, out_idx, out_val, only_flagged);
   }
   return hipGetLastError();
 }
