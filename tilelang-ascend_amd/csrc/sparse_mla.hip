@@ -218,20 +218,23 @@ __device__ __forceinline__ void pv_group_mfma(f32x4 (&o)[2][kMlaDV / 16], const 
   }
 }
 
-// O += P V over one tile: 16 pairs of 16-column blocks, the reads of pair k+1
-// in flight while pair k runs on the matrix cores.
+// O += P V over one tile: 16 pairs of 16-column blocks, the reads of pairs
+// k+1 and k+2 in flight while pair k runs on the matrix cores.
 template <bool kF16, int kGrp>
 __device__ __forceinline__ void pv_pipeline(f32x4 (&o)[2][kMlaDV / 16], const u32x4 (&pa)[2], uint32_t vaddr,
-                                            u32x2 (&cur)[4]) {
-  if constexpr (kGrp + 1 < kMlaDV / 32) {
-    u32x2 nxt[4];
-    pv_group_reads<kGrp + 1>(nxt, vaddr);
+                                            u32x2 (&cur)[4], u32x2 (&nxt)[4]) {
+  constexpr int kGroups = kMlaDV / 32;
+  if constexpr (kGrp + 2 < kGroups) {
+    u32x2 n2[4];
+    pv_group_reads<kGrp + 2>(n2, vaddr);
+    lgkm_wait<8>(cur);
+    pv_group_mfma<kF16, kGrp>(o, pa, cur);
+    pv_pipeline<kF16, kGrp + 1>(o, pa, vaddr, nxt, n2);
+  } else if constexpr (kGrp + 1 < kGroups) {
     lgkm_wait<4>(cur);
     pv_group_mfma<kF16, kGrp>(o, pa, cur);
-    pv_pipeline<kF16, kGrp + 1>(o, pa, vaddr, nxt);
-  } else {
-    lgkm_wait<0>(cur);
-    pv_group_mfma<kF16, kGrp>(o, pa, cur);
+    lgkm_wait<0>(nxt);
+    pv_group_mfma<kF16, kGrp + 1>(o, pa, nxt);
   }
 }
 
@@ -246,31 +249,35 @@ __device__ __forceinline__ void lgkm_wait2(u32x4& a, u32x4& b) {
   __asm__ __volatile__("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
 }
 
-// S^T += K Q^T over d = 576: 18 steps of 32 dims; the two K reads of step
-// st + 1 are in flight while step st runs on the matrix cores.  Lane (g, r)
-// reads chunk 4*st + g of slots r and 16 + r: bytes qa + 2048*st (+256).
+// S^T += K Q^T over d = 576: 18 steps of 32 dims; the K reads of steps
+// st + 1 and st + 2 are in flight while step st runs on the matrix cores.
+// Lane (g, r) reads chunk 4*st + g of slots r and 16 + r: bytes qa + 2048*st (+256).
+template <bool kF16, int kSt>
+__device__ __forceinline__ void qk_mfma(f32x4 (&c)[2][2], const u32x4 (&qb)[2][kMlaD / 32], const u32x4& k0,
+                                        const u32x4& k1) {
+#pragma unroll
+  for (int hb = 0; hb < 2; ++hb) {
+    c[hb][0] = mfma16<kF16>(k0, qb[hb][kSt], c[hb][0]);
+    c[hb][1] = mfma16<kF16>(k1, qb[hb][kSt], c[hb][1]);
+  }
+}
+
 template <bool kF16, int kSt>
 __device__ __forceinline__ void qk_pipeline(f32x4 (&c)[2][2], const u32x4 (&qb)[2][kMlaD / 32], uint32_t qa,
-                                            u32x4& k0, u32x4& k1) {
+                                            u32x4& a0, u32x4& a1, u32x4& b0, u32x4& b1) {
   constexpr int kSteps = kMlaD / 32;
-  if constexpr (kSt + 1 < kSteps) {
+  if constexpr (kSt + 2 < kSteps) {
     u32x4 n0, n1;
-    b128_read<2048 * (kSt + 1)>(n0, qa);
-    b128_read<2048 * (kSt + 1) + 256>(n1, qa);
-    lgkm_wait2<2>(k0, k1);
-#pragma unroll
-    for (int hb = 0; hb < 2; ++hb) {
-      c[hb][0] = mfma16<kF16>(k0, qb[hb][kSt], c[hb][0]);
-      c[hb][1] = mfma16<kF16>(k1, qb[hb][kSt], c[hb][1]);
-    }
-    qk_pipeline<kF16, kSt + 1>(c, qb, qa, n0, n1);
-  } else {
-    lgkm_wait2<0>(k0, k1);
-#pragma unroll
-    for (int hb = 0; hb < 2; ++hb) {
-      c[hb][0] = mfma16<kF16>(k0, qb[hb][kSt], c[hb][0]);
-      c[hb][1] = mfma16<kF16>(k1, qb[hb][kSt], c[hb][1]);
-    }
+    b128_read<2048 * (kSt + 2)>(n0, qa);
+    b128_read<2048 * (kSt + 2) + 256>(n1, qa);
+    lgkm_wait2<4>(a0, a1);
+    qk_mfma<kF16, kSt>(c, qb, a0, a1);
+    qk_pipeline<kF16, kSt + 1>(c, qb, qa, b0, b1, n0, n1);
+  } else if constexpr (kSt + 1 < kSteps) {
+    lgkm_wait2<2>(a0, a1);
+    qk_mfma<kF16, kSt>(c, qb, a0, a1);
+    lgkm_wait2<0>(b0, b1);
+    qk_mfma<kF16, kSt + 1>(c, qb, b0, b1);
   }
 }
 
@@ -367,8 +374,8 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   hb_on[0] = head0 < a.H;
   hb_on[1] = head0 + 16 < a.H;
 
-  const int ql = a.q_len ? a.q_len[b] : a.S;
-  const int kl = a.kv_len ? a.kv_len[b] : a.Skv;
+  const int ql = a.q_len ? min(max(a.q_len[b], 0), a.S) : a.S;
+  const int kl = a.kv_len ? min(max(a.kv_len[b], 0), a.Skv) : a.Skv;
   const bool row_active = s < ql;
   const int lim = a.causal ? (kl - ql + s) : 0x7fffffff;
   const int32_t* irow = a.indices + (int64_t)token * a.topk;
@@ -461,14 +468,21 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
     {
       // K rows come through inline-asm LDS reads (see tr_read) with explicit waits.
       const uint32_t qa = lds_u32(buf) + qk_lane;
-      u32x4 k0, k1;
+      u32x4 k0, k1, k2, k3;
       b128_read<0>(k0, qa);
       b128_read<256>(k1, qa);
-      qk_pipeline<kF16, 0>(c, qb, qa, k0, k1);
+      b128_read<2048>(k2, qa);
+      b128_read<2048 + 256>(k3, qa);
+      qk_pipeline<kF16, 0>(c, qb, qa, k0, k1, k2, k3);
     }
     // Lane (g, r) holds keys 4g+i and 16+4g+i of heads head0 + 16*hb + r.
     const i32x4 v0 = *reinterpret_cast<const i32x4*>(rows + tile * kMlaTile + 4 * g);
     const i32x4 v1 = *reinterpret_cast<const i32x4*>(rows + tile * kMlaTile + 16 + 4 * g);
+    // The first V reads do not depend on P: start them under the softmax.
+    const uint32_t va = lds_u32(buf) + pv_lane;
+    u32x2 vg0[4], vg1[4];
+    pv_group_reads<0>(vg0, va);
+    pv_group_reads<1>(vg1, va);
     bool valid[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -507,12 +521,7 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
       lsum[hb] += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
       pa[hb] = u32x4{pack2<kF16>(p[0], p[1]), pack2<kF16>(p[2], p[3]), pack2<kF16>(p[4], p[5]), pack2<kF16>(p[6], p[7])};
     }
-    {
-      const uint32_t va = lds_u32(buf) + pv_lane;
-      u32x2 first[4];
-      pv_group_reads<0>(first, va);
-      pv_pipeline<kF16, 0>(o, pa, va, first);
-    }
+    pv_pipeline<kF16, 0>(o, pa, va, vg0, vg1);
     // All reads of this stage retire before anyone refills it.
     __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
     raw_barrier();

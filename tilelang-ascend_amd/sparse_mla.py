@@ -87,13 +87,10 @@ def sparse_mla_fwd(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tensor, sm_
         skv = kv.shape[1]
     if sm_scale is None:
         sm_scale = D_QK ** -0.5
+    # Lengths stay on the device (no host sync); the kernel clamps them to
+    # [0, S] and [0, Skv] before any address arithmetic.
     ql = _lens(actual_seq_lengths_query, B, dev)
     kl = _lens(actual_seq_lengths_kv, B, dev)
-    # The kernel trusts these bounds for its address arithmetic: check them here.
-    if kl is not None and B > 0 and (int(kl.max().item()) > skv or int(kl.min().item()) < 0):
-        raise ValueError(f"actual_seq_lengths_kv must lie in [0, {skv}]")
-    if ql is not None and B > 0 and (int(ql.max().item()) > S or int(ql.min().item()) < 0):
-        raise ValueError(f"actual_seq_lengths_query must lie in [0, {S}]")
     out = torch.empty((B, S, H, D_V), dtype=q.dtype, device=dev)
     lse = torch.empty((B, S, H), dtype=torch.float32, device=dev)
     lib = _lib.load_library()
