@@ -1,6 +1,6 @@
 """Benchmark of the MI355X DSA path (one GPU).
 
-A step is one sparse-MLA forward over the prefill workload of BASELINE config
+A step is one sparse-MLA forward over the prefill workload
 C4 (B=1, Sq=Skv=16384, H=128, d_qk=576, d_v=512, topk=2048, bf16, causal
 indices with -1 padding), timed with HIP events on the launch stream.  The same
 run also measures the lightning indexer + top-k (config C2: 4096 x 32768, 64
@@ -111,7 +111,7 @@ def cpu_baseline_prefill(torch, q, kv, idx, budget_s=12.0):
     rows = 0
     t0 = time.perf_counter()
     step = 4
-    while time.perf_counter() - t0 < budget_s and rows < 256:
+    while time.perf_counter() - t0 < budget_s and rows + step <= S:
         r1 = S - rows
         r0 = r1 - step
         qs = q[:, r0:r1].cpu()
@@ -160,8 +160,12 @@ def run_step(torch, pkg, dev, args, S, H, topk, sm_scale):
         "config": {"workload": "C4 sparse MLA prefill", "batch": 1, "seq_len_q": S, "seq_len_kv": S, "heads": H,
                    "d_qk": 576, "d_v": 512, "topk": topk, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                     "kernel": "sparse_mla_kernel<4,false>", "flops_per_launch": flops},
+                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                     # HBM bytes per launch from the committed FETCH_SIZE/WRITE_SIZE summary; at H=128 the
+                     # kernel runs one 256-thread workgroup per query token.
+                     "traffic": profiled_traffic(STEP_KERNEL, S * 256),
+                     "traffic_source": "profiles/traffic_fetch_write_bench.txt",
+                     "kernel": STEP_KERNEL, "flops_per_launch": flops},
         "wall_s_timed_region": round(wall, 4),
         "step_ms_p10_p90": [round(sorted(step_ms)[len(step_ms) // 10], 4),
                             round(sorted(step_ms)[(len(step_ms) * 9) // 10], 4)],
@@ -169,8 +173,100 @@ def run_step(torch, pkg, dev, args, S, H, topk, sm_scale):
     return result, (q, kv, idx)
 
 
+PROFILES = ROOT / "profiles"
+STEP_KERNEL = "dsa::sparse_mla_kernel<4, false>"
+COPY_KERNEL = "__amd_rocclr_copyBuffer"
+
+
+def _rocpd(db):
+    import sqlite3
+
+    return sqlite3.connect(f"file:{db}?mode=ro", uri=True)
+
+
+def _kname(name):
+    """Demangled kernel name without the return type and parameter list."""
+    name = name.split("(")[0]
+    return name[5:] if name.startswith("void ") else name
+
+
+def summarize_trace(db):
+    """Per-kernel dispatch statistics from a `rocprofv3 --kernel-trace` rocpd database (durations in us)."""
+    con = _rocpd(db)
+    rows = con.execute("select name, grid_x * grid_y * grid_z, workgroup_x, duration, lds_size, scratch_size, "
+                       "vgpr_count, accum_vgpr_count from kernels").fetchall()
+    agg = {}
+    for name, grid, wg, dur, lds, scr, vg, ag in rows:
+        name = _kname(name)
+        if not name.startswith("dsa::"):
+            continue
+        key = (name, grid, wg)
+        agg.setdefault(key, {"d": [], "meta": (lds, scr, vg, ag)})["d"].append(dur / 1e3)
+    print(f"{'kernel':42s} {'grid':>9s} {'wg':>4s} {'calls':>5s} {'avg_us':>10s} {'min_us':>10s} {'max_us':>10s} "
+          f"lds/scratch/vgpr/agpr")
+    for (name, grid, wg), v in sorted(agg.items(), key=lambda kv: -sum(kv[1]["d"])):
+        d = v["d"]
+        print(f"{name:42s} {grid:9d} {wg:4d} {len(d):5d} {sum(d) / len(d):10.1f} {min(d):10.1f} {max(d):10.1f} "
+              f"{'/'.join(str(x) for x in v['meta'])}")
+
+
+def _counter_means(db, counter):
+    """{(kernel, grid): mean KiB per dispatch} for one byte counter of a `rocprofv3 --pmc` database."""
+    con = _rocpd(db)
+    acc = {}
+    for name, grid, cn, val in con.execute("select kernel_name, grid_size, counter_name, value "
+                                           "from counters_collection"):
+        if cn != counter:
+            continue
+        key = (_kname(name), grid)
+        acc.setdefault(key, []).append(val)
+    return {k: sum(v) / len(v) for k, v in acc.items()}
+
+
+def summarize_traffic(fetch_db, write_db, cal_fetch_db, cal_write_db):
+    """HBM bytes per dispatch of every dsa kernel: FETCH_SIZE and WRITE_SIZE scaled by a copy-kernel calibration.
+
+    The calibration databases hold `bench.py --copy-calibration` (a 1 GiB device copy); the factor per
+    counter is 1 GiB divided by what that counter reports for the copy kernel.
+    """
+    cal_bytes = float(1 << 30)
+    fac = {}
+    for cn, db in (("FETCH_SIZE", cal_fetch_db), ("WRITE_SIZE", cal_write_db)):
+        copies = [v for (n, _g), v in _counter_means(db, cn).items() if n == COPY_KERNEL]
+        if not copies:
+            raise SystemExit(f"no {COPY_KERNEL} dispatch with {cn} in {db}")
+        fac[cn] = cal_bytes / (copies[0] * 1024.0)
+        print(f"calibration {cn}: copy of 1 GiB reads {copies[0]:.1f} KiB -> factor {fac[cn]:.4f}")
+    fetch = _counter_means(fetch_db, "FETCH_SIZE")
+    write = _counter_means(write_db, "WRITE_SIZE")
+    print(f"{'kernel':42s} {'grid':>9s} {'FETCH_KiB':>14s} {'WRITE_KiB':>14s}  traffic_bytes")
+    for key in sorted(set(fetch) & set(write)):
+        if not key[0].startswith("dsa::"):
+            continue
+        tb = fetch[key] * 1024.0 * fac["FETCH_SIZE"] + write[key] * 1024.0 * fac["WRITE_SIZE"]
+        print(f"{key[0]:42s} {key[1]:9d} {fetch[key]:14.1f} {write[key]:14.1f}  {tb:.4e}")
+
+
+def profiled_traffic(kernel, grid):
+    """HBM bytes per launch of (kernel, grid) from the committed counter summary, or None if it has none."""
+    path = PROFILES / "traffic_fetch_write_bench.txt"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        parts = line.rsplit(None, 4)
+        if len(parts) == 5 and parts[0].strip() == kernel and parts[1] == str(grid):
+            return float(parts[4])
+    return None
+
 
 def main():
+    if len(sys.argv) > 1 and sys.argv[1] in ("--rocprof-trace", "--rocprof-traffic"):
+        # Summaries of rocprofv3 databases written by profiling this script (no GPU needed).
+        if sys.argv[1] == "--rocprof-trace":
+            summarize_trace(sys.argv[2])
+        else:
+            summarize_traffic(*sys.argv[2:6])
+        return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)

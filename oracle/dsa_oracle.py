@@ -59,7 +59,7 @@ FP8_MAX = 448.0
 # ----------------------------------------------------------------------------
 # fp8 e4m3 (OCP "fn": no inf, max 448) per-token quantiser.  Not in the
 # reference (its act_quant is int8, deepseek_v4/act_quant.py:33-92); this is the
-# producer BASELINE's fp8 indexer inputs assume.
+# producer of the fp8 indexer inputs (q per tensor, k per token with scale absmax/448).
 # ----------------------------------------------------------------------------
 def fp8_quantize_per_token(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
     """x[..., D] float -> (x_fp8 [..., D] float8_e4m3fn, scale [...] fp32), scale = absmax/448."""

@@ -1,6 +1,6 @@
 """GPU parity of the sparse MLA forward against the CPU oracle.
 
-Tolerance: out within atol = rtol = 2e-2 (bf16), lse within 1e-3.
+Tolerance of the path's parity bar: out within atol = rtol = 2e-2 (bf16), lse within 1e-3.
 """
 import math
 
@@ -26,7 +26,7 @@ def _check(out, lse, ro, rl):
 
 
 def test_config1_parity(dsa, dev):
-    # B=1, Sq=128, Skv=4096, H=16, topk=512.
+    # The CPU-runnable case C1: B=1, Sq=128, Skv=4096, H=16, topk=512.
     q, kv, idx = _inputs(1, 128, 4096, 16, 512, seed=20261201)
     out, lse = dsa.sparse_mla_fwd(q.to(dev), kv.to(dev), idx.to(dev), 1 / math.sqrt(576))
     _check(out, lse, *ref.sparse_mla_fwd(q, kv, idx))
