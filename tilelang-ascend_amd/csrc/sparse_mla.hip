@@ -116,29 +116,48 @@ struct MlaCfg {
   // DMA instructions per tile for wave w: I = w, w + kNW, ... < kTileInstr.
   static constexpr int kMaxPerWave = (kTileInstr + kNW - 1) / kNW;
   static_assert(kTileInstr % kNW == 0, "every wave issues the same number of DMA loads per tile");
-  // Tiles kept in flight: bounded by the 6-bit vmcnt.
-  static constexpr int kDepth = (kAhead * kMaxPerWave < 64) ? kAhead : (63 / kMaxPerWave);
+  // Tiles issued ahead of the one being multiplied by P V.  Iteration t needs
+  // tile t+1 resident (for its Q K^T) and keeps tiles t+2 .. t+kDepth-1 in
+  // flight, so kDepth >= 2; kDepth - 1 tiles of loads must fit the 6-bit vmcnt
+  // and the ring must hold tiles t .. t+kDepth.
+  static constexpr int kDepth = (1 + 63 / kMaxPerWave) < kAhead ? (1 + 63 / kMaxPerWave) : kAhead;
+  static_assert(kDepth >= 2 && kDepth + 1 <= kStages, "DMA ring depth");
 };
 
-// Issue the DMA of tile `tile` (slots tile*32 .. +31 of this workgroup) into `stage_base`.
-// Stage layout, in 16-byte units: chunk c (dims 8c .. 8c+7) of slot r sits at
-// position 32*c + (r ^ 4*(c & 1)).  DMA instruction I fills positions
-// 64*I .. 64*I + 63, i.e. chunks 2I and 2I+1 of all 32 slots, so a lane always
-// serves the same slot (a fixed function of the lane) and only its row base
-// changes per tile.  Empty / masked slots re-load `safe_row` (a valid row of
-// this workgroup; its probability is forced to 0), so every load stays inside
-// the KV cache.
+// Tile layout in a stage.  The tile is 32 slots x 72 16-byte chunks, stored
+// as 36 blocks of 1 KB: block a + 4b holds slots 8a .. 8a+7 x chunks
+// 8b .. 8b+7, with (slot 8a+u, chunk 8b+w) at 16-byte position
+// 8u + (w ^ lds_swizzle(u, a)) of the block.  One DMA instruction fills one
+// block, so its 64 lanes fetch 8 whole 128-byte lines (8 lanes per slot) --
+// a gather of full cache lines -- and the swizzle keeps the Q K^T operand
+// reads (ds_read_b128) and the transposed V reads (ds_read_b64_tr_b16)
+// free of LDS bank conflicts.
+__host__ __device__ constexpr int lds_swizzle(int u, int a) {
+  return ((u & 1) ? 2 : 0) ^ ((u & 2) ? 4 : 0) ^ ((u & 4) ? 1 : 0) ^ ((a & 1) ? 2 : 0);
+}
+
+// Issue the DMA of tile `tile` (slots tile*32 .. +31 of this workgroup) into
+// `stage_base`.  Wave w fills the row groups a = w, w + kNW, ...; lane
+// 8u + v loads chunk 8b + (v ^ lds_swizzle(u, a)) of slot 8a + u, so its row
+// address is fixed per row group and only the chunk-group offset 128*b
+// changes between instructions.  Empty / masked slots re-load `safe_row` (a
+// valid row of this workgroup; its probability is forced to 0), so every
+// load stays inside the KV cache.
 template <int kNW>
 __device__ __forceinline__ void issue_tile(const uint8_t* kv, const int32_t* rows, int safe_row, int tile,
                                            uint8_t* stage_base, int wave, int lane) {
-  const int r = (lane & 31) ^ (4 * ((lane >> 5) & 1));
-  int row = rows[tile * kMlaTile + r];
-  row = row >= 0 ? row : safe_row;
-  const uint8_t* src = kv + (int64_t)row * kRowBytes + 16 * (lane >> 5) + 32 * wave;
+  const int u = lane >> 3;
 #pragma unroll
-  for (int i = 0; i < MlaCfg<kNW>::kMaxPerWave; ++i) {
-    const int I = wave + i * kNW;
-    __builtin_amdgcn_global_load_lds((gbl_void*)(src + 32 * kNW * i), (lds_void*)(stage_base + I * 1024), 16, 0, 0);
+  for (int ag = 0; ag < 4 / kNW; ++ag) {
+    const int a = wave + ag * kNW;
+    int row = rows[tile * kMlaTile + 8 * a + u];
+    row = row >= 0 ? row : safe_row;
+    const uint8_t* src = kv + (int64_t)row * kRowBytes + 16 * ((lane & 7) ^ lds_swizzle(u, a));
+#pragma unroll
+    for (int b = 0; b < kRowChunks / 8; ++b) {
+      __builtin_amdgcn_global_load_lds((gbl_void*)(src + 128 * b), (lds_void*)(stage_base + (a + 4 * b) * 1024), 16,
+                                       0, 0);
+    }
   }
 }
 
@@ -197,15 +216,20 @@ __device__ __forceinline__ void lgkm_wait(u32x2 (&v)[4]) {
   __asm__ __volatile__("s_waitcnt lgkmcnt(%4)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]) : "i"(N));
 }
 
+// The two transposed reads of 16-column block kCb: keys 4g..4g+3 and
+// 16+4g..16+4g+3, at bytes vbase[kCb % 4] + 4096*(kCb / 4) (+2048).
+template <int kCb>
+__device__ __forceinline__ void pv_block_reads(u32x2& lo, u32x2& hi, const uint32_t (&vbase)[4]) {
+  tr_read<4096 * (kCb / 4)>(lo, vbase[kCb % 4]);
+  tr_read<4096 * (kCb / 4) + 2048>(hi, vbase[kCb % 4]);
+}
+
 // The four transposed reads of one pair of 16-column blocks 2*kGrp, 2*kGrp + 1:
-// v[2j], v[2j+1] = keys 4g..4g+3 and 16+4g..16+4g+3 of block 2*kGrp + j, at
-// bytes pa + 1024*cb (+256 for the second key group).
+// v[2j], v[2j+1] = keys 4g..4g+3 and 16+4g..16+4g+3 of block 2*kGrp + j.
 template <int kGrp>
-__device__ __forceinline__ void pv_group_reads(u32x2 (&v)[4], uint32_t pa) {
-  tr_read<1024 * (2 * kGrp)>(v[0], pa);
-  tr_read<1024 * (2 * kGrp) + 256>(v[1], pa);
-  tr_read<1024 * (2 * kGrp + 1)>(v[2], pa);
-  tr_read<1024 * (2 * kGrp + 1) + 256>(v[3], pa);
+__device__ __forceinline__ void pv_group_reads(u32x2 (&v)[4], const uint32_t (&vbase)[4]) {
+  pv_block_reads<2 * kGrp>(v[0], v[1], vbase);
+  pv_block_reads<2 * kGrp + 1>(v[2], v[3], vbase);
 }
 
 template <bool kF16, int kGrp>
@@ -221,8 +245,8 @@ __device__ __forceinline__ void pv_group_mfma(f32x4 (&o)[2][kMlaDV / 16], const 
 // O += P V over one tile: 16 pairs of 16-column blocks, the reads of pairs
 // k+1 and k+2 in flight while pair k runs on the matrix cores.
 template <bool kF16, int kGrp>
-__device__ __forceinline__ void pv_pipeline(f32x4 (&o)[2][kMlaDV / 16], const u32x4 (&pa)[2], uint32_t vaddr,
-                                            u32x2 (&cur)[4], u32x2 (&nxt)[4]) {
+__device__ __forceinline__ void pv_pipeline(f32x4 (&o)[2][kMlaDV / 16], const u32x4 (&pa)[2],
+                                            const uint32_t (&vaddr)[4], u32x2 (&cur)[4], u32x2 (&nxt)[4]) {
   constexpr int kGroups = kMlaDV / 32;
   if constexpr (kGrp + 2 < kGroups) {
     u32x2 n2[4];
@@ -249,9 +273,16 @@ __device__ __forceinline__ void lgkm_wait2(u32x4& a, u32x4& b) {
   __asm__ __volatile__("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
 }
 
+// The K operands of QK step kSt: chunk 4*kSt + g of slots r (lo) and 16 + r
+// (hi), at bytes kbase[kSt % 2] + 4096*(kSt / 2) (+2048).
+template <int kSt>
+__device__ __forceinline__ void qk_step_reads(u32x4& lo, u32x4& hi, const uint32_t (&kbase)[2]) {
+  b128_read<4096 * (kSt / 2)>(lo, kbase[kSt % 2]);
+  b128_read<4096 * (kSt / 2) + 2048>(hi, kbase[kSt % 2]);
+}
+
 // S^T += K Q^T over d = 576: 18 steps of 32 dims; the K reads of steps
 // st + 1 and st + 2 are in flight while step st runs on the matrix cores.
-// Lane (g, r) reads chunk 4*st + g of slots r and 16 + r: bytes qa + 2048*st (+256).
 template <bool kF16, int kSt>
 __device__ __forceinline__ void qk_mfma(f32x4 (&c)[2][2], const u32x4 (&qb)[2][kMlaD / 32], const u32x4& k0,
                                         const u32x4& k1) {
@@ -263,13 +294,12 @@ __device__ __forceinline__ void qk_mfma(f32x4 (&c)[2][2], const u32x4 (&qb)[2][k
 }
 
 template <bool kF16, int kSt>
-__device__ __forceinline__ void qk_pipeline(f32x4 (&c)[2][2], const u32x4 (&qb)[2][kMlaD / 32], uint32_t qa,
-                                            u32x4& a0, u32x4& a1, u32x4& b0, u32x4& b1) {
+__device__ __forceinline__ void qk_pipeline(f32x4 (&c)[2][2], const u32x4 (&qb)[2][kMlaD / 32],
+                                            const uint32_t (&qa)[2], u32x4& a0, u32x4& a1, u32x4& b0, u32x4& b1) {
   constexpr int kSteps = kMlaD / 32;
   if constexpr (kSt + 2 < kSteps) {
     u32x4 n0, n1;
-    b128_read<2048 * (kSt + 2)>(n0, qa);
-    b128_read<2048 * (kSt + 2) + 256>(n1, qa);
+    qk_step_reads<kSt + 2>(n0, n1, qa);
     lgkm_wait2<4>(a0, a1);
     qk_mfma<kF16, kSt>(c, qb, a0, a1);
     qk_pipeline<kF16, kSt + 1>(c, qb, qa, b0, b1, n0, n1);
@@ -279,6 +309,108 @@ __device__ __forceinline__ void qk_pipeline(f32x4 (&c)[2][2], const u32x4 (&qb)[
     lgkm_wait2<0>(b0, b1);
     qk_mfma<kF16, kSt + 1>(c, qb, b0, b1);
   }
+}
+
+// ---------------------------------------------------------------------------
+// S^T(t+1) = K(t+1) Q^T interleaved with O += P(t) V(t), in half-steps.
+//
+// Half-step j reads one K operand (key half j % 2 of QK step j / 2: one
+// ds_read_b128, feeding 2 MFMAs) and one V column block (16 columns: two
+// transposed reads, feeding 2 MFMAs) while the reads of half-steps j+1 .. j+4
+// are in flight.  Q K^T has 36 half-steps and P V 32, so the last four are
+// QK only.  The QK accumulator chains get PV work between their dependent
+// MFMAs, and 12-15 LDS reads stay outstanding (lgkmcnt counts to 15).  LDS
+// reads complete in issue order, so before half-step j's MFMAs the wait
+// count is the number of reads issued after its own.
+constexpr int kQkHalf = 2 * (kMlaD / 32);  // 36
+constexpr int kPvBlocks = kMlaDV / 16;     // 32
+constexpr int kIlAhead = 4;
+
+constexpr int il_reads(int h) { return (h < kQkHalf ? 1 : 0) + (h < kPvBlocks ? 2 : 0); }
+constexpr int il_wait_count(int j) {
+  int n = 0;
+  for (int h = j + 1; h <= j + kIlAhead; ++h) n += il_reads(h);
+  return n;
+}
+constexpr bool il_counts_fit() {
+  for (int j = 0; j < kQkHalf; ++j)
+    if (il_wait_count(j) + il_reads(j) > 15) return false;
+  return true;
+}
+static_assert(il_counts_fit(), "interleaved LDS pipeline keeps at most 15 reads outstanding");
+
+template <int N>
+__device__ __forceinline__ void lgkm_wait_kv(u32x4& k, u32x2& v0, u32x2& v1) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  __asm__ __volatile__("s_waitcnt lgkmcnt(%3)" : "+v"(k), "+v"(v0), "+v"(v1) : "i"(N));
+}
+template <int N>
+__device__ __forceinline__ void lgkm_wait_k(u32x4& k) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  __asm__ __volatile__("s_waitcnt lgkmcnt(%1)" : "+v"(k) : "i"(N));
+}
+
+// The reads of half-step J: K operand, then V column block.
+template <int J>
+__device__ __forceinline__ void il_issue(u32x4& k, u32x2& v0, u32x2& v1, const uint32_t (&qa)[2],
+                                         const uint32_t (&va)[4]) {
+  if constexpr (J < kQkHalf) b128_read<4096 * (J / 4) + 2048 * (J % 2)>(k, qa[(J / 2) % 2]);
+  if constexpr (J < kPvBlocks) pv_block_reads<J>(v0, v1, va);
+}
+
+// Register ring of kIlAhead + 1 half-steps; slot J % 5 holds half-step J.
+template <bool kF16, int J>
+__device__ __forceinline__ void il_step(f32x4 (&c)[2][2], const u32x4 (&qb)[2][kMlaD / 32], const uint32_t (&qa)[2],
+                                        f32x4 (&o)[2][kMlaDV / 16], const u32x4 (&pa)[2], const uint32_t (&va)[4],
+                                        u32x4 (&k)[kIlAhead + 1], u32x2 (&v0)[kIlAhead + 1],
+                                        u32x2 (&v1)[kIlAhead + 1]) {
+  constexpr int kSlotNext = (J + kIlAhead) % (kIlAhead + 1);
+  constexpr int kSlot = J % (kIlAhead + 1);
+  il_issue<J + kIlAhead>(k[kSlotNext], v0[kSlotNext], v1[kSlotNext], qa, va);
+  constexpr int kWait = il_wait_count(J);
+  if constexpr (J < kPvBlocks) {
+    lgkm_wait_kv<kWait>(k[kSlot], v0[kSlot], v1[kSlot]);
+    const u32x4 vb = {v0[kSlot].x, v0[kSlot].y, v1[kSlot].x, v1[kSlot].y};
+    c[0][J % 2] = mfma16<kF16>(k[kSlot], qb[0][J / 2], c[0][J % 2]);
+    o[0][J] = mfma16<kF16>(pa[0], vb, o[0][J]);
+    c[1][J % 2] = mfma16<kF16>(k[kSlot], qb[1][J / 2], c[1][J % 2]);
+    o[1][J] = mfma16<kF16>(pa[1], vb, o[1][J]);
+  } else {
+    lgkm_wait_k<kWait>(k[kSlot]);
+    c[0][J % 2] = mfma16<kF16>(k[kSlot], qb[0][J / 2], c[0][J % 2]);
+    c[1][J % 2] = mfma16<kF16>(k[kSlot], qb[1][J / 2], c[1][J % 2]);
+  }
+  if constexpr (J + 1 < kQkHalf) il_step<kF16, J + 1>(c, qb, qa, o, pa, va, k, v0, v1);
+}
+
+template <bool kF16>
+__device__ __forceinline__ void qk_pv_interleaved(f32x4 (&c)[2][2], const u32x4 (&qb)[2][kMlaD / 32],
+                                                  const uint32_t (&qa)[2], f32x4 (&o)[2][kMlaDV / 16],
+                                                  const u32x4 (&pa)[2], const uint32_t (&va)[4]) {
+  u32x4 k[kIlAhead + 1];
+  u32x2 v0[kIlAhead + 1], v1[kIlAhead + 1];
+  il_issue<0>(k[0], v0[0], v1[0], qa, va);
+  il_issue<1>(k[1], v0[1], v1[1], qa, va);
+  il_issue<2>(k[2], v0[2], v1[2], qa, va);
+  il_issue<3>(k[3], v0[3], v1[3], qa, va);
+  il_step<kF16, 0>(c, qb, qa, o, pa, va, k, v0, v1);
+}
+
+// Q K^T alone (the first tile) and P V alone (the last tile).
+template <bool kF16>
+__device__ __forceinline__ void qk_only(f32x4 (&c)[2][2], const u32x4 (&qb)[2][kMlaD / 32], const uint32_t (&qa)[2]) {
+  u32x4 k0, k1, k2, k3;
+  qk_step_reads<0>(k0, k1, qa);
+  qk_step_reads<1>(k2, k3, qa);
+  qk_pipeline<kF16, 0>(c, qb, qa, k0, k1, k2, k3);
+}
+
+template <bool kF16>
+__device__ __forceinline__ void pv_only(f32x4 (&o)[2][kMlaDV / 16], const u32x4 (&pa)[2], const uint32_t (&va)[4]) {
+  u32x2 vg0[4], vg1[4];
+  pv_group_reads<0>(vg0, va);
+  pv_group_reads<1>(vg1, va);
+  pv_pipeline<kF16, 0>(o, pa, va, vg0, vg1);
 }
 
 __device__ __forceinline__ uint32_t lds_u32(const void* p) {
@@ -428,9 +560,10 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   if (safe_row < 0) ntiles = 0;  // no valid slot: out = 0, lse = -inf
 
   const uint8_t* kvb = reinterpret_cast<const uint8_t*>(a.kv);
-  const int depth = Cfg::kDepth;
+  constexpr int kDepth = Cfg::kDepth;
+  constexpr int kL = Cfg::kMaxPerWave;
 #pragma unroll
-  for (int t = 0; t < Cfg::kDepth; ++t) {
+  for (int t = 0; t < kDepth; ++t) {
     if (t < ntiles) issue_tile<kNW>(kvb, rows, safe_row, t, lds + (t % kStages) * kStageBytes, wave, lane);
   }
 
@@ -444,52 +577,50 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   int32_t* overflow_flag = rows + kSlotsCap;
   bool overflow = false;
 
-  // Per-lane LDS byte offsets in a stage (see issue_tile for the layout).
-  // QK A operand: chunk 4*st + g of slots r, 16 + r -> 512*g + 16*(r ^ 4*(g & 1)) + 2048*st (+256).
-  const uint32_t qk_lane = 512 * g + 16 * (r ^ (4 * (g & 1)));
-  // PV B operand through transposed reads: lane (g, s = r) addresses slot
-  // 4g + (r >> 2) (+16), columns 16*cb + 4*(r & 3), i.e. chunk 2*cb + h with
-  // h = (r >> 1) & 1 -> 512*h + 16*((4g + (r >> 2)) ^ 4h) + 8*(r & 1) + 1024*cb (+256).
-  const int hh = (r >> 1) & 1;
-  const uint32_t pv_lane = 512 * hh + 16 * ((4 * g + (r >> 2)) ^ (4 * hh)) + 8 * (r & 1);
-
-  for (int tile = 0; tile < ntiles; ++tile) {
-    uint8_t* buf = lds + (tile % kStages) * kStageBytes;
-    if (tile + depth < ntiles) {
-      issue_tile<kNW>(kvb, rows, safe_row, tile + depth, lds + ((tile + depth) % kStages) * kStageBytes, wave, lane);
-    }
-    wait_tiles<Cfg::kMaxPerWave>(min(depth, ntiles - 1 - tile));
-    raw_barrier();
-
-    // S^T[key][head] for keys 0-15 (kb 0) and 16-31 (kb 1), both head blocks.
-    f32x4 c[2][2];
+  // Per-lane LDS byte offsets in a stage (layout: see lds_swizzle).
+  // QK A operand of step st: chunk 4*st + g of slots r (+16): slot r is row
+  // u = r & 7 of row group r >> 3, chunk 4*st + g is chunk 4*(st & 1) + g of
+  // chunk group st / 2 -> qk_lane[st & 1] + 4096*(st / 2) (+2048).
+  uint32_t qk_lane[2];
 #pragma unroll
-    for (int hb = 0; hb < 2; ++hb) c[hb][0] = c[hb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    {
-      // K rows come through inline-asm LDS reads (see tr_read) with explicit waits.
-      const uint32_t qa = lds_u32(buf) + qk_lane;
-      u32x4 k0, k1, k2, k3;
-      b128_read<0>(k0, qa);
-      b128_read<256>(k1, qa);
-      b128_read<2048>(k2, qa);
-      b128_read<2048 + 256>(k3, qa);
-      qk_pipeline<kF16, 0>(c, qb, qa, k0, k1, k2, k3);
-    }
-    // Lane (g, r) holds keys 4g+i and 16+4g+i of heads head0 + 16*hb + r.
+  for (int par = 0; par < 2; ++par)
+    qk_lane[par] = 1024 * (r >> 3) + 128 * (r & 7) + 16 * ((4 * par + g) ^ lds_swizzle(r & 7, r >> 3));
+  // PV B operand through transposed reads: lane (g, r) addresses slot
+  // 4g + (r >> 2) (+16), columns 16*cb + 4*(r & 3), i.e. chunk 2*cb + h with
+  // h = (r >> 1) & 1: row u = 4*(g & 1) + (r >> 2) of row group g >> 1, chunk
+  // 2*(cb & 3) + h of chunk group cb / 4 -> pv_lane[cb & 3] + 4096*(cb / 4) (+2048).
+  uint32_t pv_lane[4];
+  {
+    const int u = 4 * (g & 1) + (r >> 2);
+#pragma unroll
+    for (int k4 = 0; k4 < 4; ++k4)
+      pv_lane[k4] = 1024 * (g >> 1) + 128 * u + 16 * ((2 * k4 + ((r >> 1) & 1)) ^ lds_swizzle(u, g >> 1)) + 8 * (r & 1);
+  }
+  auto stage_k = [&](int tile, uint32_t (&out)[2]) {
+    const uint32_t base = lds_u32(lds + (tile % kStages) * kStageBytes);
+    out[0] = base + qk_lane[0];
+    out[1] = base + qk_lane[1];
+  };
+  auto stage_v = [&](int tile, uint32_t (&out)[4]) {
+    const uint32_t base = lds_u32(lds + (tile % kStages) * kStageBytes);
+#pragma unroll
+    for (int k4 = 0; k4 < 4; ++k4) out[k4] = base + pv_lane[k4];
+  };
+
+  // Softmax of one tile's scores (S^T: lane (g, r) holds keys 4g+i and
+  // 16+4g+i of heads head0 + 16*hb + r) into the P operands of O += P V.
+  // (A reference to the kernel argument block would put it in scratch memory:
+  // the lambda captures locals only.)
+  const float scale_log2 = a.scale_log2;
+  auto softmax_tile = [&](const f32x4 (&c)[2][2], int tile, u32x4 (&pa)[2]) {
     const i32x4 v0 = *reinterpret_cast<const i32x4*>(rows + tile * kMlaTile + 4 * g);
     const i32x4 v1 = *reinterpret_cast<const i32x4*>(rows + tile * kMlaTile + 16 + 4 * g);
-    // The first V reads do not depend on P: start them under the softmax.
-    const uint32_t va = lds_u32(buf) + pv_lane;
-    u32x2 vg0[4], vg1[4];
-    pv_group_reads<0>(vg0, va);
-    pv_group_reads<1>(vg1, va);
     bool valid[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       valid[i] = v0[i] >= 0;
       valid[4 + i] = v1[i] >= 0;
     }
-    u32x4 pa[2];
 #pragma unroll
     for (int hb = 0; hb < 2; ++hb) {
       // Raw scores with empty slots at -inf; sm_scale > 0, so the max commutes with it.
@@ -502,7 +633,7 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
       float cmax = fmaxf(fmaxf(fmaxf(cm[0], cm[1]), fmaxf(cm[2], cm[3])), fmaxf(fmaxf(cm[4], cm[5]), fmaxf(cm[6], cm[7])));
       cmax = fmaxf(cmax, __shfl_xor(cmax, 16, kWave));
       cmax = fmaxf(cmax, __shfl_xor(cmax, 32, kWave));
-      const float tmax = cmax * a.scale_log2;
+      const float tmax = cmax * scale_log2;
       // The reference max is fixed by the first tile with a valid score, biased
       // up by 2^kRefBias so later scores may exceed it by 2^(kRefBias +
       // kOverflowGuard) without a rescale of O (scaling by a power of two is
@@ -517,16 +648,53 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
       const float neg_m = (m_ref[hb] == -__builtin_huge_valf()) ? 0.f : -m_ref[hb];
       float p[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) p[i] = fast_exp2(fmaf(cm[i], a.scale_log2, neg_m));
+      for (int i = 0; i < 8; ++i) p[i] = fast_exp2(fmaf(cm[i], scale_log2, neg_m));
       lsum[hb] += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
       pa[hb] = u32x4{pack2<kF16>(p[0], p[1]), pack2<kF16>(p[2], p[3]), pack2<kF16>(p[4], p[5]), pack2<kF16>(p[6], p[7])};
     }
-    pv_pipeline<kF16, 0>(o, pa, va, vg0, vg1);
-    // All reads of this stage retire before anyone refills it.
-    __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
-    raw_barrier();
-  }
+  };
 
+  // Software pipeline over tiles.  Before iteration t, P(t) is known; the
+  // iteration multiplies Q K(t+1)^T while it accumulates P(t) V(t), then
+  // turns S(t+1) into P(t+1).  One barrier per tile: it publishes tile t+1
+  // and certifies that every wave is done with tile t-1, whose stage the DMA
+  // of tile t + kDepth then refills.
+  if (ntiles > 0) {
+    u32x4 pa[2];
+    {
+      wait_tiles<kL>(min(kDepth - 1, ntiles - 1));
+      raw_barrier();
+      f32x4 c[2][2];
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb) c[hb][0] = c[hb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      uint32_t qa[2];
+      stage_k(0, qa);
+      qk_only<kF16>(c, qb, qa);
+      softmax_tile(c, 0, pa);
+    }
+    for (int tile = 0; tile + 1 < ntiles; ++tile) {
+      wait_tiles<kL>(min(kDepth - 2, ntiles - 2 - tile));
+      raw_barrier();
+      if (tile + kDepth < ntiles) {
+        issue_tile<kNW>(kvb, rows, safe_row, tile + kDepth, lds + ((tile + kDepth) % kStages) * kStageBytes, wave,
+                        lane);
+      }
+      f32x4 c[2][2];
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb) c[hb][0] = c[hb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      uint32_t qa[2], va[4];
+      stage_k(tile + 1, qa);
+      stage_v(tile, va);
+      qk_pv_interleaved<kF16>(c, qb, qa, o, pa, va);
+      softmax_tile(c, tile + 1, pa);
+    }
+    // The last tile is resident and published; no DMA targets its stage.
+    uint32_t va[4];
+    stage_v(ntiles - 1, va);
+    pv_only<kF16>(o, pa, va);
+  }
+  // All LDS reads retire before the ring is reused below.
+  __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
   // Any wave whose scores outgrew the biased reference: recompute exactly.
   if (tid == 0) *overflow_flag = 0;
   __syncthreads();
