@@ -52,13 +52,16 @@ constexpr int kStageBytes = kMlaTile * kRowBytes;  // 36864
 constexpr int kTileInstr = kStageBytes / 1024;     // 36 wave-wide 16-byte DMA loads per tile
 constexpr int kSlotsCap = 2048;                    // slots per workgroup (physical rows kept in LDS)
 constexpr int kRowsOffset = kStages * kStageBytes; // 147456
-constexpr int kMlaLds = kRowsOffset + kSlotsCap * 4 + 16;  // rows + overflow flag + first valid slot
+constexpr int kTileMaskOffset = kRowsOffset + kSlotsCap * 4 + 16;  // after rows, overflow flag, first valid slot
+constexpr int kMlaLds = kTileMaskOffset + (kSlotsCap / 32) * 4;       // + one valid-slot bitmask per tile
 // Reference max = first valid tile's max + kRefBias (log2); the fast path accepts
 // P up to 2^kOverflowGuard.  bf16 shares fp32's exponent range; fp16 P must stay
 // within [2^-14, 65504].
 template <bool kF16> struct PRange;
 template <> struct PRange<false> { static constexpr float kRefBias = 60.f, kOverflowGuard = 60.f; };
 template <> struct PRange<true> { static constexpr float kRefBias = 8.f, kOverflowGuard = 15.f; };
+// 2^kOverflowGuard as the bound on a lane's per-tile sum of probabilities.
+template <bool kF16> constexpr float kOverflowSumOf = kF16 ? 32768.f : 1152921504606846976.f;
 constexpr int kHeadsPerWave = 32;                  // two 16-head MFMA blocks share every K / V operand
 
 struct MlaArgs {
@@ -324,7 +327,7 @@ __device__ __forceinline__ void qk_pipeline(f32x4 (&c)[2][2], const u32x4 (&qb)[
 // count is the number of reads issued after its own.
 constexpr int kQkHalf = 2 * (kMlaD / 32);  // 36
 constexpr int kPvBlocks = kMlaDV / 16;     // 32
-constexpr int kIlAhead = 4;
+constexpr int kIlAhead = 3;
 
 constexpr int il_reads(int h) { return (h < kQkHalf ? 1 : 0) + (h < kPvBlocks ? 2 : 0); }
 constexpr int il_wait_count(int j) {
@@ -383,16 +386,25 @@ __device__ __forceinline__ void il_step(f32x4 (&c)[2][2], const u32x4 (&qb)[2][k
   if constexpr (J + 1 < kQkHalf) il_step<kF16, J + 1>(c, qb, qa, o, pa, va, k, v0, v1);
 }
 
+template <int J>
+__device__ __forceinline__ void il_prologue(u32x4 (&k)[kIlAhead + 1], u32x2 (&v0)[kIlAhead + 1],
+                                            u32x2 (&v1)[kIlAhead + 1], const uint32_t (&qa)[2],
+                                            const uint32_t (&va)[4]) {
+  if constexpr (J < kIlAhead) {
+    il_issue<J>(k[J], v0[J], v1[J], qa, va);
+    il_prologue<J + 1>(k, v0, v1, qa, va);
+  }
+}
+
 template <bool kF16>
 __device__ __forceinline__ void qk_pv_interleaved(f32x4 (&c)[2][2], const u32x4 (&qb)[2][kMlaD / 32],
                                                   const uint32_t (&qa)[2], f32x4 (&o)[2][kMlaDV / 16],
                                                   const u32x4 (&pa)[2], const uint32_t (&va)[4]) {
   u32x4 k[kIlAhead + 1];
   u32x2 v0[kIlAhead + 1], v1[kIlAhead + 1];
-  il_issue<0>(k[0], v0[0], v1[0], qa, va);
-  il_issue<1>(k[1], v0[1], v1[1], qa, va);
-  il_issue<2>(k[2], v0[2], v1[2], qa, va);
-  il_issue<3>(k[3], v0[3], v1[3], qa, va);
+  // Exactly the first kIlAhead half-steps: a read issued twice into one slot
+  // would leave an in-flight LDS write to registers the compiler sees as dead.
+  il_prologue<0>(k, v0, v1, qa, va);
   il_step<kF16, 0>(c, qb, qa, o, pa, va, k, v0, v1);
 }
 
@@ -538,7 +550,11 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   int32_t* first_valid = rows + kSlotsCap + 1;
   if (tid == 0) *first_valid = 0x7fffffff;
   __syncthreads();
-  for (int i = tid; i < ntiles * kMlaTile; i += Cfg::kThreads) {
+  // Each wave translates 64 consecutive slots per pass and records, per tile
+  // of 32, the bitmask of its valid slots.
+  uint32_t* tile_mask = reinterpret_cast<uint32_t*>(lds + kTileMaskOffset);
+  for (int i0 = wave * kWave; i0 < ntiles * kMlaTile; i0 += Cfg::kThreads) {
+    const int i = i0 + lane;
     int row = -1;
     if (i < nslots) {
       const int idx = irow[slot_begin + i];
@@ -551,20 +567,32 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
         }
       }
     }
-    rows[i] = row;
+    if (i < ntiles * kMlaTile) rows[i] = row;
     if (row >= 0) atomicMin(first_valid, i);
+    const uint64_t vm = __ballot(row >= 0);
+    if (lane == 0) {
+      tile_mask[i0 / kMlaTile] = (uint32_t)vm;
+      if (i0 / kMlaTile + 1 < ntiles) tile_mask[i0 / kMlaTile + 1] = (uint32_t)(vm >> 32);
+    }
   }
   __syncthreads();
   const int fv = *first_valid;
   const int safe_row = fv < kSlotsCap ? rows[fv] : -1;
-  if (safe_row < 0) ntiles = 0;  // no valid slot: out = 0, lse = -inf
+  const int nslots_all = ntiles * kMlaTile;  // the exact fallback walks every slot
+  if (safe_row < 0) ntiles = 0;              // no valid slot: out = 0, lse = -inf
+  // Tiles before the first valid slot contribute nothing: start at its tile,
+  // which then also fixes the softmax reference.
+  const int t_first = safe_row < 0 ? 0 : fv / kMlaTile;
+  ntiles -= t_first;
+  const int32_t* trows = rows + t_first * kMlaTile;
+  const uint32_t* tmask = tile_mask + t_first;
 
   const uint8_t* kvb = reinterpret_cast<const uint8_t*>(a.kv);
   constexpr int kDepth = Cfg::kDepth;
   constexpr int kL = Cfg::kMaxPerWave;
 #pragma unroll
   for (int t = 0; t < kDepth; ++t) {
-    if (t < ntiles) issue_tile<kNW>(kvb, rows, safe_row, t, lds + (t % kStages) * kStageBytes, wave, lane);
+    if (t < ntiles) issue_tile<kNW>(kvb, trows, safe_row, t, lds + (t % kStages) * kStageBytes, wave, lane);
   }
 
   f32x4 o[2][kMlaDV / 16];
@@ -609,49 +637,63 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
 
   // Softmax of one tile's scores (S^T: lane (g, r) holds keys 4g+i and
   // 16+4g+i of heads head0 + 16*hb + r) into the P operands of O += P V.
+  // The reference max m_ref is fixed by the first tile with a valid slot
+  // (the same tile for every head: validity is per slot), biased up by
+  // 2^kRefBias so later scores may exceed it by 2^(kRefBias + kOverflowGuard)
+  // without a rescale of O (scaling by a power of two is exact; for bf16,
+  // contributions more than 2^66 below the first tile's max underflow,
+  // negligibly).  After that tile no cross-lane maximum is needed: a later
+  // score beyond the headroom makes its probability -- hence the lane's sum of
+  // this tile's probabilities -- exceed 2^kOverflowGuard, which flags the
+  // workgroup for the exact fallback after the loop.
   // (A reference to the kernel argument block would put it in scratch memory:
   // the lambda captures locals only.)
   const float scale_log2 = a.scale_log2;
-  auto softmax_tile = [&](const f32x4 (&c)[2][2], int tile, u32x4 (&pa)[2]) {
-    const i32x4 v0 = *reinterpret_cast<const i32x4*>(rows + tile * kMlaTile + 4 * g);
-    const i32x4 v1 = *reinterpret_cast<const i32x4*>(rows + tile * kMlaTile + 16 + 4 * g);
-    bool valid[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      valid[i] = v0[i] >= 0;
-      valid[4 + i] = v1[i] >= 0;
-    }
+  constexpr float kOverflowSum = kOverflowSumOf<kF16>;
+  static_assert(kOverflowSumOf<false> == 0x1p60f && kOverflowSumOf<true> == 0x1p15f, "2^kOverflowGuard");
+  // P of one tile given its valid-slot mask m (wave-uniform).
+  auto probs = [&](const f32x4 (&c)[2][2], uint32_t m, u32x4 (&pa)[2]) {
 #pragma unroll
     for (int hb = 0; hb < 2; ++hb) {
-      // Raw scores with empty slots at -inf; sm_scale > 0, so the max commutes with it.
-      float cm[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        cm[i] = valid[i] ? c[hb][0][i] : -__builtin_huge_valf();
-        cm[4 + i] = valid[4 + i] ? c[hb][1][i] : -__builtin_huge_valf();
-      }
-      float cmax = fmaxf(fmaxf(fmaxf(cm[0], cm[1]), fmaxf(cm[2], cm[3])), fmaxf(fmaxf(cm[4], cm[5]), fmaxf(cm[6], cm[7])));
-      cmax = fmaxf(cmax, __shfl_xor(cmax, 16, kWave));
-      cmax = fmaxf(cmax, __shfl_xor(cmax, 32, kWave));
-      const float tmax = cmax * scale_log2;
-      // The reference max is fixed by the first tile with a valid score, biased
-      // up by 2^kRefBias so later scores may exceed it by 2^(kRefBias +
-      // kOverflowGuard) without a rescale of O (scaling by a power of two is
-      // exact; for bf16, contributions more than 2^66 below the first tile's
-      // max underflow, negligibly).  A larger jump flags the workgroup for the
-      // exact fallback after the loop.
-      if (m_ref[hb] == -__builtin_huge_valf()) {
-        if (tmax != -__builtin_huge_valf()) m_ref[hb] = tmax + PRange<kF16>::kRefBias;
-      } else if (tmax > m_ref[hb] + PRange<kF16>::kOverflowGuard) {
-        overflow = true;
-      }
-      const float neg_m = (m_ref[hb] == -__builtin_huge_valf()) ? 0.f : -m_ref[hb];
+      const float neg_m = -m_ref[hb];
       float p[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) p[i] = fast_exp2(fmaf(cm[i], scale_log2, neg_m));
-      lsum[hb] += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+      for (int i = 0; i < 4; ++i) {
+        p[i] = fast_exp2(fmaf(c[hb][0][i], scale_log2, neg_m));
+        p[4 + i] = fast_exp2(fmaf(c[hb][1][i], scale_log2, neg_m));
+      }
+      if (m != 0xffffffffu) {  // a partly valid tile (rare): zero the empty slots
+        const uint32_t lane_bits = ((m >> (4 * g)) & 15u) | (((m >> (16 + 4 * g)) & 15u) << 4);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) p[i] = ((lane_bits >> i) & 1u) ? p[i] : 0.f;
+      }
+      const float ps = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+      lsum[hb] += ps;
+      overflow = overflow || !(ps <= kOverflowSum);
       pa[hb] = u32x4{pack2<kF16>(p[0], p[1]), pack2<kF16>(p[2], p[3]), pack2<kF16>(p[4], p[5]), pack2<kF16>(p[6], p[7])};
     }
+  };
+  // The first processed tile holds the first valid slot: it fixes m_ref.
+  auto softmax_first = [&](const f32x4 (&c)[2][2], u32x4 (&pa)[2]) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane(tmask[0]);
+    const uint32_t lane_bits = ((m >> (4 * g)) & 15u) | (((m >> (16 + 4 * g)) & 15u) << 4);
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+      float cmax = -__builtin_huge_valf();
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if ((lane_bits >> i) & 1u) cmax = fmaxf(cmax, c[hb][0][i]);
+        if ((lane_bits >> (4 + i)) & 1u) cmax = fmaxf(cmax, c[hb][1][i]);
+      }
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 16, kWave));
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 32, kWave));
+      // sm_scale > 0, so the max commutes with the scaling.
+      m_ref[hb] = cmax * scale_log2 + PRange<kF16>::kRefBias;
+    }
+    probs(c, m, pa);
+  };
+  auto softmax_next = [&](const f32x4 (&c)[2][2], int tile, u32x4 (&pa)[2]) {
+    probs(c, __builtin_amdgcn_readfirstlane(tmask[tile]), pa);
   };
 
   // Software pipeline over tiles.  Before iteration t, P(t) is known; the
@@ -670,13 +712,13 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
       uint32_t qa[2];
       stage_k(0, qa);
       qk_only<kF16>(c, qb, qa);
-      softmax_tile(c, 0, pa);
+      softmax_first(c, pa);
     }
     for (int tile = 0; tile + 1 < ntiles; ++tile) {
       wait_tiles<kL>(min(kDepth - 2, ntiles - 2 - tile));
       raw_barrier();
       if (tile + kDepth < ntiles) {
-        issue_tile<kNW>(kvb, rows, safe_row, tile + kDepth, lds + ((tile + kDepth) % kStages) * kStageBytes, wave,
+        issue_tile<kNW>(kvb, trows, safe_row, tile + kDepth, lds + ((tile + kDepth) % kStages) * kStageBytes, wave,
                         lane);
       }
       f32x4 c[2][2];
@@ -686,7 +728,7 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
       stage_k(tile + 1, qa);
       stage_v(tile, va);
       qk_pv_interleaved<kF16>(c, qb, qa, o, pa, va);
-      softmax_tile(c, tile + 1, pa);
+      softmax_next(c, tile + 1, pa);
     }
     // The last tile is resident and published; no DMA targets its stage.
     uint32_t va[4];
@@ -705,7 +747,7 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   float* lbase = final_out ? a.lse : a.part_lse + (int64_t)split * T * a.H;
   if (*overflow_flag) {
     mla_exact_fallback<kF16>(a.q, reinterpret_cast<const uint8_t*>(a.kv), obase, lbase, a.H, a.scale_log2, rows,
-                             ntiles * kMlaTile, token, blockIdx.y * (kNW * kHeadsPerWave), kNW * kHeadsPerWave,
+                             nslots_all, token, blockIdx.y * (kNW * kHeadsPerWave), kNW * kHeadsPerWave,
                              reinterpret_cast<float*>(lds), kNW * kWave);
     return;
   }
