@@ -139,30 +139,50 @@ __host__ __device__ constexpr int lds_swizzle(int u, int a) {
   return ((u & 1) ? 2 : 0) ^ ((u & 2) ? 4 : 0) ^ ((u & 4) ? 1 : 0) ^ ((a & 1) ? 2 : 0);
 }
 
-// Issue the DMA of tile `tile` (slots tile*32 .. +31 of this workgroup) into
-// `stage_base`.  Wave w fills the row groups a = w, w + kNW, ...; lane
-// 8u + v loads chunk 8b + (v ^ lds_swizzle(u, a)) of slot 8a + u, so its row
-// address is fixed per row group and only the chunk-group offset 128*b
-// changes between instructions.  Empty / masked slots re-load `safe_row` (a
-// valid row of this workgroup; its probability is forced to 0), so every
-// load stays inside the KV cache.
+// The DMA of tile `tile` (slots tile*32 .. +31 of this workgroup) into a
+// stage.  Wave w fills the row groups a = w, w + kNW, ...; lane 8u + v loads
+// chunk 8b + (v ^ lds_swizzle(u, a)) of slot 8a + u, so its row address is
+// fixed per row group and only the chunk-group offset 128*b changes between
+// instructions.  Empty / masked slots re-load `safe_row` (a valid row of this
+// workgroup; its probability is forced to 0), so every load stays inside the
+// KV cache.
+// The same DMA, split so that its instructions can be spread over the
+// matrix work of an iteration: prepare() computes the lane's row addresses
+// (reading the slot -> row map from LDS), issue<D>() sends instruction D.
+// Sent in one burst, the instructions of the four waves queue behind each
+// other in the memory pipeline and stall the issuing waves.  Past the last
+// tile (`live` false) every lane re-reads `safe_row` into the stage nobody
+// uses any more, which keeps the matrix loop free of branches.
 template <int kNW>
-__device__ __forceinline__ void issue_tile(const uint8_t* kv, const int32_t* rows, int safe_row, int tile,
-                                           uint8_t* stage_base, int wave, int lane) {
-  const int u = lane >> 3;
+struct TileDma {
+  static constexpr int kGroups = 4 / kNW;                    // row groups per wave
+  static constexpr int kCount = kGroups * (kRowChunks / 8);  // instructions per wave and tile
+  const uint8_t* src[kGroups];
+  uint8_t* stage;
+  int wave;
+
+  __device__ __forceinline__ void prepare(const uint8_t* kv, const int32_t* rows, int safe_row, int tile,
+                                          uint8_t* stage_base, int wave_, int lane, bool live) {
+    wave = wave_;
+    stage = stage_base;
+    const int u = lane >> 3;
 #pragma unroll
-  for (int ag = 0; ag < 4 / kNW; ++ag) {
-    const int a = wave + ag * kNW;
-    int row = rows[tile * kMlaTile + 8 * a + u];
-    row = row >= 0 ? row : safe_row;
-    const uint8_t* src = kv + (int64_t)row * kRowBytes + 16 * ((lane & 7) ^ lds_swizzle(u, a));
-#pragma unroll
-    for (int b = 0; b < kRowChunks / 8; ++b) {
-      __builtin_amdgcn_global_load_lds((gbl_void*)(src + 128 * b), (lds_void*)(stage_base + (a + 4 * b) * 1024), 16,
-                                       0, 0);
+    for (int ag = 0; ag < kGroups; ++ag) {
+      const int a = wave + ag * kNW;
+      int row = live ? rows[tile * kMlaTile + 8 * a + u] : -1;
+      row = row >= 0 ? row : safe_row;
+      src[ag] = kv + (int64_t)row * kRowBytes + 16 * ((lane & 7) ^ lds_swizzle(u, a));
     }
   }
-}
+  template <int D>
+  __device__ __forceinline__ void issue() {
+    static_assert(D >= 0 && D < kCount, "DMA instruction index");
+    constexpr int kAg = D / (kRowChunks / 8), kB = D % (kRowChunks / 8);
+    const int a = wave + kAg * kNW;
+    __builtin_amdgcn_global_load_lds((gbl_void*)(src[kAg] + 128 * kB), (lds_void*)(stage + (a + 4 * kB) * 1024), 16,
+                                     0, 0);
+  }
+};
 
 template <bool kF16>
 __device__ __forceinline__ f32x4 mfma16(const u32x4& av, const u32x4& bv, const f32x4& c) {
@@ -362,14 +382,32 @@ __device__ __forceinline__ void il_issue(u32x4& k, u32x2& v0, u32x2& v1, const u
 }
 
 // Register ring of kIlAhead + 1 half-steps; slot J % 5 holds half-step J.
-template <bool kF16, int J>
+template <int kNW, int D = 0>
+__device__ __forceinline__ void il_dma_all(TileDma<kNW>& dma) {
+  if constexpr (D < TileDma<kNW>::kCount) {
+    dma.template issue<D>();
+    il_dma_all<kNW, D + 1>(dma);
+  }
+}
+
+// DMA instructions D with D * kQkHalf / kCount == J go out at half-step J.
+template <int kNW, int J, int D = 0>
+__device__ __forceinline__ void il_dma(TileDma<kNW>& dma) {
+  if constexpr (D < TileDma<kNW>::kCount) {
+    if constexpr (D * kQkHalf / TileDma<kNW>::kCount == J) dma.template issue<D>();
+    il_dma<kNW, J, D + 1>(dma);
+  }
+}
+
+template <bool kF16, int kNW, int J>
 __device__ __forceinline__ void il_step(f32x4 (&c)[2][2], const u32x4 (&qb)[2][kMlaD / 32], const uint32_t (&qa)[2],
                                         f32x4 (&o)[2][kMlaDV / 16], const u32x4 (&pa)[2], const uint32_t (&va)[4],
                                         u32x4 (&k)[kIlAhead + 1], u32x2 (&v0)[kIlAhead + 1],
-                                        u32x2 (&v1)[kIlAhead + 1]) {
+                                        u32x2 (&v1)[kIlAhead + 1], TileDma<kNW>& dma) {
   constexpr int kSlotNext = (J + kIlAhead) % (kIlAhead + 1);
   constexpr int kSlot = J % (kIlAhead + 1);
   il_issue<J + kIlAhead>(k[kSlotNext], v0[kSlotNext], v1[kSlotNext], qa, va);
+  il_dma<kNW, J>(dma);
   constexpr int kWait = il_wait_count(J);
   if constexpr (J < kPvBlocks) {
     lgkm_wait_kv<kWait>(k[kSlot], v0[kSlot], v1[kSlot]);
@@ -383,7 +421,7 @@ __device__ __forceinline__ void il_step(f32x4 (&c)[2][2], const u32x4 (&qb)[2][k
     c[0][J % 2] = mfma16<kF16>(k[kSlot], qb[0][J / 2], c[0][J % 2]);
     c[1][J % 2] = mfma16<kF16>(k[kSlot], qb[1][J / 2], c[1][J % 2]);
   }
-  if constexpr (J + 1 < kQkHalf) il_step<kF16, J + 1>(c, qb, qa, o, pa, va, k, v0, v1);
+  if constexpr (J + 1 < kQkHalf) il_step<kF16, kNW, J + 1>(c, qb, qa, o, pa, va, k, v0, v1, dma);
 }
 
 template <int J>
@@ -396,16 +434,16 @@ __device__ __forceinline__ void il_prologue(u32x4 (&k)[kIlAhead + 1], u32x2 (&v0
   }
 }
 
-template <bool kF16>
+template <bool kF16, int kNW>
 __device__ __forceinline__ void qk_pv_interleaved(f32x4 (&c)[2][2], const u32x4 (&qb)[2][kMlaD / 32],
                                                   const uint32_t (&qa)[2], f32x4 (&o)[2][kMlaDV / 16],
-                                                  const u32x4 (&pa)[2], const uint32_t (&va)[4]) {
+                                                  const u32x4 (&pa)[2], const uint32_t (&va)[4], TileDma<kNW>& dma) {
   u32x4 k[kIlAhead + 1];
   u32x2 v0[kIlAhead + 1], v1[kIlAhead + 1];
   // Exactly the first kIlAhead half-steps: a read issued twice into one slot
   // would leave an in-flight LDS write to registers the compiler sees as dead.
   il_prologue<0>(k, v0, v1, qa, va);
-  il_step<kF16, 0>(c, qb, qa, o, pa, va, k, v0, v1);
+  il_step<kF16, kNW, 0>(c, qb, qa, o, pa, va, k, v0, v1, dma);
 }
 
 // Q K^T alone (the first tile) and P V alone (the last tile).
@@ -424,6 +462,117 @@ __device__ __forceinline__ void pv_only(f32x4 (&o)[2][kMlaDV / 16], const u32x4 
   pv_group_reads<1>(vg1, va);
   pv_pipeline<kF16, 0>(o, pa, va, vg0, vg1);
 }
+
+// ---------------------------------------------------------------------------
+// Phase A of an iteration: S^T(t+1) = K(t+1) Q^T in half-steps.  Half-step J
+// reads one K operand (key half J % 2 of 32-dim step J / 2, one
+// ds_read_b128) and runs its 2 MFMAs (both head blocks).  Even and odd dim
+// steps accumulate into separate sets, so eight independent MFMA chains are in
+// flight, and kQkAhead reads stay outstanding.  The DMA of a future tile is
+// spread over the half-steps.
+constexpr int kQkAhead = 6;
+
+template <bool kF16, int kNW, bool kDma, int J>
+__device__ __forceinline__ void qk_half(f32x4 (&c)[2][2][2], const u32x4 (&qb)[2][kMlaD / 32],
+                                        const uint32_t (&qa)[2], u32x4 (&k)[kQkAhead + 1], TileDma<kNW>& dma) {
+  constexpr int kNext = J + kQkAhead;
+  if constexpr (kNext < kQkHalf) {
+    b128_read<4096 * (kNext / 4) + 2048 * (kNext % 2)>(k[kNext % (kQkAhead + 1)], qa[(kNext / 2) % 2]);
+  }
+  if constexpr (kDma) il_dma<kNW, J>(dma);
+  constexpr int kWait = (kQkHalf - 1 - J) < kQkAhead ? (kQkHalf - 1 - J) : kQkAhead;
+  constexpr int kSlot = J % (kQkAhead + 1);
+  lgkm_wait_k<kWait>(k[kSlot]);
+  constexpr int kSet = (J / 2) % 2, kKb = J % 2, kSt = J / 2;
+  c[kSet][0][kKb] = mfma16<kF16>(k[kSlot], qb[0][kSt], c[kSet][0][kKb]);
+  c[kSet][1][kKb] = mfma16<kF16>(k[kSlot], qb[1][kSt], c[kSet][1][kKb]);
+  if constexpr (J + 1 < kQkHalf) qk_half<kF16, kNW, kDma, J + 1>(c, qb, qa, k, dma);
+}
+
+template <int J>
+__device__ __forceinline__ void qk_prologue(u32x4 (&k)[kQkAhead + 1], const uint32_t (&qa)[2]) {
+  if constexpr (J < kQkAhead) {
+    b128_read<4096 * (J / 4) + 2048 * (J % 2)>(k[J], qa[(J / 2) % 2]);
+    qk_prologue<J + 1>(k, qa);
+  }
+}
+
+template <bool kF16, int kNW, bool kDma>
+__device__ __forceinline__ void qk_phase(f32x4 (&s)[2][2], const u32x4 (&qb)[2][kMlaD / 32],
+                                         const uint32_t (&qa)[2], TileDma<kNW>& dma) {
+  f32x4 c[2][2][2];
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) c[st][hb][0] = c[st][hb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  u32x4 k[kQkAhead + 1];
+  qk_prologue<0>(k, qa);
+  qk_half<kF16, kNW, kDma, 0>(c, qb, qa, k, dma);
+#pragma unroll
+  for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) s[hb][kb] = c[0][hb][kb] + c[1][hb][kb];
+}
+
+// Phase B: O += P(t) V(t) while the softmax of tile t+1 turns its scores into
+// P(t+1).  The softmax is cut into slices run between the MFMA groups of the
+// P V pipeline, so its VALU work overlaps the matrix cores.  Lane (g, r)
+// holds scores of keys 4g+i (kb 0) and 16+4g+i (kb 1) of heads head0 + 16*hb
+// + r; scores of empty slots were set to -inf beforehand.
+template <bool kF16>
+struct SoftmaxSlices {
+  static constexpr int kSlices = 10;  // per head block: 4 x (2 exponentials), 1 x (sum, pack)
+  const f32x4 (&c)[2][2];
+  u32x4 (&pa)[2];
+  float (&lsum)[2];
+  bool& overflow;
+  float neg_m[2];
+  float scale;
+  float p[2][8];
+
+  template <int kS>
+  __device__ __forceinline__ void run() {
+    if constexpr (kS < kSlices) {
+      constexpr int kHb = kS / 5, kPart = kS % 5;
+      if constexpr (kPart < 4) {
+#pragma unroll
+        for (int e = 2 * kPart; e < 2 * kPart + 2; ++e) {
+          p[kHb][e] = fast_exp2(fmaf(c[kHb][e / 4][e % 4], scale, neg_m[kHb]));
+        }
+      } else {
+        const float* q = p[kHb];
+        const float ps = ((q[0] + q[1]) + (q[2] + q[3])) + ((q[4] + q[5]) + (q[6] + q[7]));
+        lsum[kHb] += ps;
+        overflow = overflow || !(ps <= kOverflowSumOf<kF16>);
+        pa[kHb] = u32x4{pack2<kF16>(q[0], q[1]), pack2<kF16>(q[2], q[3]), pack2<kF16>(q[4], q[5]),
+                        pack2<kF16>(q[6], q[7])};
+      }
+    }
+  }
+};
+
+template <bool kF16, int kGrp>
+__device__ __forceinline__ void pv_softmax_pipeline(f32x4 (&o)[2][kMlaDV / 16], const u32x4 (&pa)[2],
+                                                    const uint32_t (&vaddr)[4], u32x2 (&cur)[4], u32x2 (&nxt)[4],
+                                                    SoftmaxSlices<kF16>& sm) {
+  constexpr int kGroups = kMlaDV / 32;
+  if constexpr (kGrp + 2 < kGroups) {
+    u32x2 n2[4];
+    pv_group_reads<kGrp + 2>(n2, vaddr);
+    sm.template run<kGrp>();
+    lgkm_wait<8>(cur);
+    pv_group_mfma<kF16, kGrp>(o, pa, cur);
+    pv_softmax_pipeline<kF16, kGrp + 1>(o, pa, vaddr, nxt, n2, sm);
+  } else if constexpr (kGrp + 1 < kGroups) {
+    sm.template run<kGrp>();
+    lgkm_wait<4>(cur);
+    pv_group_mfma<kF16, kGrp>(o, pa, cur);
+    sm.template run<kGrp + 1>();
+    lgkm_wait<0>(nxt);
+    pv_group_mfma<kF16, kGrp + 1>(o, pa, nxt);
+  }
+}
+static_assert(SoftmaxSlices<false>::kSlices <= kMlaDV / 32, "every softmax slice has a P V group");
 
 __device__ __forceinline__ uint32_t lds_u32(const void* p) {
   return (uint32_t)(uintptr_t)(const lds_void*)p;
@@ -590,9 +739,15 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   const uint8_t* kvb = reinterpret_cast<const uint8_t*>(a.kv);
   constexpr int kDepth = Cfg::kDepth;
   constexpr int kL = Cfg::kMaxPerWave;
+  // Every tile index below ntiles + kDepth gets a DMA (a dummy one past the
+  // end), so each iteration waits for a fixed number of outstanding tiles.
+  if (ntiles > 0) {
 #pragma unroll
-  for (int t = 0; t < kDepth; ++t) {
-    if (t < ntiles) issue_tile<kNW>(kvb, trows, safe_row, t, lds + (t % kStages) * kStageBytes, wave, lane);
+    for (int t = 0; t < kDepth; ++t) {
+      TileDma<kNW> dma;
+      dma.prepare(kvb, trows, safe_row, t, lds + (t % kStages) * kStageBytes, wave, lane, t < ntiles);
+      il_dma_all(dma);
+    }
   }
 
   f32x4 o[2][kMlaDV / 16];
@@ -649,94 +804,89 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   // (A reference to the kernel argument block would put it in scratch memory:
   // the lambda captures locals only.)
   const float scale_log2 = a.scale_log2;
-  constexpr float kOverflowSum = kOverflowSumOf<kF16>;
-  static_assert(kOverflowSumOf<false> == 0x1p60f && kOverflowSumOf<true> == 0x1p15f, "2^kOverflowGuard");
-  // P of one tile given its valid-slot mask m (wave-uniform).
-  auto probs = [&](const f32x4 (&c)[2][2], uint32_t m, u32x4 (&pa)[2]) {
+  // Scores of empty slots -> -inf (a partly valid tile is rare: uniform branch).
+  auto mask_scores = [&](f32x4 (&c)[2][2], uint32_t m) {
+    if (m != 0xffffffffu) {
+      const uint32_t lane_bits = ((m >> (4 * g)) & 15u) | (((m >> (16 + 4 * g)) & 15u) << 4);
 #pragma unroll
-    for (int hb = 0; hb < 2; ++hb) {
-      const float neg_m = -m_ref[hb];
-      float p[8];
+      for (int e = 0; e < 8; ++e) {
+        const bool v = (lane_bits >> e) & 1u;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        p[i] = fast_exp2(fmaf(c[hb][0][i], scale_log2, neg_m));
-        p[4 + i] = fast_exp2(fmaf(c[hb][1][i], scale_log2, neg_m));
+        for (int hb = 0; hb < 2; ++hb) c[hb][e / 4][e % 4] = v ? c[hb][e / 4][e % 4] : -__builtin_huge_valf();
       }
-      if (m != 0xffffffffu) {  // a partly valid tile (rare): zero the empty slots
-        const uint32_t lane_bits = ((m >> (4 * g)) & 15u) | (((m >> (16 + 4 * g)) & 15u) << 4);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) p[i] = ((lane_bits >> i) & 1u) ? p[i] : 0.f;
-      }
-      const float ps = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
-      lsum[hb] += ps;
-      overflow = overflow || !(ps <= kOverflowSum);
-      pa[hb] = u32x4{pack2<kF16>(p[0], p[1]), pack2<kF16>(p[2], p[3]), pack2<kF16>(p[4], p[5]), pack2<kF16>(p[6], p[7])};
     }
-  };
-  // The first processed tile holds the first valid slot: it fixes m_ref.
-  auto softmax_first = [&](const f32x4 (&c)[2][2], u32x4 (&pa)[2]) {
-    const uint32_t m = __builtin_amdgcn_readfirstlane(tmask[0]);
-    const uint32_t lane_bits = ((m >> (4 * g)) & 15u) | (((m >> (16 + 4 * g)) & 15u) << 4);
-#pragma unroll
-    for (int hb = 0; hb < 2; ++hb) {
-      float cmax = -__builtin_huge_valf();
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if ((lane_bits >> i) & 1u) cmax = fmaxf(cmax, c[hb][0][i]);
-        if ((lane_bits >> (4 + i)) & 1u) cmax = fmaxf(cmax, c[hb][1][i]);
-      }
-      cmax = fmaxf(cmax, __shfl_xor(cmax, 16, kWave));
-      cmax = fmaxf(cmax, __shfl_xor(cmax, 32, kWave));
-      // sm_scale > 0, so the max commutes with the scaling.
-      m_ref[hb] = cmax * scale_log2 + PRange<kF16>::kRefBias;
-    }
-    probs(c, m, pa);
-  };
-  auto softmax_next = [&](const f32x4 (&c)[2][2], int tile, u32x4 (&pa)[2]) {
-    probs(c, __builtin_amdgcn_readfirstlane(tmask[tile]), pa);
   };
 
-  // Software pipeline over tiles.  Before iteration t, P(t) is known; the
-  // iteration multiplies Q K(t+1)^T while it accumulates P(t) V(t), then
-  // turns S(t+1) into P(t+1).  One barrier per tile: it publishes tile t+1
-  // and certifies that every wave is done with tile t-1, whose stage the DMA
-  // of tile t + kDepth then refills.
+  // Software pipeline over tiles.  Before iteration t, P(t) is known.  The
+  // iteration computes S(t+1) = Q K(t+1)^T (phase A, with the DMA of tile
+  // t + kDepth spread over it), then accumulates O += P(t) V(t) while the
+  // softmax turns S(t+1) into P(t+1) (phase B).  One barrier per tile: it
+  // publishes tile t+1 and certifies that every wave is done with tile t-1,
+  // whose stage the DMA of tile t + kDepth then refills.
   if (ntiles > 0) {
     u32x4 pa[2];
     {
-      wait_tiles<kL>(min(kDepth - 1, ntiles - 1));
+      wait_tiles<kL>(kDepth - 1);
       raw_barrier();
       f32x4 c[2][2];
-#pragma unroll
-      for (int hb = 0; hb < 2; ++hb) c[hb][0] = c[hb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
       uint32_t qa[2];
       stage_k(0, qa);
-      qk_only<kF16>(c, qb, qa);
-      softmax_first(c, pa);
+      TileDma<kNW> none;
+      qk_phase<kF16, kNW, false>(c, qb, qa, none);
+      mask_scores(c, __builtin_amdgcn_readfirstlane(tmask[0]));
+      // The first processed tile holds the first valid slot: it fixes m_ref.
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb) {
+        float cmax = -__builtin_huge_valf();
+#pragma unroll
+        for (int e = 0; e < 8; ++e) cmax = fmaxf(cmax, c[hb][e / 4][e % 4]);
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 16, kWave));
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 32, kWave));
+        // sm_scale > 0, so the max commutes with the scaling.
+        m_ref[hb] = cmax * scale_log2 + PRange<kF16>::kRefBias;
+      }
+      SoftmaxSlices<kF16> sm{c, pa, lsum, overflow, {-m_ref[0], -m_ref[1]}, scale_log2, {}};
+      sm.template run<0>();
+      sm.template run<1>();
+      sm.template run<2>();
+      sm.template run<3>();
+      sm.template run<4>();
+      sm.template run<5>();
+      sm.template run<6>();
+      sm.template run<7>();
+      sm.template run<8>();
+      sm.template run<9>();
     }
     for (int tile = 0; tile + 1 < ntiles; ++tile) {
-      wait_tiles<kL>(min(kDepth - 2, ntiles - 2 - tile));
+      wait_tiles<kL>(kDepth - 2);
       raw_barrier();
-      if (tile + kDepth < ntiles) {
-        issue_tile<kNW>(kvb, trows, safe_row, tile + kDepth, lds + ((tile + kDepth) % kStages) * kStageBytes, wave,
-                        lane);
-      }
+      // The DMA of tile + kDepth (into the stage tile - 1 left) goes out
+      // spread over phase A.
+      TileDma<kNW> dma;
+      dma.prepare(kvb, trows, safe_row, tile + kDepth, lds + ((tile + kDepth) % kStages) * kStageBytes, wave, lane,
+                  tile + kDepth < ntiles);
       f32x4 c[2][2];
-#pragma unroll
-      for (int hb = 0; hb < 2; ++hb) c[hb][0] = c[hb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
       uint32_t qa[2], va[4];
       stage_k(tile + 1, qa);
       stage_v(tile, va);
-      qk_pv_interleaved<kF16>(c, qb, qa, o, pa, va);
-      softmax_next(c, tile + 1, pa);
+      qk_phase<kF16, kNW, true>(c, qb, qa, dma);
+      mask_scores(c, __builtin_amdgcn_readfirstlane(tmask[tile + 1]));
+      u32x4 pa_next[2];
+      SoftmaxSlices<kF16> sm{c, pa_next, lsum, overflow, {-m_ref[0], -m_ref[1]}, scale_log2, {}};
+      u32x2 vg0[4], vg1[4];
+      pv_group_reads<0>(vg0, va);
+      pv_group_reads<1>(vg1, va);
+      pv_softmax_pipeline<kF16, 0>(o, pa, va, vg0, vg1, sm);
+      pa[0] = pa_next[0];
+      pa[1] = pa_next[1];
     }
     // The last tile is resident and published; no DMA targets its stage.
     uint32_t va[4];
     stage_v(ntiles - 1, va);
     pv_only<kF16>(o, pa, va);
   }
-  // All LDS reads retire before the ring is reused below.
-  __builtin_amdgcn_s_waitcnt((15) | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
+  // All LDS reads and the trailing dummy DMAs retire before the ring is reused below.
+  __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
   // Any wave whose scores outgrew the biased reference: recompute exactly.
   if (tid == 0) *overflow_flag = 0;
   __syncthreads();
