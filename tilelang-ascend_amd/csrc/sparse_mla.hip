@@ -239,29 +239,33 @@ __device__ __forceinline__ void lgkm_wait(u32x2 (&v)[4]) {
   __asm__ __volatile__("s_waitcnt lgkmcnt(%4)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]) : "i"(N));
 }
 
-// The two transposed reads of 16-column block kCb: keys 4g..4g+3 and
-// 16+4g..16+4g+3, at bytes vbase[kCb % 4] + 4096*(kCb / 4) (+2048).
+// The two transposed reads of V block kCb (keys 4g..4g+3 and 16+4g..16+4g+3):
+// block 2p + h holds columns 32p + 8m' + 4h + i for MFMA row 4m' + i, read at
+// bytes vbase[p % 2] + 4096*(p / 2) + 8h (+2048).
 template <int kCb>
-__device__ __forceinline__ void pv_block_reads(u32x2& lo, u32x2& hi, const uint32_t (&vbase)[4]) {
-  tr_read<4096 * (kCb / 4)>(lo, vbase[kCb % 4]);
-  tr_read<4096 * (kCb / 4) + 2048>(hi, vbase[kCb % 4]);
+__device__ __forceinline__ void pv_block_reads(u32x2& lo, u32x2& hi, const uint32_t (&vbase)[2]) {
+  constexpr int kP = kCb / 2, kH = kCb % 2;
+  tr_read<4096 * (kP / 2) + 8 * kH>(lo, vbase[kP % 2]);
+  tr_read<4096 * (kP / 2) + 8 * kH + 2048>(hi, vbase[kP % 2]);
 }
 
-// The four transposed reads of one pair of 16-column blocks 2*kGrp, 2*kGrp + 1:
+// The four transposed reads of one pair of V blocks 2*kGrp, 2*kGrp + 1:
 // v[2j], v[2j+1] = keys 4g..4g+3 and 16+4g..16+4g+3 of block 2*kGrp + j.
 template <int kGrp>
-__device__ __forceinline__ void pv_group_reads(u32x2 (&v)[4], const uint32_t (&vbase)[4]) {
+__device__ __forceinline__ void pv_group_reads(u32x2 (&v)[4], const uint32_t (&vbase)[2]) {
   pv_block_reads<2 * kGrp>(v[0], v[1], vbase);
   pv_block_reads<2 * kGrp + 1>(v[2], v[3], vbase);
 }
 
+// O^T += V^T P^T: V^T is the A operand, P the B operand, so lane (g, r) of
+// block 2p + h accumulates head r, columns 32p + 8g + 4h .. +3.
 template <bool kF16, int kGrp>
 __device__ __forceinline__ void pv_group_mfma(f32x4 (&o)[2][kMlaDV / 16], const u32x4 (&pa)[2], const u32x2 (&v)[4]) {
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const u32x4 vb = {v[2 * j].x, v[2 * j].y, v[2 * j + 1].x, v[2 * j + 1].y};
-    o[0][2 * kGrp + j] = mfma16<kF16>(pa[0], vb, o[0][2 * kGrp + j]);
-    o[1][2 * kGrp + j] = mfma16<kF16>(pa[1], vb, o[1][2 * kGrp + j]);
+    o[0][2 * kGrp + j] = mfma16<kF16>(vb, pa[0], o[0][2 * kGrp + j]);
+    o[1][2 * kGrp + j] = mfma16<kF16>(vb, pa[1], o[1][2 * kGrp + j]);
   }
 }
 
@@ -269,7 +273,7 @@ __device__ __forceinline__ void pv_group_mfma(f32x4 (&o)[2][kMlaDV / 16], const 
 // k+1 and k+2 in flight while pair k runs on the matrix cores.
 template <bool kF16, int kGrp>
 __device__ __forceinline__ void pv_pipeline(f32x4 (&o)[2][kMlaDV / 16], const u32x4 (&pa)[2],
-                                            const uint32_t (&vaddr)[4], u32x2 (&cur)[4], u32x2 (&nxt)[4]) {
+                                            const uint32_t (&vaddr)[2], u32x2 (&cur)[4], u32x2 (&nxt)[4]) {
   constexpr int kGroups = kMlaDV / 32;
   if constexpr (kGrp + 2 < kGroups) {
     u32x2 n2[4];
@@ -334,54 +338,14 @@ __device__ __forceinline__ void qk_pipeline(f32x4 (&c)[2][2], const u32x4 (&qb)[
   }
 }
 
-// ---------------------------------------------------------------------------
-// S^T(t+1) = K(t+1) Q^T interleaved with O += P(t) V(t), in half-steps.
-//
-// Half-step j reads one K operand (key half j % 2 of QK step j / 2: one
-// ds_read_b128, feeding 2 MFMAs) and one V column block (16 columns: two
-// transposed reads, feeding 2 MFMAs) while the reads of half-steps j+1 .. j+4
-// are in flight.  Q K^T has 36 half-steps and P V 32, so the last four are
-// QK only.  The QK accumulator chains get PV work between their dependent
-// MFMAs, and 12-15 LDS reads stay outstanding (lgkmcnt counts to 15).  LDS
-// reads complete in issue order, so before half-step j's MFMAs the wait
-// count is the number of reads issued after its own.
-constexpr int kQkHalf = 2 * (kMlaD / 32);  // 36
-constexpr int kPvBlocks = kMlaDV / 16;     // 32
-constexpr int kIlAhead = 3;
+constexpr int kQkHalf = 2 * (kMlaD / 32);  // 36 half-steps of Q K^T
 
-constexpr int il_reads(int h) { return (h < kQkHalf ? 1 : 0) + (h < kPvBlocks ? 2 : 0); }
-constexpr int il_wait_count(int j) {
-  int n = 0;
-  for (int h = j + 1; h <= j + kIlAhead; ++h) n += il_reads(h);
-  return n;
-}
-constexpr bool il_counts_fit() {
-  for (int j = 0; j < kQkHalf; ++j)
-    if (il_wait_count(j) + il_reads(j) > 15) return false;
-  return true;
-}
-static_assert(il_counts_fit(), "interleaved LDS pipeline keeps at most 15 reads outstanding");
-
-template <int N>
-__device__ __forceinline__ void lgkm_wait_kv(u32x4& k, u32x2& v0, u32x2& v1) {
-  static_assert(N >= 0 && N < 16, "lgkmcnt range");
-  __asm__ __volatile__("s_waitcnt lgkmcnt(%3)" : "+v"(k), "+v"(v0), "+v"(v1) : "i"(N));
-}
 template <int N>
 __device__ __forceinline__ void lgkm_wait_k(u32x4& k) {
   static_assert(N >= 0 && N < 16, "lgkmcnt range");
   __asm__ __volatile__("s_waitcnt lgkmcnt(%1)" : "+v"(k) : "i"(N));
 }
 
-// The reads of half-step J: K operand, then V column block.
-template <int J>
-__device__ __forceinline__ void il_issue(u32x4& k, u32x2& v0, u32x2& v1, const uint32_t (&qa)[2],
-                                         const uint32_t (&va)[4]) {
-  if constexpr (J < kQkHalf) b128_read<4096 * (J / 4) + 2048 * (J % 2)>(k, qa[(J / 2) % 2]);
-  if constexpr (J < kPvBlocks) pv_block_reads<J>(v0, v1, va);
-}
-
-// Register ring of kIlAhead + 1 half-steps; slot J % 5 holds half-step J.
 template <int kNW, int D = 0>
 __device__ __forceinline__ void il_dma_all(TileDma<kNW>& dma) {
   if constexpr (D < TileDma<kNW>::kCount) {
@@ -399,64 +363,9 @@ __device__ __forceinline__ void il_dma(TileDma<kNW>& dma) {
   }
 }
 
-template <bool kF16, int kNW, int J>
-__device__ __forceinline__ void il_step(f32x4 (&c)[2][2], const u32x4 (&qb)[2][kMlaD / 32], const uint32_t (&qa)[2],
-                                        f32x4 (&o)[2][kMlaDV / 16], const u32x4 (&pa)[2], const uint32_t (&va)[4],
-                                        u32x4 (&k)[kIlAhead + 1], u32x2 (&v0)[kIlAhead + 1],
-                                        u32x2 (&v1)[kIlAhead + 1], TileDma<kNW>& dma) {
-  constexpr int kSlotNext = (J + kIlAhead) % (kIlAhead + 1);
-  constexpr int kSlot = J % (kIlAhead + 1);
-  il_issue<J + kIlAhead>(k[kSlotNext], v0[kSlotNext], v1[kSlotNext], qa, va);
-  il_dma<kNW, J>(dma);
-  constexpr int kWait = il_wait_count(J);
-  if constexpr (J < kPvBlocks) {
-    lgkm_wait_kv<kWait>(k[kSlot], v0[kSlot], v1[kSlot]);
-    const u32x4 vb = {v0[kSlot].x, v0[kSlot].y, v1[kSlot].x, v1[kSlot].y};
-    c[0][J % 2] = mfma16<kF16>(k[kSlot], qb[0][J / 2], c[0][J % 2]);
-    o[0][J] = mfma16<kF16>(pa[0], vb, o[0][J]);
-    c[1][J % 2] = mfma16<kF16>(k[kSlot], qb[1][J / 2], c[1][J % 2]);
-    o[1][J] = mfma16<kF16>(pa[1], vb, o[1][J]);
-  } else {
-    lgkm_wait_k<kWait>(k[kSlot]);
-    c[0][J % 2] = mfma16<kF16>(k[kSlot], qb[0][J / 2], c[0][J % 2]);
-    c[1][J % 2] = mfma16<kF16>(k[kSlot], qb[1][J / 2], c[1][J % 2]);
-  }
-  if constexpr (J + 1 < kQkHalf) il_step<kF16, kNW, J + 1>(c, qb, qa, o, pa, va, k, v0, v1, dma);
-}
-
-template <int J>
-__device__ __forceinline__ void il_prologue(u32x4 (&k)[kIlAhead + 1], u32x2 (&v0)[kIlAhead + 1],
-                                            u32x2 (&v1)[kIlAhead + 1], const uint32_t (&qa)[2],
-                                            const uint32_t (&va)[4]) {
-  if constexpr (J < kIlAhead) {
-    il_issue<J>(k[J], v0[J], v1[J], qa, va);
-    il_prologue<J + 1>(k, v0, v1, qa, va);
-  }
-}
-
-template <bool kF16, int kNW>
-__device__ __forceinline__ void qk_pv_interleaved(f32x4 (&c)[2][2], const u32x4 (&qb)[2][kMlaD / 32],
-                                                  const uint32_t (&qa)[2], f32x4 (&o)[2][kMlaDV / 16],
-                                                  const u32x4 (&pa)[2], const uint32_t (&va)[4], TileDma<kNW>& dma) {
-  u32x4 k[kIlAhead + 1];
-  u32x2 v0[kIlAhead + 1], v1[kIlAhead + 1];
-  // Exactly the first kIlAhead half-steps: a read issued twice into one slot
-  // would leave an in-flight LDS write to registers the compiler sees as dead.
-  il_prologue<0>(k, v0, v1, qa, va);
-  il_step<kF16, kNW, 0>(c, qb, qa, o, pa, va, k, v0, v1, dma);
-}
-
-// Q K^T alone (the first tile) and P V alone (the last tile).
+// P V alone (the last tile).
 template <bool kF16>
-__device__ __forceinline__ void qk_only(f32x4 (&c)[2][2], const u32x4 (&qb)[2][kMlaD / 32], const uint32_t (&qa)[2]) {
-  u32x4 k0, k1, k2, k3;
-  qk_step_reads<0>(k0, k1, qa);
-  qk_step_reads<1>(k2, k3, qa);
-  qk_pipeline<kF16, 0>(c, qb, qa, k0, k1, k2, k3);
-}
-
-template <bool kF16>
-__device__ __forceinline__ void pv_only(f32x4 (&o)[2][kMlaDV / 16], const u32x4 (&pa)[2], const uint32_t (&va)[4]) {
+__device__ __forceinline__ void pv_only(f32x4 (&o)[2][kMlaDV / 16], const u32x4 (&pa)[2], const uint32_t (&va)[2]) {
   u32x2 vg0[4], vg1[4];
   pv_group_reads<0>(vg0, va);
   pv_group_reads<1>(vg1, va);
@@ -553,7 +462,7 @@ struct SoftmaxSlices {
 
 template <bool kF16, int kGrp>
 __device__ __forceinline__ void pv_softmax_pipeline(f32x4 (&o)[2][kMlaDV / 16], const u32x4 (&pa)[2],
-                                                    const uint32_t (&vaddr)[4], u32x2 (&cur)[4], u32x2 (&nxt)[4],
+                                                    const uint32_t (&vaddr)[2], u32x2 (&cur)[4], u32x2 (&nxt)[4],
                                                     SoftmaxSlices<kF16>& sm) {
   constexpr int kGroups = kMlaDV / 32;
   if constexpr (kGrp + 2 < kGroups) {
@@ -652,7 +561,7 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   int32_t* rows = reinterpret_cast<int32_t*>(lds + kRowsOffset);
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
-  const int wave = tid / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform
   const int r = lane & 15;
   const int g = lane >> 4;
 
@@ -667,63 +576,102 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   hb_on[0] = head0 < a.H;
   hb_on[1] = head0 + 16 < a.H;
 
-  const int ql = a.q_len ? min(max(a.q_len[b], 0), a.S) : a.S;
-  const int kl = a.kv_len ? min(max(a.kv_len[b], 0), a.Skv) : a.Skv;
-  const bool row_active = s < ql;
-  const int lim = a.causal ? (kl - ql + s) : 0x7fffffff;
+  // The prologue is a chain of global-memory latencies; it is ordered so
+  // they overlap: the lengths and this lane's slot indices go out first, the
+  // Q rows (the largest load) right behind them (a compiler barrier keeps
+  // that order), and the block-table lookups as soon as the indices are back.
   const int32_t* irow = a.indices + (int64_t)token * a.topk;
   const int slot_begin = split * a.keys_per_split;
   const int slot_end = min(a.topk, slot_begin + a.keys_per_split);
   const int nslots = slot_end > slot_begin ? slot_end - slot_begin : 0;
-  int ntiles = row_active ? (nslots + kMlaTile - 1) / kMlaTile : 0;
+  // Every load below is issued unconditionally, from a clamped valid address
+  // (its value is discarded later if out of range): conditional loads would
+  // make the compiler wait for them on the spot.
+  constexpr int kIdxPerLane = kSlotsCap / (kNW * kWave);  // slot indices a lane may translate
+  const int last_slot = max(min(slot_end, a.topk) - 1, 0);
+  int idx_raw[kIdxPerLane];
+#pragma unroll
+  for (int j = 0; j < kIdxPerLane; ++j) {
+    const int i = wave * kWave + j * Cfg::kThreads + lane;
+    idx_raw[j] = irow[min(slot_begin + i, last_slot)];
+  }
+  // Per-sequence lengths through the scalar cache (wave-uniform).
+  typedef const __attribute__((address_space(4))) int32_t const_i32;
+  const int ql_raw = a.q_len ? *(const_i32*)(a.q_len + b) : a.S;
+  const int kl_raw = a.kv_len ? *(const_i32*)(a.kv_len + b) : a.Skv;
+  __asm__ __volatile__("" ::: "memory");
 
   // Q operands (B of S^T = K Q^T): head head0 + 16*hb + r, dims 32*st + 8*g .. +8.
   u32x4 qb[2][kMlaD / 32];
 #pragma unroll
   for (int hb = 0; hb < 2; ++hb) {
-    const uint16_t* qp = a.q + ((int64_t)token * a.H + head0 + 16 * hb + r) * kMlaD + 8 * g;
-    const bool on = hb_on[hb] && row_active;
+    const int h = min(head0 + 16 * hb + r, a.H - 1);
+    const uint16_t* qp = a.q + ((int64_t)token * a.H + h) * kMlaD + 8 * g;
 #pragma unroll
-    for (int st = 0; st < kMlaD / 32; ++st) {
-      qb[hb][st] = on ? *reinterpret_cast<const u32x4*>(qp + 32 * st) : u32x4{0, 0, 0, 0};
-    }
+    for (int st = 0; st < kMlaD / 32; ++st) qb[hb][st] = *reinterpret_cast<const u32x4*>(qp + 32 * st);
   }
-  // Q must be resident before the DMA ring starts: vmcnt then only counts DMA.
+  const int ql = min(max(ql_raw, 0), a.S);
+  const int kl = min(max(kl_raw, 0), a.Skv);
+  const bool row_active = s < ql;
+  const int lim = a.causal ? (kl - ql + s) : 0x7fffffff;
+  int ntiles = row_active ? (nslots + kMlaTile - 1) / kMlaTile : 0;
+
+  // Slots -> physical rows (-1: empty or masked); the lowest valid slot's row
+  // doubles as the DMA source of the empty ones.
+  int row_of[kIdxPerLane];
+  bool ok[kIdxPerLane];
+#pragma unroll
+  for (int j = 0; j < kIdxPerLane; ++j) {
+    const int i = wave * kWave + j * Cfg::kThreads + lane;
+    const int idx = idx_raw[j];
+    ok[j] = i < nslots && idx >= 0 && idx < kl && idx <= lim;
+  }
+  if (a.block_table) {
+    // All lookups first (from a clamped valid entry), then the translation.
+    int blk[kIdxPerLane];
+    const int32_t* bt = a.block_table + (int64_t)b * a.max_blocks;
+#pragma unroll
+    for (int j = 0; j < kIdxPerLane; ++j) blk[j] = bt[ok[j] ? idx_raw[j] / a.block_size : 0];
+#pragma unroll
+    for (int j = 0; j < kIdxPerLane; ++j) row_of[j] = ok[j] ? blk[j] * a.block_size + idx_raw[j] % a.block_size : -1;
+  } else {
+#pragma unroll
+    for (int j = 0; j < kIdxPerLane; ++j) row_of[j] = ok[j] ? b * a.Skv + idx_raw[j] : -1;
+  }
+  // Q and the block-table lookups must be resident before the DMA ring
+  // starts: vmcnt then only counts DMA.
   wait_vmcnt<0>();
 #pragma unroll
   for (int hb = 0; hb < 2; ++hb)
 #pragma unroll
-    for (int st = 0; st < kMlaD / 32; ++st) __asm__ __volatile__("" : "+v"(qb[hb][st]));
-  // Slots -> physical rows (-1: empty or masked); the lowest valid slot's row
-  // doubles as the DMA source of the empty ones.
+    for (int st = 0; st < kMlaD / 32; ++st) {
+      if (!hb_on[hb]) qb[hb][st] = u32x4{0, 0, 0, 0};  // heads past H (wave-uniform)
+      __asm__ __volatile__("" : "+v"(qb[hb][st]));
+    }
+#pragma unroll
+  for (int j = 0; j < kIdxPerLane; ++j) __asm__ __volatile__("" : "+v"(row_of[j]));
   int32_t* first_valid = rows + kSlotsCap + 1;
   if (tid == 0) *first_valid = 0x7fffffff;
   __syncthreads();
-  // Each wave translates 64 consecutive slots per pass and records, per tile
-  // of 32, the bitmask of its valid slots.
+  // Each wave wrote 64 consecutive slots per pass; record, per tile of 32,
+  // the bitmask of its valid slots.
   uint32_t* tile_mask = reinterpret_cast<uint32_t*>(lds + kTileMaskOffset);
-  for (int i0 = wave * kWave; i0 < ntiles * kMlaTile; i0 += Cfg::kThreads) {
+  int wave_first = 0x7fffffff;  // lowest valid slot this wave saw (wave-uniform)
+#pragma unroll
+  for (int j = 0; j < kIdxPerLane; ++j) {
+    const int i0 = wave * kWave + j * Cfg::kThreads;
     const int i = i0 + lane;
-    int row = -1;
-    if (i < nslots) {
-      const int idx = irow[slot_begin + i];
-      if (idx >= 0 && idx < kl && idx <= lim) {
-        if (a.block_table) {
-          const int blk = a.block_table[(int64_t)b * a.max_blocks + idx / a.block_size];
-          row = blk * a.block_size + idx % a.block_size;
-        } else {
-          row = b * a.Skv + idx;
-        }
-      }
-    }
+    const int row = row_active ? row_of[j] : -1;
     if (i < ntiles * kMlaTile) rows[i] = row;
-    if (row >= 0) atomicMin(first_valid, i);
-    const uint64_t vm = __ballot(row >= 0);
-    if (lane == 0) {
+    const uint64_t vm = __ballot(row >= 0 && i < ntiles * kMlaTile);
+    if (vm != 0) wave_first = min(wave_first, i0 + (int)__builtin_ctzll(vm));
+    if (lane == 0 && i0 < ntiles * kMlaTile) {
       tile_mask[i0 / kMlaTile] = (uint32_t)vm;
       if (i0 / kMlaTile + 1 < ntiles) tile_mask[i0 / kMlaTile + 1] = (uint32_t)(vm >> 32);
     }
   }
+  // One LDS atomic per wave (one per valid slot would serialise hundreds).
+  if (lane == 0 && wave_first != 0x7fffffff) atomicMin(first_valid, wave_first);
   __syncthreads();
   const int fv = *first_valid;
   const int safe_row = fv < kSlotsCap ? rows[fv] : -1;
@@ -768,26 +716,27 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
 #pragma unroll
   for (int par = 0; par < 2; ++par)
     qk_lane[par] = 1024 * (r >> 3) + 128 * (r & 7) + 16 * ((4 * par + g) ^ lds_swizzle(r & 7, r >> 3));
-  // PV B operand through transposed reads: lane (g, r) addresses slot
-  // 4g + (r >> 2) (+16), columns 16*cb + 4*(r & 3), i.e. chunk 2*cb + h with
-  // h = (r >> 1) & 1: row u = 4*(g & 1) + (r >> 2) of row group g >> 1, chunk
-  // 2*(cb & 3) + h of chunk group cb / 4 -> pv_lane[cb & 3] + 4096*(cb / 4) (+2048).
-  uint32_t pv_lane[4];
+  // V^T operand of block 2p + h through transposed reads: lane (g, r)
+  // addresses slot 4g + (r >> 2) (+16), columns 32p + 8*(r & 3) + 4h .. +3,
+  // i.e. chunk 4p + (r & 3), byte 8h: row u = 4*(g & 1) + (r >> 2) of row
+  // group g >> 1, chunk 4*(p & 1) + (r & 3) of chunk group p / 2
+  // -> pv_lane[p & 1] + 4096*(p / 2) + 8h (+2048).
+  uint32_t pv_lane[2];
   {
     const int u = 4 * (g & 1) + (r >> 2);
 #pragma unroll
-    for (int k4 = 0; k4 < 4; ++k4)
-      pv_lane[k4] = 1024 * (g >> 1) + 128 * u + 16 * ((2 * k4 + ((r >> 1) & 1)) ^ lds_swizzle(u, g >> 1)) + 8 * (r & 1);
+    for (int par = 0; par < 2; ++par)
+      pv_lane[par] = 1024 * (g >> 1) + 128 * u + 16 * ((4 * par + (r & 3)) ^ lds_swizzle(u, g >> 1));
   }
   auto stage_k = [&](int tile, uint32_t (&out)[2]) {
     const uint32_t base = lds_u32(lds + (tile % kStages) * kStageBytes);
     out[0] = base + qk_lane[0];
     out[1] = base + qk_lane[1];
   };
-  auto stage_v = [&](int tile, uint32_t (&out)[4]) {
+  auto stage_v = [&](int tile, uint32_t (&out)[2]) {
     const uint32_t base = lds_u32(lds + (tile % kStages) * kStageBytes);
-#pragma unroll
-    for (int k4 = 0; k4 < 4; ++k4) out[k4] = base + pv_lane[k4];
+    out[0] = base + pv_lane[0];
+    out[1] = base + pv_lane[1];
   };
 
   // Softmax of one tile's scores (S^T: lane (g, r) holds keys 4g+i and
@@ -866,7 +815,7 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
       dma.prepare(kvb, trows, safe_row, tile + kDepth, lds + ((tile + kDepth) % kStages) * kStageBytes, wave, lane,
                   tile + kDepth < ntiles);
       f32x4 c[2][2];
-      uint32_t qa[2], va[4];
+      uint32_t qa[2], va[2];
       stage_k(tile + 1, qa);
       stage_v(tile, va);
       qk_phase<kF16, kNW, true>(c, qb, qa, dma);
@@ -881,7 +830,7 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
       pa[1] = pa_next[1];
     }
     // The last tile is resident and published; no DMA targets its stage.
-    uint32_t va[4];
+    uint32_t va[2];
     stage_v(ntiles - 1, va);
     pv_only<kF16>(o, pa, va);
   }
@@ -902,38 +851,31 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
     return;
   }
 
-  // Epilogue: normalise, write out (or the split partial) and the LSE.
-  __syncthreads();  // the ring is free: reuse it to stage the output rows
-  uint16_t* stage = reinterpret_cast<uint16_t*>(lds) + wave * kHeadsPerWave * (kMlaDV + 8);
+  // Epilogue: normalise, write out (or the split partial) and the LSE.  Lane
+  // (g, r) holds, for head 16*hb + r, columns 32p + 8g .. 32p + 8g + 7 in
+  // blocks 2p and 2p + 1: normalised, they go out as one 16-byte store each.
 #pragma unroll
   for (int hb = 0; hb < 2; ++hb) {
     float l_tot = lsum[hb];
     l_tot += __shfl_xor(l_tot, 16, kWave);
     l_tot += __shfl_xor(l_tot, 32, kWave);
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    float inv_i[4];
+    const int h = head0 + 16 * hb + r;
+    if (hb_on[hb]) {
+      uint16_t* orow = obase + ((int64_t)token * a.H + h) * kMlaDV + 8 * g;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) inv_i[i] = __shfl(inv, 4 * g + i, kWave);
-#pragma unroll
-    for (int cb = 0; cb < kMlaDV / 16; ++cb) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        stage[(16 * hb + 4 * g + i) * (kMlaDV + 8) + 16 * cb + r] = cvt1<kF16>(o[hb][cb][i] * inv_i[i]);
+      for (int p2 = 0; p2 < kMlaDV / 32; ++p2) {
+        const f32x4& x = o[hb][2 * p2];
+        const f32x4& y = o[hb][2 * p2 + 1];
+        const u32x4 v = {pack2<kF16>(x[0] * inv, x[1] * inv), pack2<kF16>(x[2] * inv, x[3] * inv),
+                         pack2<kF16>(y[0] * inv, y[1] * inv), pack2<kF16>(y[2] * inv, y[3] * inv)};
+        *reinterpret_cast<u32x4*>(orow + 32 * p2) = v;
+      }
+      if (g == 0) {
+        lbase[(int64_t)token * a.H + h] =
+            l_tot > 0.f ? (m_ref[hb] + fast_log2(l_tot)) * 0.69314718055994531f : -__builtin_huge_valf();
+      }
     }
-    if (hb_on[hb] && g == 0) {
-      const float lse = l_tot > 0.f ? (m_ref[hb] + fast_log2(l_tot)) * 0.69314718055994531f : -__builtin_huge_valf();
-      lbase[(int64_t)token * a.H + head0 + 16 * hb + r] = lse;
-    }
-  }
-  __syncthreads();
-  uint16_t* orow = obase + ((int64_t)token * a.H + head0) * kMlaDV;
-#pragma unroll
-  for (int it = 0; it < kHeadsPerWave * kMlaDV / 8 / kWave; ++it) {
-    const int e = lane + it * kWave;  // 16-byte chunk: head e / 64, cols 8*(e % 64)
-    const int h = e >> 6;
-    const int c = (e & 63) * 8;
-    if (head0 + h < a.H)
-      *reinterpret_cast<u32x4*>(orow + h * kMlaDV + c) = *reinterpret_cast<const u32x4*>(stage + h * (kMlaDV + 8) + c);
   }
 }
 
