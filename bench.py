@@ -173,6 +173,124 @@ def run_step(torch, pkg, dev, args, S, H, topk, sm_scale):
     return result, (q, kv, idx)
 
 
+def run_c5(torch, pkg, dev, args, flush, ctx=131072, chunk=4096, H=128, topk=2048, dec_b=32):
+    """C5: one sequence of 128K keys; a prefill chunk of 4096 queries at its tail runs indexer -> top-k ->
+    sparse MLA on the indexer's own selection; then a decode step of 32 sequences (one query each, 128K keys
+    each, paged 64-token blocks) through the same three kernels."""
+    from tilelang_ascend_amd import _lib as L
+
+    lib = pkg.load_library()
+    stream = L.stream_handle(dev)
+    _log("C5 inputs")
+    g = torch.Generator(device=dev).manual_seed(20261205)
+    Hi, D = 64, 128
+    qi = torch.randn(1, chunk, Hi, D, generator=g, device=dev).to(torch.float8_e4m3fn)
+    kf = torch.randn(1, ctx, D, generator=g, device=dev)
+    ks = (kf.abs().amax(dim=-1) / 448.0).to(torch.float32)
+    ki = (kf / ks.unsqueeze(-1)).clamp(-448, 448).to(torch.float8_e4m3fn).contiguous()
+    del kf
+    wi = torch.randn(1, chunk, Hi, generator=g, device=dev) / 8
+    logits = torch.empty(chunk, ctx, dtype=torch.float32, device=dev)
+    idx = torch.empty(1, chunk, 1, topk, dtype=torch.int32, device=dev)
+    q = (torch.randn(1, chunk, H, 576, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    kv = (torch.randn(1, ctx, 1, 576, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    out = torch.empty(1, chunk, H, 512, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(1, chunk, H, dtype=torch.float32, device=dev)
+    ws_b = lib.dsa_sparse_mla_workspace_size(1, chunk, H, topk)
+    ws = torch.empty(max(ws_b, 1), dtype=torch.uint8, device=dev)
+    sm = 576 ** -0.5
+
+    def run_idx():
+        L.check(lib.dsa_indexer_logits(L.KIND_FP8_E4M3, qi.data_ptr(), ki.data_ptr(), ks.data_ptr(), wi.data_ptr(), 1,
+                                       chunk, ctx, Hi, D, None, None, None, 0, 0, 3, logits.data_ptr(), ctx, stream),
+                "c5 indexer")
+
+    tws_b = lib.dsa_topk_select_workspace_size(chunk, ctx, topk)
+    tws = torch.empty(max(tws_b, 1), dtype=torch.uint8, device=dev)
+
+    def run_topk():
+        L.check(lib.dsa_topk_select_ws(logits.data_ptr(), ctx, chunk, ctx, topk, None, 1, idx.data_ptr(), None,
+                                       tws.data_ptr(), tws_b, stream), "c5 topk")
+
+    def run_mla():
+        L.check(lib.dsa_sparse_mla_fwd(L.KIND_BF16, q.data_ptr(), kv.data_ptr(), idx.data_ptr(), None, None, None, 1,
+                                       chunk, H, 576, 512, ctx, 0, 0, topk, sm, 1, out.data_ptr(), lse.data_ptr(),
+                                       ws.data_ptr(), ws_b, stream), "c5 mla")
+
+    for f in (run_idx, run_topk, run_mla):
+        f()
+    torch.cuda.synchronize()
+    reps = max(3, args.reps // 2)
+    t_idx = _median(_timed(torch, run_idx, reps, flush))
+    t_topk = _median(_timed(torch, run_topk, reps, flush))
+    t_mla = _median(_timed(torch, run_mla, reps, flush))
+    pairs = sum(min(ctx, ctx - chunk + t + 1) for t in range(chunk))
+    idx_flops = 2.0 * Hi * D * chunk * ctx
+    mla_flops = 2.0 * H * topk * (576 + 512) * chunk
+    topk_bytes = chunk * ctx * 4 + chunk * topk * 4
+    roof_us = (idx_flops / (PEAK_FP8_TFLOPS * 1e12) + topk_bytes / (PEAK_HBM_GBS * 1e9)) * 1e6
+    del qi, ki, wi, logits, q, kv, out, lse, ws, tws
+
+    # Decode step: 32 sequences x 1 query, 128K keys each, paged KV (64-token blocks).
+    _log("C5 decode inputs")
+    bs = 64
+    nblk = ctx // bs
+    qd = torch.randn(dec_b, 1, Hi, D, generator=g, device=dev).to(torch.float8_e4m3fn)
+    kdf = torch.randn(dec_b * nblk, bs, D, generator=g, device=dev)
+    kds = (kdf.abs().amax(dim=-1) / 448.0).to(torch.float32)
+    kd = (kdf / kds.unsqueeze(-1)).clamp(-448, 448).to(torch.float8_e4m3fn).contiguous()
+    del kdf
+    wd = torch.randn(dec_b, 1, Hi, generator=g, device=dev) / 8
+    table = torch.randperm(dec_b * nblk, generator=g, device=dev).view(dec_b, nblk).to(torch.int32)
+    lens_q = torch.ones(dec_b, dtype=torch.int32, device=dev)
+    lens_k = torch.full((dec_b,), ctx, dtype=torch.int32, device=dev)
+    dlog = torch.empty(dec_b, 1, ctx, dtype=torch.float32, device=dev)
+    didx = torch.empty(dec_b, 1, 1, topk, dtype=torch.int32, device=dev)
+    qm = (torch.randn(dec_b, 1, H, 576, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    pool = (torch.randn(dec_b * nblk, bs, 1, 576, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    dout = torch.empty(dec_b, 1, H, 512, dtype=torch.bfloat16, device=dev)
+    dlse = torch.empty(dec_b, 1, H, dtype=torch.float32, device=dev)
+    dws_b = lib.dsa_sparse_mla_workspace_size(dec_b, 1, H, topk)
+    dws = torch.empty(max(dws_b, 1), dtype=torch.uint8, device=dev)
+
+    dtws_b = lib.dsa_topk_select_workspace_size(dec_b, ctx, topk)
+    dtws = torch.empty(max(dtws_b, 1), dtype=torch.uint8, device=dev)
+
+    def run_decode():
+        L.check(lib.dsa_indexer_logits(L.KIND_FP8_E4M3, qd.data_ptr(), kd.data_ptr(), kds.data_ptr(), wd.data_ptr(),
+                                       dec_b, 1, ctx, Hi, D, lens_q.data_ptr(), lens_k.data_ptr(), table.data_ptr(),
+                                       bs, nblk, 3, dlog.data_ptr(), ctx, stream), "c5 decode indexer")
+        L.check(lib.dsa_topk_select_ws(dlog.data_ptr(), ctx, dec_b, ctx, topk, None, 1, didx.data_ptr(), None,
+                                       dtws.data_ptr(), dtws_b, stream), "c5 decode topk")
+        L.check(lib.dsa_sparse_mla_fwd(L.KIND_BF16, qm.data_ptr(), pool.data_ptr(), didx.data_ptr(), table.data_ptr(),
+                                       lens_q.data_ptr(), lens_k.data_ptr(), dec_b, 1, H, 576, 512, ctx, bs, nblk,
+                                       topk, sm, 1, dout.data_ptr(), dlse.data_ptr(), dws.data_ptr(), dws_b, stream),
+                "c5 decode mla")
+
+    run_decode()
+    torch.cuda.synchronize()
+    t_dec = _median(_timed(torch, run_decode, reps, flush))
+    dec_bytes = dec_b * (ctx * (D + 4) + topk * 576 * 2 + H * 576 * 2 + H * 512 * 2) + dec_b * ctx * 4 * 2
+    _log(f"C5: indexer {t_idx * 1e3:.1f} us, topk {t_topk * 1e3:.1f} us, mla {t_mla * 1e3:.1f} us, "
+         f"decode chain {t_dec * 1e3:.1f} us")
+    del qd, kd, kds, wd, table, dlog, didx, qm, pool, dout, dlse, dws, dtws
+    return {
+        "workload": "C5: 4096-query chunk at the tail of a 128K context (fp8 indexer 64x128 -> top-2048 -> sparse "
+                    "MLA H=128 on that selection), plus a decode step of 32 sequences x 128K keys",
+        "indexer_us": round(t_idx * 1e3, 1),
+        "topk_us": round(t_topk * 1e3, 1),
+        "indexer_topk_us": round((t_idx + t_topk) * 1e3, 1),
+        "indexer_topk_roofline_us": round(roof_us, 1),
+        "indexer_topk_frac_roofline": round(roof_us / ((t_idx + t_topk) * 1e3), 4),
+        "indexer_tflops_dense": round(idx_flops / (t_idx * 1e-3) / 1e12, 1),
+        "indexer_causal_pair_frac": round(pairs / (chunk * ctx), 4),
+        "mla_us": round(t_mla * 1e3, 1),
+        "mla_tflops": round(mla_flops / (t_mla * 1e-3) / 1e12, 1),
+        "decode_chain_us": round(t_dec * 1e3, 1),
+        "decode_chain_bytes": dec_bytes,
+    }
+
+
 PROFILES = ROOT / "profiles"
 STEP_KERNEL = "dsa::sparse_mla_kernel<4, false>"
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
@@ -272,7 +390,7 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--reps", type=int, default=20, help="repetitions of the secondary (flushed) benchmarks")
-    ap.add_argument("--skip", default="", help="comma list of parts to skip: step,indexer,decode,cpu")
+    ap.add_argument("--skip", default="", help="comma list of parts to skip: step,indexer,decode,c5,cpu")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy (HBM byte-counter calibration for rocprof)")
     args = ap.parse_args()
@@ -402,6 +520,10 @@ def main():
         }
         _log(f"C3 decode: {t_dec * 1e3:.1f} us, {dec_gbs:.0f} GB/s")
         del qd, pool, table, idd
+
+    # ---------------- full DSA layer at 128K context (C5) ----------------
+    if "c5" not in skip:
+        result["layer_128k"] = run_c5(torch, pkg, dev, args, flush)
 
     del flush
     if "cpu" not in skip and cpu_inputs is not None:

@@ -55,6 +55,21 @@ const char* dsa_last_error_message(void);
 int dsa_topk_select(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k, const int32_t* row_len,
                     int sorted, int32_t* out_idx, float* out_val, void* stream);
 
+/* Workspace bytes dsa_topk_select_ws needs (0: rows short enough for one pass). */
+size_t dsa_topk_select_workspace_size(int64_t rows, int64_t n, int64_t k);
+
+/*
+ * dsa_topk_select with a caller-provided workspace, for rows longer than
+ * 32768 scores (the 128K-context indexer rows): the rows are selected in
+ * segments, then over the segments' candidates, instead of by repeated radix
+ * passes over the whole row.  Same reference interface and results as
+ * dsa_topk_select; the workspace plays the role of the reference kernels'
+ * workspace buffers (tilelang/jit/__init__.py:212-255, workspace_idx).
+ */
+int dsa_topk_select_ws(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k, const int32_t* row_len,
+                       int sorted, int32_t* out_idx, float* out_val, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
 /*
  * Lightning-indexer logits (fp32, masked positions = -inf).
  * Replaces the QK/ReLU/weighted-head-sum stage of `make_lightning_indexer_kernel`
@@ -77,8 +92,9 @@ int dsa_indexer_logits(int kind, const void* q, const void* k, const float* k_sc
                        const int32_t* actual_k_len, const int32_t* block_table, int64_t block_size,
                        int64_t max_blocks, int sparse_mode, float* logits, int64_t ld, void* stream);
 
-/* Workspace bytes dsa_lightning_indexer needs (the fp32 logits of all rows). */
-size_t dsa_lightning_indexer_workspace_size(int64_t B, int64_t S1, int64_t S2);
+/* Workspace bytes dsa_lightning_indexer needs: the fp32 logits of all rows,
+ * plus the top-k candidate buffer when S2 > 32768. */
+size_t dsa_lightning_indexer_workspace_size(int64_t B, int64_t S1, int64_t S2, int64_t sparse_count);
 
 /*
  * Lightning indexer: logits then top-`sparse_count` per query row.

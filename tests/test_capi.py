@@ -21,8 +21,9 @@ def _declared_functions():
 
 def test_header_declares_the_entry_points():
     names = _declared_functions()
-    assert {"dsa_topk_select", "dsa_indexer_logits", "dsa_lightning_indexer", "dsa_sparse_mla_fwd",
-            "dsa_sparse_mla_workspace_size", "dsa_lightning_indexer_workspace_size"} <= names
+    assert {"dsa_topk_select", "dsa_topk_select_ws", "dsa_topk_select_workspace_size", "dsa_indexer_logits",
+            "dsa_lightning_indexer", "dsa_sparse_mla_fwd", "dsa_sparse_mla_workspace_size",
+            "dsa_lightning_indexer_workspace_size"} <= names
 
 
 def test_library_exports_every_declared_symbol(dsa):
@@ -39,7 +40,7 @@ def test_binding_signatures_cover_the_header(dsa):
 
 def test_abi_rejects_bad_arguments_without_launching(dsa):
     lib = dsa.load_library()
-    assert lib.dsa_abi_version() == 100
+    assert lib.dsa_abi_version() == 101
     # k out of range
     assert lib.dsa_topk_select(None, 8, 1, 8, 0, None, 1, None, None, None) == 1
     assert b"k must be" in lib.dsa_last_error_message()

@@ -125,3 +125,19 @@ def test_reference_example_builder(dsa, dev):
         for s in range(S1):
             mism += len(set(out[b, 0, s].tolist()) ^ set(wi[b, 0, s].tolist()))
     assert 1 - mism / (B * S1 * K) > 0.99
+
+
+def test_lightning_indexer_long_context_topk(dsa, dev):
+    # S2 > 32768: the indexer's top-k takes the segmented path; indices bit-exact given the GPU logits.
+    g = torch.Generator().manual_seed(91)
+    B, S1, S2, H, D, K = 1, 6, 40000, 32, 128, 2048
+    q = torch.randn(B, S1, H, D, generator=g).to(torch.float8_e4m3fn)
+    kf = torch.randn(B, S2, D, generator=g)
+    ks = kf.abs().amax(-1) / 448.0
+    k = (kf / ks.unsqueeze(-1)).to(torch.float8_e4m3fn).unsqueeze(2)
+    w = torch.randn(B, S1, H, generator=g) / 8
+    qd, kd, wd, ksd = q.to(dev), k.to(dev), w.to(dev), ks.to(dev)
+    logits = dsa.indexer_logits(qd, kd, wd, ksd, sparse_mode=3)
+    idx, _ = dsa.lightning_indexer(qd, kd, wd, key_scale=ksd, sparse_count=K, sparse_mode=3)
+    ri, _ = ref.topk_stable(logits.view(S1, S2).float().cpu(), K)
+    assert torch.equal(idx.view(S1, K).cpu(), ri)

@@ -116,3 +116,42 @@ def test_mixed_fast_and_exact_rows(dsa, dev):
     x[10, 17] = 1.0
     _check(dsa, dev, x, 2048)
     _check(dsa, dev, x, 100, sorted=False)
+
+
+# Rows longer than 32768 scores: segments, then a top-k over the segments' candidates.
+@pytest.mark.parametrize("N,K", [(131072, 2048), (50001, 100), (40000, 4096)])
+def test_long_rows_two_stage(dsa, dev, N, K):
+    g = torch.Generator().manual_seed(N + K)
+    x = torch.randn(5, N, generator=g)
+    x[1, N // 2:] = float("-inf")                 # masked tail
+    x[2, :] = float("-inf")
+    x[2, 7] = 0.25                                # a single present score
+    x[3] = torch.randint(0, 5, (N,), generator=g).float()  # heavy ties: exact fallback
+    _check(dsa, dev, x, K)
+
+
+def test_long_rows_row_len_and_strides(dsa, dev):
+    g = torch.Generator().manual_seed(77)
+    base = torch.randn(4, 70003, generator=g)
+    x = base[:, :70000]                           # ld 70003: unaligned rows
+    row_len = torch.tensor([70000, 65537, 2048, 0], dtype=torch.int32)
+    _check(dsa, dev, x, 2048, row_len=row_len)
+
+
+def test_long_rows_ws_matches_plain_entry(dsa, dev):
+    # dsa_topk_select (no workspace: radix passes) and dsa_topk_select_ws agree bit for bit.
+    from tilelang_ascend_amd import _lib as L
+    g = torch.Generator().manual_seed(78)
+    x = (torch.randn(3, 100000, generator=g) * 4).to(dev)
+    lib = L.load_library()
+    a = torch.empty(3, 2048, dtype=torch.int32, device=dev)
+    b = torch.empty_like(a)
+    st = L.stream_handle(dev)
+    L.check(lib.dsa_topk_select(x.data_ptr(), 100000, 3, 100000, 2048, None, 1, a.data_ptr(), None, st), "plain")
+    nws = lib.dsa_topk_select_workspace_size(3, 100000, 2048)
+    assert nws > 0
+    ws = torch.empty(nws, dtype=torch.uint8, device=dev)
+    L.check(lib.dsa_topk_select_ws(x.data_ptr(), 100000, 3, 100000, 2048, None, 1, b.data_ptr(), None,
+                                   ws.data_ptr(), nws, st), "ws")
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)

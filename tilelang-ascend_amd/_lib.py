@@ -30,9 +30,12 @@ SIGNATURES = {
     "dsa_abi_version": (_c_int, []),
     "dsa_last_error_message": (ctypes.c_char_p, []),
     "dsa_topk_select": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_int, _c_vp, _c_vp, _c_vp]),
+    "dsa_topk_select_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64]),
+    "dsa_topk_select_ws": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_int, _c_vp, _c_vp, _c_vp, _c_size,
+                                    _c_vp]),
     "dsa_indexer_logits": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                     _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_vp, _c_i64, _c_vp]),
-    "dsa_lightning_indexer_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64]),
+    "dsa_lightning_indexer_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64]),
     "dsa_lightning_indexer": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                        _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_i64, _c_vp, _c_vp, _c_vp,
                                        _c_size, _c_vp]),

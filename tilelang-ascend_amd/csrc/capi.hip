@@ -7,7 +7,8 @@
 
 namespace dsa {
 hipError_t launch_topk(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k, const int32_t* row_len,
-                       int sorted, int32_t* out_idx, float* out_val, hipStream_t stream);
+                       int sorted, int32_t* out_idx, float* out_val, void* workspace, hipStream_t stream);
+size_t topk_workspace_bytes(int64_t rows, int64_t n, int64_t k);
 hipError_t launch_indexer_logits(int kind, const void* q, const void* k, const float* k_scale, const float* w,
                                  int64_t B, int64_t S1, int64_t S2, int64_t H, int64_t D, const int32_t* aq_len,
                                  const int32_t* ak_len, const int32_t* block_table, int64_t block_size,
@@ -37,18 +38,41 @@ constexpr int64_t kMaxInt = 0x7fffffff;
 
 extern "C" {
 
-int dsa_abi_version(void) { return 100; }
+int dsa_abi_version(void) { return 101; }
 
 const char* dsa_last_error_message(void) { return g_msg; }
 
-int dsa_topk_select(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k, const int32_t* row_len,
-                    int sorted, int32_t* out_idx, float* out_val, void* stream) {
+static int check_topk(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k, const int32_t* out_idx) {
   if (rows < 0 || n < 0 || rows > kMaxInt || n >= kMaxInt) return reject("topk: rows/n out of range");
   if (k < 1 || k > 8192) return reject("topk: k must be in [1, 8192]");
   if (ld < n) return reject("topk: ld < n");
   if (rows > 0 && (!out_idx || (n > 0 && !x))) return reject("topk: null pointer");
-  return ok(dsa::launch_topk(x, ld, rows, n, k, row_len, sorted ? 1 : 0, out_idx, out_val,
+  return 0;
+}
+
+int dsa_topk_select(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k, const int32_t* row_len,
+                    int sorted, int32_t* out_idx, float* out_val, void* stream) {
+  int rc = check_topk(x, ld, rows, n, k, out_idx);
+  if (rc) return rc;
+  return ok(dsa::launch_topk(x, ld, rows, n, k, row_len, sorted ? 1 : 0, out_idx, out_val, nullptr,
                              static_cast<hipStream_t>(stream)));
+}
+
+size_t dsa_topk_select_workspace_size(int64_t rows, int64_t n, int64_t k) {
+  if (rows <= 0 || n <= 0 || k < 1) return 0;
+  return dsa::topk_workspace_bytes(rows, n, k);
+}
+
+int dsa_topk_select_ws(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k, const int32_t* row_len,
+                       int sorted, int32_t* out_idx, float* out_val, void* workspace, size_t workspace_bytes,
+                       void* stream) {
+  int rc = check_topk(x, ld, rows, n, k, out_idx);
+  if (rc) return rc;
+  const size_t need = dsa_topk_select_workspace_size(rows, n, k);
+  if (workspace_bytes < need) return reject("topk: workspace too small");
+  if (need > 0 && !workspace) return reject("topk: null workspace");
+  return ok(dsa::launch_topk(x, ld, rows, n, k, row_len, sorted ? 1 : 0, out_idx, out_val,
+                             need > 0 ? workspace : nullptr, static_cast<hipStream_t>(stream)));
 }
 
 static int check_indexer(int kind, const void* q, const void* k, const float* weights, int64_t B, int64_t S1,
@@ -78,10 +102,16 @@ int dsa_indexer_logits(int kind, const void* q, const void* k, const float* k_sc
                                        static_cast<hipStream_t>(stream)));
 }
 
-size_t dsa_lightning_indexer_workspace_size(int64_t B, int64_t S1, int64_t S2) {
-  if (B <= 0 || S1 <= 0 || S2 <= 0) return 0;
+// Logits of every row, then the top-k candidate buffer for long rows (256-byte aligned).
+static size_t indexer_logits_bytes(int64_t B, int64_t S1, int64_t S2) {
   const int64_t ld = (S2 + 3) & ~int64_t(3);
-  return (size_t)(B * S1 * ld) * sizeof(float);
+  return ((size_t)(B * S1 * ld) * sizeof(float) + 255) & ~size_t(255);
+}
+
+size_t dsa_lightning_indexer_workspace_size(int64_t B, int64_t S1, int64_t S2, int64_t sparse_count) {
+  if (B <= 0 || S1 <= 0 || S2 <= 0) return 0;
+  const int64_t k = sparse_count < 1 ? 1 : sparse_count;
+  return indexer_logits_bytes(B, S1, S2) + dsa::topk_workspace_bytes(B * S1, S2, k);
 }
 
 int dsa_lightning_indexer(int kind, const void* q, const void* k, const float* k_scale, const float* weights,
@@ -92,7 +122,8 @@ int dsa_lightning_indexer(int kind, const void* q, const void* k, const float* k
   int rc = check_indexer(kind, q, k, weights, B, S1, S2, H, D, block_table, block_size, max_blocks, sparse_mode);
   if (rc) return rc;
   if (sparse_count < 1 || sparse_count > 8192) return reject("indexer: sparse_count must be in [1, 8192]");
-  if (workspace_bytes < dsa_lightning_indexer_workspace_size(B, S1, S2)) return reject("indexer: workspace too small");
+  if (workspace_bytes < dsa_lightning_indexer_workspace_size(B, S1, S2, sparse_count))
+    return reject("indexer: workspace too small");
   if (B * S1 > 0 && !out_idx) return reject("indexer: null out_idx");
   if (B * S1 == 0) return 0;
   const int64_t ld = (S2 + 3) & ~int64_t(3);
@@ -101,7 +132,10 @@ int dsa_lightning_indexer(int kind, const void* q, const void* k, const float* k
   hipError_t e = dsa::launch_indexer_logits(kind, q, k, k_scale, weights, B, S1, S2, H, D, actual_q_len, actual_k_len,
                                             block_table, block_size, max_blocks, sparse_mode, logits, ld, st);
   if (e != hipSuccess) return ok(e);
-  return ok(dsa::launch_topk(logits, ld, B * S1, S2, sparse_count, nullptr, 1, out_idx, out_val, st));
+  void* cand = dsa::topk_workspace_bytes(B * S1, S2, sparse_count) > 0
+                   ? static_cast<void*>(static_cast<uint8_t*>(workspace) + indexer_logits_bytes(B, S1, S2))
+                   : nullptr;
+  return ok(dsa::launch_topk(logits, ld, B * S1, S2, sparse_count, nullptr, 1, out_idx, out_val, cand, st));
 }
 
 size_t dsa_sparse_mla_workspace_size(int64_t B, int64_t S, int64_t H, int64_t topk) {

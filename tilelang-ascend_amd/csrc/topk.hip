@@ -235,29 +235,53 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(
 // fast path cannot bound (all-equal scores, a list over kListCap, a bin over
 // kBinCap, non-finite range) are flagged in out_idx[row][0] for the exact
 // radix kernel, launched right after on the same stream.
+//
+// Rows longer than the registers hold go through it twice.  Stage 1 runs one
+// workgroup per segment of a row (nseg > 1): the segment's own top-k, with
+// global indices, into a candidate buffer -- every element of the row's top-k
+// is in its segment's top-k under the same order.  Stage 2 selects over the
+// nseg*k candidates of each row, taking the tie-break index from idx_map (the
+// candidates' original indices) and flagging the row if any of its segments
+// was flagged, so that the radix kernel redoes it from the original row.
 // ----------------------------------------------------------------------------
 constexpr int kListCap = 4096;
 constexpr int kBinCap = 512;
+constexpr int kRegMax = 4 * kTopkThreads * 8;  // longest row the register path holds (32768)
 
 template <int kChunks>
 __global__ __launch_bounds__(kTopkThreads) void topk_reg_kernel(const float* __restrict__ x, int64_t ld, int n, int k,
                                                                 const int32_t* __restrict__ row_len,
                                                                 int32_t* __restrict__ out_idx,
-                                                                float* __restrict__ out_val) {
+                                                                float* __restrict__ out_val, int nseg, int seg_len,
+                                                                const int32_t* __restrict__ idx_map) {
   __shared__ uint32_t cnt[kHistBins];
   __shared__ uint32_t offs[kHistBins];
   __shared__ uint32_t fill[kHistBins];
   __shared__ uint32_t red[kRedWords];
   __shared__ uint64_t list[kListCap];
-  const int row = blockIdx.x;
+  const int vrow = blockIdx.x;  // output row: segment vrow % nseg of input row vrow / nseg
+  const int row = vrow / nseg;
+  const int seg = vrow - row * nseg;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
-  const float* __restrict__ xr = x + (int64_t)row * ld;
-  int32_t* __restrict__ oi = out_idx + (int64_t)row * k;
-  float* __restrict__ ov = out_val ? out_val + (int64_t)row * k : nullptr;
+  const int base = seg * seg_len;  // index of this segment's first element
+  const float* __restrict__ xr = x + (int64_t)row * ld + base;
+  int32_t* __restrict__ oi = out_idx + (int64_t)vrow * k;
+  float* __restrict__ ov = out_val ? out_val + (int64_t)vrow * k : nullptr;
+  const int32_t* __restrict__ imap = idx_map ? idx_map + (int64_t)row * ld : nullptr;
   int nv = n;
   if (row_len) nv = min(max(row_len[row], 0), n);
+  nv = min(max(nv - base, 0), seg_len);
+  if (imap) {
+    // Stage 2: a flagged segment (its first candidate index) sends the whole row to the exact path.
+    bool flagged = false;
+    for (int sg = 0; sg * k < n; ++sg) flagged |= imap[sg * k] == kFallbackFlag;
+    if (flagged) {
+      if (tid == 0) oi[0] = kFallbackFlag;
+      return;  // block-uniform
+    }
+  }
 
   // 1. Load: thread t holds elements 4*(t + c*1024) .. +3 of chunk c.
   float v[kChunks][4];
@@ -365,7 +389,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_reg_kernel(const float* __r
           const int b = min(kHistBins - 1, (int)((val - vmin) * inv));
           if (b >= bstar) {
             const uint32_t pos = offs[b] + atomicAdd(&fill[b], 1u);
-            const int idx = 4 * (tid + c * kTopkThreads) + j;
+            const int p = 4 * (tid + c * kTopkThreads) + j;
+            const int idx = imap ? imap[p] : base + p;
             list[pos] = ((uint64_t)float_key(val) << 32) | (uint32_t)(~(uint32_t)idx);
           }
         }
@@ -399,29 +424,67 @@ static int next_pow2(int v) {
   return p;
 }
 
-// Launch on `stream`.  Caller has validated shapes (rows, n >= 0; 1 <= k <= 8192).
-template <int kChunks>
+// Launch on `stream`: `rows` output rows (rows / nseg input rows of nseg segments of seg_len).
 static hipError_t launch_reg(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k, const int32_t* row_len,
-                             int32_t* out_idx, float* out_val, hipStream_t stream) {
-  hipLaunchKernelGGL((topk_reg_kernel<kChunks>), dim3((unsigned)rows), dim3(kTopkThreads), 0, stream, x, ld, (int)n,
-                     (int)k, row_len, out_idx, out_val);
+                             int32_t* out_idx, float* out_val, int nseg, int64_t seg_len, const int32_t* idx_map,
+                             hipStream_t stream) {
+  const dim3 grid((unsigned)rows), block(kTopkThreads);
+#define DSA_REG(C)                                                                                                \
+  hipLaunchKernelGGL((topk_reg_kernel<C>), grid, block, 0, stream, x, ld, (int)n, (int)k, row_len, out_idx, out_val, \
+                     nseg, (int)seg_len, idx_map)
+  if (seg_len <= 4 * kTopkThreads) DSA_REG(1);
+  else if (seg_len <= 8 * kTopkThreads) DSA_REG(2);
+  else if (seg_len <= 16 * kTopkThreads) DSA_REG(4);
+  else DSA_REG(8);
+#undef DSA_REG
   return hipGetLastError();
 }
 
-// Launch on `stream`.  Caller has validated shapes (rows, n >= 0; 1 <= k <= 8192).
+// Segments per row for the two-stage path (0: not used).  A segment holds at
+// most kRegMax scores and at least k; the candidates (nseg * k) must fit the
+// register path again; small row counts get more segments to fill the GPU.
+static int long_row_segments(int64_t rows, int64_t n, int64_t k) {
+  if (n <= kRegMax || k > kListCap) return 0;
+  int nseg = (int)((n + kRegMax - 1) / kRegMax);
+  while (rows * nseg < 512 && (int64_t)(nseg * 2) * k <= kRegMax && (n + nseg * 2 - 1) / (nseg * 2) >= k) nseg *= 2;
+  if ((int64_t)nseg * k > kRegMax) return 0;
+  return nseg;
+}
+
+static int64_t segment_length(int64_t n, int nseg) {
+  return ((n + nseg - 1) / nseg + 3) & ~int64_t(3);  // multiple of 4: segments stay 16-byte aligned
+}
+
+size_t topk_workspace_bytes(int64_t rows, int64_t n, int64_t k) {
+  const int nseg = long_row_segments(rows, n, k);
+  if (nseg == 0) return 0;
+  return (size_t)rows * nseg * k * 8;  // candidate values + indices
+}
+
+// Launch on `stream`.  Caller has validated shapes (rows, n >= 0; 1 <= k <= 8192) and, when
+// topk_workspace_bytes() is non-zero, passes a workspace of at least that size (else: nullptr,
+// and long rows take the radix kernel alone).
 hipError_t launch_topk(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k,
                        const int32_t* row_len, int sorted, int32_t* out_idx, float* out_val,
-                       hipStream_t stream) {
+                       void* workspace, hipStream_t stream) {
   if (rows == 0) return hipSuccess;
-  // Fast path for rows that fit in registers; the exact radix kernel then
-  // takes only the rows the fast path flagged (its output is sorted either way).
+  // Fast path for rows that fit in registers (directly, or in segments then
+  // over the segments' candidates); the exact radix kernel then takes only the
+  // rows the fast path flagged (its output is sorted either way).
   int only_flagged = 0;
-  if (n <= 4 * kTopkThreads * 8 && k <= kListCap) {
-    hipError_t e;
-    if (n <= 4 * kTopkThreads) e = launch_reg<1>(x, ld, rows, n, k, row_len, out_idx, out_val, stream);
-    else if (n <= 8 * kTopkThreads) e = launch_reg<2>(x, ld, rows, n, k, row_len, out_idx, out_val, stream);
-    else if (n <= 16 * kTopkThreads) e = launch_reg<4>(x, ld, rows, n, k, row_len, out_idx, out_val, stream);
-    else e = launch_reg<8>(x, ld, rows, n, k, row_len, out_idx, out_val, stream);
+  const int nseg = workspace ? long_row_segments(rows, n, k) : 0;
+  if (n <= kRegMax && k <= kListCap) {
+    hipError_t e = launch_reg(x, ld, rows, n, k, row_len, out_idx, out_val, 1, n, nullptr, stream);
+    if (e != hipSuccess) return e;
+    only_flagged = 1;
+    sorted = 1;
+  } else if (nseg > 0) {
+    float* cval = static_cast<float*>(workspace);
+    int32_t* cidx = reinterpret_cast<int32_t*>(cval + (size_t)rows * nseg * k);
+    hipError_t e = launch_reg(x, ld, rows * nseg, n, k, row_len, cidx, cval, nseg, segment_length(n, nseg), nullptr,
+                              stream);
+    if (e != hipSuccess) return e;
+    e = launch_reg(cval, nseg * k, rows, nseg * k, k, nullptr, out_idx, out_val, 1, nseg * k, cidx, stream);
     if (e != hipSuccess) return e;
     only_flagged = 1;
     sorted = 1;

@@ -159,7 +159,7 @@ def lightning_indexer(query: torch.Tensor, key: torch.Tensor, weights: torch.Ten
         return idx, vals
     val = torch.empty((B, S1, 1, sparse_count), dtype=torch.float32, device=dev) if return_value else None
     lib = _lib.load_library()
-    ws_bytes = lib.dsa_lightning_indexer_workspace_size(B, S1, S2)
+    ws_bytes = lib.dsa_lightning_indexer_workspace_size(B, S1, S2, sparse_count)
     ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
     rc = lib.dsa_lightning_indexer(_KINDS[query.dtype], _lib.ptr(query), _lib.ptr(key), _lib.ptr(ks), _lib.ptr(w),
                                    B, S1, S2, N1, D, _lib.ptr(aq), _lib.ptr(ak), _lib.ptr(bt), bs, mb, sparse_mode,

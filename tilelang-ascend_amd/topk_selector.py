@@ -46,9 +46,11 @@ def topk_selector(x: torch.Tensor, top_k: int, sorted: bool = True, *, row_len: 
     idx = torch.empty((rows, top_k), dtype=torch.int32, device=dev)
     val = torch.empty((rows, top_k), dtype=torch.float32, device=dev) if return_values else None
     lib = _lib.load_library()
-    rc = lib.dsa_topk_select(_lib.ptr(xf), ld, rows, n, top_k, _lib.ptr(row_len), 1 if sorted else 0,
-                             _lib.ptr(idx), _lib.ptr(val), _lib.stream_handle(dev))
-    _lib.check(rc, "dsa_topk_select")
+    ws_bytes = lib.dsa_topk_select_workspace_size(rows, n, top_k)
+    ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev) if ws_bytes else None
+    rc = lib.dsa_topk_select_ws(_lib.ptr(xf), ld, rows, n, top_k, _lib.ptr(row_len), 1 if sorted else 0,
+                                _lib.ptr(idx), _lib.ptr(val), _lib.ptr(ws), ws_bytes, _lib.stream_handle(dev))
+    _lib.check(rc, "dsa_topk_select_ws")
     idx = idx.view(*lead, top_k)
     if return_values:
         return idx, val.view(*lead, top_k)
