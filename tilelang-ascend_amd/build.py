@@ -35,9 +35,16 @@ COMMON_FLAGS = [
 ]
 
 
+# Per-file extras.  indexer.hip: keep MFMA results in VGPRs (its epilogue reads
+# every result with VALU; AGPR results would each need a v_accvgpr_read).
+FILE_FLAGS = {
+    "indexer.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def _compile(src: Path, verbose: bool) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [HIPCC, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *COMMON_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

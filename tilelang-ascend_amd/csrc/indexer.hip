@@ -45,59 +45,65 @@ struct IdxTraits {
 template <int kKind, int kD>
 constexpr int lds_pitch() { return IdxTraits<kKind, kD>::kRowBytes + 16; }
 
+// A lane's K-slice of one 16-row operand, as 16-byte pieces.  fp8 with D = 128
+// is kept as the 32-byte MFMA operand itself, so no per-instruction copies.
 template <int kKind, int kD>
 struct Operand {
-  static constexpr int kWords = IdxTraits<kKind, kD>::kLaneBytes / 4;
-  uint32_t w[kWords];
+  static constexpr int kPieces = IdxTraits<kKind, kD>::kLaneBytes / 16;
+  static constexpr bool kWhole = kKind == kFp8 && kD == 128;
+  i32x8 v;              // kWhole
+  u32x4 p[kPieces];     // otherwise
 };
 
 template <int kKind, int kD>
-__device__ __forceinline__ void load_operand_global(Operand<kKind, kD>& op, const uint8_t* p, bool valid) {
-  constexpr int n16 = IdxTraits<kKind, kD>::kLaneBytes / 16;
-#pragma unroll
-  for (int c = 0; c < n16; ++c) {
-    u32x4 v = valid ? *reinterpret_cast<const u32x4*>(p + 16 * c) : u32x4{0, 0, 0, 0};
-    op.w[4 * c + 0] = v.x; op.w[4 * c + 1] = v.y; op.w[4 * c + 2] = v.z; op.w[4 * c + 3] = v.w;
+__device__ __forceinline__ void set_piece(Operand<kKind, kD>& op, int c, const u32x4& x) {
+  if constexpr (Operand<kKind, kD>::kWhole) {
+    op.v[4 * c + 0] = (int)x.x; op.v[4 * c + 1] = (int)x.y; op.v[4 * c + 2] = (int)x.z; op.v[4 * c + 3] = (int)x.w;
+  } else {
+    op.p[c] = x;
   }
+}
+
+template <int kKind, int kD>
+__device__ __forceinline__ void load_operand_global(Operand<kKind, kD>& op, const uint8_t* p, bool valid) {
+#pragma unroll
+  for (int c = 0; c < Operand<kKind, kD>::kPieces; ++c)
+    set_piece(op, c, valid ? *reinterpret_cast<const u32x4*>(p + 16 * c) : u32x4{0, 0, 0, 0});
 }
 
 template <int kKind, int kD>
 __device__ __forceinline__ void load_operand_lds(Operand<kKind, kD>& op, const uint8_t* p) {
-  constexpr int n16 = IdxTraits<kKind, kD>::kLaneBytes / 16;
 #pragma unroll
-  for (int c = 0; c < n16; ++c) {
-    u32x4 v = *reinterpret_cast<const u32x4*>(p + 16 * c);
-    op.w[4 * c + 0] = v.x; op.w[4 * c + 1] = v.y; op.w[4 * c + 2] = v.z; op.w[4 * c + 3] = v.w;
-  }
+  for (int c = 0; c < Operand<kKind, kD>::kPieces; ++c) set_piece(op, c, *reinterpret_cast<const u32x4*>(p + 16 * c));
 }
 
 template <int kKind, int kD>
 __device__ __forceinline__ f32x4 mfma_qk(const Operand<kKind, kD>& a, const Operand<kKind, kD>& b) {
-  constexpr int kW = Operand<kKind, kD>::kWords;
   f32x4 c = {0.f, 0.f, 0.f, 0.f};
-  if constexpr (kKind == kFp8) {
+  if constexpr (Operand<kKind, kD>::kWhole) {
+    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a.v, b.v, c, 0, 0, 0, 0, 0, 0);
+  } else if constexpr (kKind == kFp8) {
     // One 16x16x128 fp8 MFMA; a D = 64 row leaves half of each lane's K-slice zero.
-    i32x8 av, bv;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      av[i] = i < kW ? (int)a.w[i] : 0;
-      bv[i] = i < kW ? (int)b.w[i] : 0;
-    }
+    const i32x8 av = {(int)a.p[0].x, (int)a.p[0].y, (int)a.p[0].z, (int)a.p[0].w, 0, 0, 0, 0};
+    const i32x8 bv = {(int)b.p[0].x, (int)b.p[0].y, (int)b.p[0].z, (int)b.p[0].w, 0, 0, 0, 0};
     c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 0, 0, 0, 0, 0, 0);
   } else {
 #pragma unroll
-    for (int s = 0; s < kW / 4; ++s) {
-      u32x4 au = {a.w[4 * s], a.w[4 * s + 1], a.w[4 * s + 2], a.w[4 * s + 3]};
-      u32x4 bu = {b.w[4 * s], b.w[4 * s + 1], b.w[4 * s + 2], b.w[4 * s + 3]};
+    for (int s = 0; s < Operand<kKind, kD>::kPieces; ++s) {
       if constexpr (kKind == kBf16) {
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, au), __builtin_bit_cast(bf16x8, bu), c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a.p[s]), __builtin_bit_cast(bf16x8, b.p[s]), c, 0, 0, 0);
       } else {
-        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, au), __builtin_bit_cast(f16x8, bu), c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a.p[s]), __builtin_bit_cast(f16x8, b.p[s]), c, 0, 0, 0);
       }
     }
   }
   return c;
 }
+
+// ReLU of a dot product in one v_med3_f32 (fmaxf adds a NaN-quieting max in
+// IEEE mode).  The bound 3e38 is never reached: |q . k| for fp8/bf16/fp16
+// inputs is far below it.
+__device__ __forceinline__ float relu(float x) { return __builtin_amdgcn_fmed3f(x, 0.f, 3.0e38f); }
 
 struct IdxArgs {
   const uint8_t* q;        // [B, S1, H, 128]
@@ -242,17 +248,19 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_logits_kernel(IdxArgs a) 
       load_operand_lds<kKind, kD>(kb, &ktile[buf][(sub * 16 + r) * kPitch + g * kLB]);
 #pragma unroll
       for (int j = 0; j < kTokPW; ++j) {
-        float acc = 0.f;
+        float acc2[2] = {0.f, 0.f};  // two chains: head blocks 0, 2 and 1, 3
 #pragma unroll
         for (int hb = 0; hb < 4; ++hb) {
           if (hb < nhb) {
             const f32x4 c = mfma_qk<kKind, kD>(qa[j][hb], kb);
-            acc = fmaf(wv[j][hb].x, fmaxf(c.x, 0.f), acc);
-            acc = fmaf(wv[j][hb].y, fmaxf(c.y, 0.f), acc);
-            acc = fmaf(wv[j][hb].z, fmaxf(c.z, 0.f), acc);
-            acc = fmaf(wv[j][hb].w, fmaxf(c.w, 0.f), acc);
+            float& acc = acc2[hb & 1];
+            acc = fmaf(wv[j][hb].x, relu(c.x), acc);
+            acc = fmaf(wv[j][hb].y, relu(c.y), acc);
+            acc = fmaf(wv[j][hb].z, relu(c.z), acc);
+            acc = fmaf(wv[j][hb].w, relu(c.w), acc);
           }
         }
+        float acc = acc2[0] + acc2[1];
         acc += __shfl_xor(acc, 16, kWave);
         acc += __shfl_xor(acc, 32, kWave);
         res[j] = (g == sub) ? acc : res[j];
