@@ -29,23 +29,39 @@ constexpr int kRedWords = 64;
 constexpr int kLdsBytes = 160 * 1024;
 constexpr int32_t kFallbackFlag = (int32_t)0x80000000;  // out_idx[row][0] marker: row needs the exact radix path
 
+// Inclusive wave scan and wave reductions on DPP (row shifts, then the row
+// broadcasts 15 and 31).
+#define DSA_DPP(old, x, ctrl, rmask) __builtin_amdgcn_update_dpp((int)(old), (int)(x), ctrl, rmask, 0xf, false)
+
+__device__ __forceinline__ uint32_t wave_scan_add(uint32_t x) {
+  x += (uint32_t)DSA_DPP(0, x, 0x111, 0xf);
+  x += (uint32_t)DSA_DPP(0, x, 0x112, 0xf);
+  x += (uint32_t)DSA_DPP(0, x, 0x114, 0xf);
+  x += (uint32_t)DSA_DPP(0, x, 0x118, 0xf);
+  x += (uint32_t)DSA_DPP(0, x, 0x142, 0xa);
+  x += (uint32_t)DSA_DPP(0, x, 0x143, 0xc);
+  return x;
+}
+
 // Block-wide exclusive scan of one uint32 per thread; `total` receives the sum.
-// Uses red[0..kTopkWaves) and ends with a barrier so red can be reused.
+// Uses red[0..kTopkWaves); with kTrailingBarrier it ends with a barrier so red
+// can be reused.
+template <bool kTrailingBarrier = true>
 __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* red, uint32_t& total) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  uint32_t incl = wave_incl_scan(v);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const uint32_t incl = wave_scan_add(v);
   if (lane == kWave - 1) red[wave] = incl;
   __syncthreads();
-  uint32_t before = 0, tot = 0;
-#pragma unroll
-  for (int w = 0; w < kTopkWaves; ++w) {
-    uint32_t s = red[w];
-    before += (w < wave) ? s : 0u;
-    tot += s;
-  }
-  __syncthreads();
-  total = tot;
+  // Lanes 0..15 scan the 16 wave totals.
+  uint32_t w = lane < kTopkWaves ? red[lane] : 0u;
+  w += (uint32_t)DSA_DPP(0, w, 0x111, 0xf);
+  w += (uint32_t)DSA_DPP(0, w, 0x112, 0xf);
+  w += (uint32_t)DSA_DPP(0, w, 0x114, 0xf);
+  w += (uint32_t)DSA_DPP(0, w, 0x118, 0xf);
+  total = (uint32_t)__builtin_amdgcn_readlane((int)w, kTopkWaves - 1);
+  const uint32_t before = wave ? (uint32_t)__builtin_amdgcn_readlane((int)w, wave - 1) : 0u;
+  if constexpr (kTrailingBarrier) __syncthreads();
   return before + incl - v;
 }
 
@@ -223,48 +239,159 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(
 // Register-resident fast path (rows of up to 4096 * kChunks scores).
 //
 // The row is loaded once into VGPRs (kChunks 16-byte loads per thread, all in
-// flight together).  Present scores (> -1e30, not NaN) are bucketed into 2048
-// bins linear in value between the row's min and max -- a monotone map, so
-// every score in a higher bin is strictly larger -- which spreads the
-// histogram atomics far better than key-bit radix digits do.  A descending
-// scan finds the bin b* holding the k-th largest; every score in bins >= b*
-// goes, as a (key << 32 | ~index) word, into an LDS list grouped by bin.  Each
-// list entry then counts the entries of its own bin that beat it: bin offset
-// + that rank is its final sorted position (value desc, index asc), exact
-// with ties, and entries landing below k are written out directly.  Rows the
-// fast path cannot bound (all-equal scores, a list over kListCap, a bin over
-// kBinCap, non-finite range) are flagged in out_idx[row][0] for the exact
-// radix kernel, launched right after on the same stream.
+// flight together) and never re-read.  One score per thread (1024, spread over
+// the row) forms a sample.  A two-level histogram of the samples' order keys
+// (top 10 key bits, then the next 10 inside the bin that matters) gives a
+// threshold t whose expected candidate count (scores >= t) sits midway between
+// k and the candidate capacity.  One pass over the registers compacts the
+// candidates into LDS with wave ballots, every wave into its own region.  The
+// set {score >= t} is closed upwards in the order (value desc, index asc), so
+// once it holds at least k scores (or t admits every present score) it holds
+// the whole top-k; otherwise t moves by bisection over the sample ranks and
+// the pass repeats.  The candidates alone are then bucketed into 4096 bins of
+// their order keys (key - key(min)) >> shift, a descending scan finds the bin
+// b* holding the k-th largest, the candidates of bins >= b* are regrouped by
+// bin, and each counts the entries of its own bin that beat it (bins rarely
+// hold more than one): bin start + that rank is its sorted position, exact
+// with ties, and it is stored there directly.  Rows the fast path cannot bound
+// (no threshold with k..kCandCap candidates, a bin over kBinCap) are flagged
+// in out_idx[row][0] for the exact radix kernel, launched right after on the
+// same stream.
 //
 // Rows longer than the registers hold go through it twice.  Stage 1 runs one
-// workgroup per segment of a row (nseg > 1): the segment's own top-k, with
-// global indices, into a candidate buffer -- every element of the row's top-k
-// is in its segment's top-k under the same order.  Stage 2 selects over the
-// nseg*k candidates of each row, taking the tie-break index from idx_map (the
-// candidates' original indices) and flagging the row if any of its segments
-// was flagged, so that the radix kernel redoes it from the original row.
+// workgroup per segment of a row (nseg > 1): the segment's own sorted top-k,
+// with global indices, into a candidate buffer -- every element of the row's
+// top-k is in its segment's top-k under the same order.  Stage 2 selects over
+// the nseg*k candidates of each row and maps positions back through idx_map
+// (the candidates' original indices); among equal scores, candidate position
+// order is original index order (segments are contiguous and each is sorted),
+// so positions break the ties.  A row any of whose segments was flagged is
+// flagged again, so that the radix kernel redoes it from the original row.
 // ----------------------------------------------------------------------------
-constexpr int kListCap = 4096;
-constexpr int kBinCap = 512;
-constexpr int kRegMax = 4 * kTopkThreads * 8;  // longest row the register path holds (32768)
+constexpr int kListCap = 4096;                   // largest k the fast path takes
+constexpr int kWaveCap = 320;                    // candidates one wave may hold
+constexpr int kCandCap = kWaveCap * kTopkWaves;  // 5120
+constexpr int kLaneEntries = kWaveCap / kWave;   // 5
+constexpr int kCandBins = 4096;
+constexpr int kCandBinBits = 12;
+constexpr int kSampleBins = 1024;                // per level; one sample per thread
+constexpr int kBinCap = 512;                     // longest bin the rank loop walks
+constexpr int kMaxTries = 12;
+constexpr int kRegChunks = 8;
+constexpr int kRegMax = 4 * kTopkThreads * kRegChunks;  // longest row the register path holds (32768)
+constexpr uint32_t kFloorBits = 0xF149F2C9u;     // next float above -1e30f: v >= it <=> v > -1e30f
+constexpr int kPosBits = 15;                     // positions inside a register row (< kRegMax)
+static_assert((kRegMax - 1) >> kPosBits == 0 && kCandBins << kPosBits != 0, "bin and position share a word");
 
-template <int kChunks>
-__global__ __launch_bounds__(kTopkThreads) void topk_reg_kernel(const float* __restrict__ x, int64_t ld, int n, int k,
-                                                                const int32_t* __restrict__ row_len,
-                                                                int32_t* __restrict__ out_idx,
-                                                                float* __restrict__ out_val, int nseg, int seg_len,
-                                                                const int32_t* __restrict__ idx_map) {
-  __shared__ uint32_t cnt[kHistBins];
-  __shared__ uint32_t offs[kHistBins];
-  __shared__ uint32_t fill[kHistBins];
-  __shared__ uint32_t red[kRedWords];
-  __shared__ uint64_t list[kListCap];
+// LDS of the register path, in 32-bit words.  A wave that finds more than
+// kWaveCap candidates keeps writing past its region (values into the next
+// regions and the position array, positions into cnt); such a try is retried,
+// and cnt is cleared after every compaction, so nothing else is reached.
+constexpr int kLdsVal = 0;                            // kCandCap candidate values
+constexpr int kLdsPos = kLdsVal + kCandCap;           // kCandCap candidate positions
+constexpr int kLdsCnt = kLdsPos + kCandCap;           // kCandBins bin counts
+constexpr int kLdsOffs = kLdsCnt + kCandBins;         // kCandBins bin offsets; before them the sample histograms
+constexpr int kLdsSample = kLdsOffs + kCandBins;      // kTopkThreads sample keys (0: absent)
+constexpr int kLdsRed = kLdsSample + kTopkThreads;     // reduction words
+constexpr int kLdsRegWords = kLdsRed + 128;
+static_assert(kWave * 4 * kRegChunks - kWaveCap <= kCandBins, "a wave's overrun must stay inside cnt");
+static_assert(2 * kSampleBins <= kCandBins, "sample histograms live in the offsets array");
+// Reduction words.
+constexpr int kRedCoarse = 0;      // coarse sample bin of the threshold
+constexpr int kRedAbove = 1;       // samples above that bin
+constexpr int kRedThresh = 2;      // threshold key
+constexpr int kRedFlag = 3;        // a bin over kBinCap
+constexpr int kRedBstar = 4;
+constexpr int kRedScan = 16;       // block_excl_scan scratch (16)
+constexpr int kRedCount = 32;      // per wave: candidates held
+constexpr int kRedMin = 48;        // per wave: smallest candidate
+constexpr int kRedMax = 64;        // per wave: largest candidate
+constexpr int kRedPresent = 80;    // per wave: present samples
+
+// Inclusive sum / max over lanes 0..15 (row 0 of the wave), read from lane 15.
+__device__ __forceinline__ uint32_t row0_sum(uint32_t x) {
+  x += (uint32_t)DSA_DPP(0, x, 0x111, 0xf);
+  x += (uint32_t)DSA_DPP(0, x, 0x112, 0xf);
+  x += (uint32_t)DSA_DPP(0, x, 0x114, 0xf);
+  x += (uint32_t)DSA_DPP(0, x, 0x118, 0xf);
+  return (uint32_t)__builtin_amdgcn_readlane((int)x, 15);
+}
+
+__device__ __forceinline__ uint32_t row0_max(uint32_t x) {
+  x = max(x, (uint32_t)DSA_DPP(0, x, 0x111, 0xf));
+  x = max(x, (uint32_t)DSA_DPP(0, x, 0x112, 0xf));
+  x = max(x, (uint32_t)DSA_DPP(0, x, 0x114, 0xf));
+  x = max(x, (uint32_t)DSA_DPP(0, x, 0x118, 0xf));
+  return (uint32_t)__builtin_amdgcn_readlane((int)x, 15);
+}
+
+// Max over the wave of uint32, identical in every lane.
+__device__ __forceinline__ uint32_t wave_all_umax(uint32_t x) {
+  x = max(x, (uint32_t)DSA_DPP(0, x, 0x111, 0xf));
+  x = max(x, (uint32_t)DSA_DPP(0, x, 0x112, 0xf));
+  x = max(x, (uint32_t)DSA_DPP(0, x, 0x114, 0xf));
+  x = max(x, (uint32_t)DSA_DPP(0, x, 0x118, 0xf));
+  x = max(x, (uint32_t)DSA_DPP(0, x, 0x142, 0xa));
+  x = max(x, (uint32_t)DSA_DPP(0, x, 0x143, 0xc));
+  return (uint32_t)__builtin_amdgcn_readlane((int)x, kWave - 1);
+}
+
+__device__ __forceinline__ uint32_t lane_prefix(uint64_t m, uint32_t add) {  // add + set bits of m below this lane
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, add));
+}
+
+// Order key with -0 folded onto +0 (x + 0 turns -0 into +0); NaN never reaches it.
+__device__ __forceinline__ uint32_t cand_key(float x) {
+  const uint32_t u = __float_as_uint(x + 0.0f);
+  return u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
+}
+
+// One wave: the bin of a 1024-bin histogram holding the r-th largest entry
+// (1 <= r <= total); `above` receives the entries in higher bins.
+__device__ __forceinline__ int rank_bin(const uint32_t* h, uint32_t r, uint32_t& above) {
+  const int lane = threadIdx.x & (kWave - 1);
+  // Lane l sums bins [1008 - 16 l, 1024 - 16 l): lane 0 holds the top bins.
+  const u32x4* h4 = reinterpret_cast<const u32x4*>(h) + (kSampleBins / 4 - 4 - 4 * lane);
+  uint32_t sum = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const u32x4 t = h4[q];
+    sum += t.x + t.y + t.z + t.w;
+  }
+  const uint32_t incl = wave_scan_add(sum);
+  const int L = (int)__builtin_ctzll(__builtin_amdgcn_ballot_w64(incl >= r));
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)(incl - sum), L);
+  // Lanes 0..15 take lane L's bins from the top down.
+  const uint32_t c = lane < 16 ? h[kSampleBins - 1 - 16 * L - lane] : 0u;
+  uint32_t ci = c;
+  ci += (uint32_t)DSA_DPP(0, ci, 0x111, 0xf);
+  ci += (uint32_t)DSA_DPP(0, ci, 0x112, 0xf);
+  ci += (uint32_t)DSA_DPP(0, ci, 0x114, 0xf);
+  ci += (uint32_t)DSA_DPP(0, ci, 0x118, 0xf);
+  const int i = (int)__builtin_ctzll(__builtin_amdgcn_ballot_w64(lane < 16 && a + ci >= r));
+  above = a + (uint32_t)__builtin_amdgcn_readlane((int)(ci - c), i);
+  return kSampleBins - 1 - 16 * L - i;
+}
+
+template <int kChunks, bool kFull>
+__global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8, 8))) void topk_reg_kernel(
+    const float* __restrict__ x, int64_t ld, int n, int k, const int32_t* __restrict__ row_len,
+    int32_t* __restrict__ out_idx, float* __restrict__ out_val, int nseg, int seg_len,
+    const int32_t* __restrict__ idx_map) {
+  __shared__ __align__(16) uint32_t lds[kLdsRegWords];
+  uint32_t* lv = lds + kLdsVal;
+  uint32_t* lp = lds + kLdsPos;
+  uint32_t* cnt = lds + kLdsCnt;
+  uint32_t* offs = lds + kLdsOffs;
+  uint32_t* shc = offs;                // coarse sample histogram
+  uint32_t* shf = offs + kSampleBins;  // fine sample histogram
+  uint32_t* red = lds + kLdsRed;
   const int vrow = blockIdx.x;  // output row: segment vrow % nseg of input row vrow / nseg
   const int row = vrow / nseg;
   const int seg = vrow - row * nseg;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
-  const int wave = tid / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int base = seg * seg_len;  // index of this segment's first element
   const float* __restrict__ xr = x + (int64_t)row * ld + base;
   int32_t* __restrict__ oi = out_idx + (int64_t)vrow * k;
@@ -283,138 +410,249 @@ __global__ __launch_bounds__(kTopkThreads) void topk_reg_kernel(const float* __r
     }
   }
 
-  // 1. Load: thread t holds elements 4*(t + c*1024) .. +3 of chunk c.
+  // 1. Load: thread t holds positions 4*(t + c*1024) .. +3 of chunk c.  kFull:
+  // the host has checked that every row is whole (4096 * kChunks scores) and
+  // 16-byte aligned, so the loads are straight-line.
   float v[kChunks][4];
-  const bool vec = ((reinterpret_cast<uintptr_t>(xr) & 15) == 0);
+  const int g_full = nv >> 2;
+  if constexpr (kFull) {
 #pragma unroll
-  for (int c = 0; c < kChunks; ++c) {
-    const int e0 = 4 * (tid + c * kTopkThreads);
-    if (vec && e0 + 3 < nv) {
-      const f32x4 t = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(xr) + (tid + c * kTopkThreads));
+    for (int c = 0; c < kChunks; ++c) {
+      const f32x4 t = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(xr) + tid + c * kTopkThreads);
       v[c][0] = t[0]; v[c][1] = t[1]; v[c][2] = t[2]; v[c][3] = t[3];
-    } else {
+    }
+  } else if ((reinterpret_cast<uintptr_t>(xr) & 15) == 0) {  // block-uniform
+    // Whole groups of 4 with 16-byte loads; the one partial group at the end by element.
+    const f32x4 ninf4 = {-__builtin_huge_valf(), -__builtin_huge_valf(), -__builtin_huge_valf(), -__builtin_huge_valf()};
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+      const int g = tid + c * kTopkThreads;
+      f32x4 t = ninf4;
+      if (g < g_full) t = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(xr) + g);
+      v[c][0] = t[0]; v[c][1] = t[1]; v[c][2] = t[2]; v[c][3] = t[3];
+    }
+    if (nv & 3) {
+      const int g = g_full;  // its owner: thread g % 1024, chunk g / 1024
+      if (tid == (g & (kTopkThreads - 1))) {
+#pragma unroll
+        for (int c = 0; c < kChunks; ++c)
+          if (c == g / kTopkThreads) {
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+              if (4 * g + j < nv) v[c][j] = xr[4 * g + j];
+          }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c) {
+      const int e0 = 4 * (tid + c * kTopkThreads);
 #pragma unroll
       for (int j = 0; j < 4; ++j) v[c][j] = (e0 + j < nv) ? xr[e0 + j] : -__builtin_huge_valf();
     }
   }
-  for (int b = tid; b < kHistBins; b += kTopkThreads) { cnt[b] = 0; fill[b] = 0; }
+  // Sample histograms (both levels) start empty.
+  reinterpret_cast<u32x2*>(shc)[tid] = u32x2{0u, 0u};
+  if (tid == 0) red[kRedFlag] = 0;
+  __syncthreads();
 
-  // 2. Count, min and max of the present scores.
-  uint32_t present = 0;
-  float vmin = __builtin_huge_valf(), vmax = -__builtin_huge_valf();
+  // 2. Sample: wave w takes register (c, j) = (w % kChunks, (w / kChunks) % 4),
+  // 64 positions 4 apart in each of 16 windows spread over the row.  (A
+  // separate, earlier sample load costs more than it saves: the row loads
+  // fetched its lines from HBM a second time.)
+  float s = v[0][0];
 #pragma unroll
   for (int c = 0; c < kChunks; ++c)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const bool p = v[c][j] > -1e30f;  // false for NaN too
-      present += p;
-      if (p) { vmin = fminf(vmin, v[c][j]); vmax = fmaxf(vmax, v[c][j]); }
+    for (int j = 0; j < 4; ++j)
+      if (wave % kChunks == c && (wave / kChunks) % 4 == j) s = v[c][j];  // wave-uniform choice
+  const uint32_t sk = float_key(s);
+  const bool sp = sk > kKeyInvalidMax;  // present: > -1e30, not NaN
+  if (sp) atomicAdd(&shc[sk >> 22], 1u);
+  // Parked in LDS for the fine level: no register held across the retries.
+  lds[kLdsSample + tid] = sp ? sk : 0u;
+  const uint32_t wave_present = (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(sp));  // all lanes vote
+  if (lane == 0) red[kRedPresent + wave] = wave_present;
+  __syncthreads();
+  const int s_present = (int)row0_sum(lane < kTopkWaves ? red[kRedPresent + lane] : 0u);
+
+  // 3. Threshold and candidate compaction.  Sample rank r aims at
+  // (k + kCandCap) / 2 candidates; r > s_present admits every present score.
+  const float floor_t = __uint_as_float(kFloorBits);
+  const int span = 4 * kTopkThreads * kChunks;  // positions the sample stands for
+  int lo = 0, hi = s_present + 1;
+  int r = (int)(((int64_t)((k + kCandCap) / 2) * kTopkThreads + span - 1) / span);
+  r = min(max(r, 1), hi);
+  const uint32_t e4 = 4u * (uint32_t)tid;
+  const uint32_t wreg = (uint32_t)wave * kWaveCap;
+  uint32_t total = 0, held = 0;
+  bool all_present = false;
+  for (int tries = 0;; ++tries) {
+    all_present = r > s_present;
+    float t = floor_t;
+    if (!all_present) {  // block-uniform
+      if (wave == 0) {
+        if (tries > 0) reinterpret_cast<u32x4*>(shf)[lane] = u32x4{0u, 0u, 0u, 0u},
+                       reinterpret_cast<u32x4*>(shf)[lane + 64] = u32x4{0u, 0u, 0u, 0u},
+                       reinterpret_cast<u32x4*>(shf)[lane + 128] = u32x4{0u, 0u, 0u, 0u},
+                       reinterpret_cast<u32x4*>(shf)[lane + 192] = u32x4{0u, 0u, 0u, 0u};
+        uint32_t above;
+        const int bc = rank_bin(shc, (uint32_t)r, above);
+        if (lane == 0) { red[kRedCoarse] = (uint32_t)bc; red[kRedAbove] = above; }
+      }
+      __syncthreads();
+      const uint32_t bc = red[kRedCoarse];
+      const uint32_t skl = lds[kLdsSample + tid];  // 0 (absent) never matches: present keys sit in coarse bins >= 58
+      if ((skl >> 22) == bc) atomicAdd(&shf[(skl >> 12) & (kSampleBins - 1)], 1u);
+      __syncthreads();
+      if (wave == 0) {
+        uint32_t above2;
+        const int bf = rank_bin(shf, (uint32_t)r - red[kRedAbove], above2);
+        if (lane == 0) red[kRedThresh] = (bc << 22) | ((uint32_t)bf << 12);
+      }
+      __syncthreads();
+      t = fmaxf(key_to_float(red[kRedThresh]), floor_t);
     }
-  present = (uint32_t)wave_sum_i((int)present);
-  vmin = -wave_max(-vmin);
-  vmax = wave_max(vmax);
-  if (lane == 0) {
-    red[wave] = present;
-    red[16 + wave] = __float_as_uint(vmin);
-    red[32 + wave] = __float_as_uint(vmax);
-  }
-  __syncthreads();
-  uint32_t m_total = 0;
-  vmin = __builtin_huge_valf();
-  vmax = -__builtin_huge_valf();
-#pragma unroll
-  for (int w = 0; w < kTopkWaves; ++w) {
-    m_total += red[w];
-    vmin = fminf(vmin, __uint_as_float(red[16 + w]));
-    vmax = fmaxf(vmax, __uint_as_float(red[32 + w]));
-  }
-  const int kk = min((int)m_total, k);
-  const float inv = 2048.f / (vmax - vmin);
-  // Degenerate ranges go to the exact path (a single distinct value, or a
-  // range whose width or inverse is not a normal finite number).
-  if (kk > 0 && !(vmax > vmin && inv < 3.0e38f && inv > 0.f)) {
-    if (tid == 0) oi[0] = kFallbackFlag;
-    return;  // block-uniform
-  }
-  __syncthreads();
-
-  // 3. Histogram of bin(v) = min(2047, (int)((v - vmin) * inv)).
-  if (kk > 0) {
-#pragma unroll
-    for (int c = 0; c < kChunks; ++c)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (v[c][j] > -1e30f) atomicAdd(&cnt[min(kHistBins - 1, (int)((v[c][j] - vmin) * inv))], 1u);
-  }
-  __syncthreads();
-
-  // 4. Descending scan: offs[b] = number of present scores in bins above b.
-  const int bhi = kHistBins - 1 - 2 * tid, blo = bhi - 1;
-  const uint32_t chi = cnt[bhi], clo = cnt[blo];
-  uint32_t tot;
-  const uint32_t excl = block_excl_scan(chi + clo, red, tot);
-  offs[bhi] = excl;
-  offs[blo] = excl + chi;
-  if (excl < (uint32_t)kk && excl + chi + clo >= (uint32_t)kk) red[kTopkWaves] = (excl + chi >= (uint32_t)kk) ? bhi : blo;
-  // Largest bin at or above b* bounds the rank work; find it after b* is known.
-  __syncthreads();
-  const int bstar = kk > 0 ? (int)red[kTopkWaves] : kHistBins;
-  const uint32_t list_n = kk > 0 ? offs[bstar] + cnt[bstar] : 0;
-  uint32_t bigbin = 0;
-  if (bhi >= bstar) bigbin = max(bigbin, chi);
-  if (blo >= bstar) bigbin = max(bigbin, clo);
-  {
-    uint32_t bm = bigbin;
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) bm = max(bm, (uint32_t)__shfl_xor((int)bm, o, kWave));
-    if (lane == 0) red[kTopkWaves + 1 + wave] = bm;
-  }
-  __syncthreads();
-  uint32_t maxbin = 0;
-#pragma unroll
-  for (int w = 0; w < kTopkWaves; ++w) maxbin = max(maxbin, red[kTopkWaves + 1 + w]);
-  if (kk > 0 && (list_n > (uint32_t)kListCap || maxbin > (uint32_t)kBinCap)) {
-    if (tid == 0) oi[0] = kFallbackFlag;
-    return;  // block-uniform
-  }
-
-  // 5. Scatter the bins >= b* into the list, grouped by bin.
-  if (kk > 0) {
+    uint32_t wcnt = 0;  // wave-uniform
+    // Opaque copy: keeps the 32 positions from being hoisted out of the retry loop as live registers.
+    uint32_t e4o;
+    __asm__ volatile("v_mov_b32 %0, %1" : "=v"(e4o) : "v"(e4));
 #pragma unroll
     for (int c = 0; c < kChunks; ++c)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float val = v[c][j];
-        if (val > -1e30f) {
-          const int b = min(kHistBins - 1, (int)((val - vmin) * inv));
-          if (b >= bstar) {
-            const uint32_t pos = offs[b] + atomicAdd(&fill[b], 1u);
-            const int p = 4 * (tid + c * kTopkThreads) + j;
-            const int idx = imap ? imap[p] : base + p;
-            list[pos] = ((uint64_t)float_key(val) << 32) | (uint32_t)(~(uint32_t)idx);
-          }
+        const bool p = val >= t;
+        const uint64_t m = __builtin_amdgcn_ballot_w64(p);
+        if (p) {
+          const uint32_t i = lane_prefix(m, wreg + wcnt);
+          lv[i] = __float_as_uint(val);
+          lp[i] = e4o + (uint32_t)(4 * kTopkThreads * c + j);
         }
+        wcnt += (uint32_t)__builtin_popcountll(m);
       }
+    // cnt may hold an overrun's positions; clear it for the candidate histogram.
+    reinterpret_cast<u32x4*>(cnt)[tid] = u32x4{0u, 0u, 0u, 0u};
+    if (lane == 0) red[kRedCount + wave] = wcnt;
+    held = min(wcnt, (uint32_t)kWaveCap);
+    __syncthreads();
+    const uint32_t cw = lane < kTopkWaves ? red[kRedCount + lane] : 0u;
+    total = row0_sum(cw);
+    const bool over = __builtin_amdgcn_ballot_w64(cw > (uint32_t)kWaveCap) != 0;
+    if (!over && (all_present || total >= (uint32_t)k)) break;  // block-uniform
+    if (over) hi = r;
+    else lo = r;
+    if (hi - lo <= 1 || tries + 1 == kMaxTries) {
+      if (tid == 0) oi[0] = kFallbackFlag;
+      return;  // block-uniform
+    }
+    r = (lo + hi + 1) / 2;
+  }
+  const int kk = all_present ? min((int)total, k) : k;
+
+  // Each lane takes entries lane + 64 q of its wave's region (a wave's LDS
+  // accesses stay in order), and the block the candidates' key range.
+  float ev[kLaneEntries];
+  uint32_t ep[kLaneEntries];
+  {
+    uint32_t lmin = 0xffffffffu, lmax = 0u;
+#pragma unroll
+    for (int q = 0; q < kLaneEntries; ++q) {
+      const uint32_t i = (uint32_t)(lane + kWave * q);
+      const uint32_t a = wreg + min(i, (uint32_t)kWaveCap - 1);
+      ev[q] = __uint_as_float(lv[a]);
+      ep[q] = lp[a];
+      const uint32_t key = cand_key(ev[q]);
+      if (i < held) { lmin = min(lmin, key); lmax = max(lmax, key); }
+      else ev[q] = -__builtin_huge_valf();
+    }
+    lmax = wave_all_umax(lmax);
+    lmin = ~wave_all_umax(~lmin);
+    if (lane == 0) {
+      red[kRedMin + wave] = lmin;
+      red[kRedMax + wave] = lmax;
+    }
   }
   __syncthreads();
+  const bool wl = lane < kTopkWaves;
+  const uint32_t kmin = ~row0_max(wl ? ~red[kRedMin + lane] : 0u);
+  const uint32_t kmax = row0_max(wl ? red[kRedMax + lane] : 0u);
 
-  // 6. Rank inside the bin; final position = bin offset + rank.
-  for (uint32_t p = tid; p < list_n; p += kTopkThreads) {
-    const uint64_t e = list[p];
-    const float val = key_to_float((uint32_t)(e >> 32));
-    const int b = min(kHistBins - 1, (int)((val - vmin) * inv));
-    const uint32_t lo = offs[b], nb = cnt[b];
-    uint32_t rank = 0;
-    for (uint32_t j = 0; j < nb; ++j) rank += list[lo + j] > e;
-    const uint32_t pos = lo + rank;
-    if (pos < (uint32_t)kk) {
-      oi[pos] = (int32_t)(~(uint32_t)e);
-      if (ov) ov[pos] = val;
+  if (kk > 0) {
+    // 4. Bucket the candidates by order key: bin = (key - kmin) >> sh < 4096.
+    const uint32_t range = kmax - kmin;
+    const int sh = max(0, (range ? 32 - __builtin_clz(range) : 0) - kCandBinBits);
+    uint32_t eb[kLaneEntries];
+#pragma unroll
+    for (int q = 0; q < kLaneEntries; ++q) {
+      eb[q] = (cand_key(ev[q]) - kmin) >> sh;
+      if (ev[q] != -__builtin_huge_valf()) atomicAdd(&cnt[eb[q]], 1u);
+      else eb[q] = 0xffffffffu;
+    }
+    __syncthreads();
+
+    // 5. Descending scan: offs[b] = candidates in bins above b; b* holds the kk-th.
+    {
+      const u32x4 c4 = reinterpret_cast<const u32x4*>(cnt)[kCandBins / 4 - 1 - tid];  // bins 4095-4t .. 4092-4t
+      uint32_t tot;
+      const uint32_t excl = block_excl_scan<false>(c4.x + c4.y + c4.z + c4.w, red + kRedScan, tot);
+      const uint32_t ow = excl, oz = ow + c4.w, oy = oz + c4.z, ox = oy + c4.y;
+      reinterpret_cast<u32x4*>(offs)[kCandBins / 4 - 1 - tid] = u32x4{ox, oy, oz, ow};
+      const uint32_t top = kCandBins - 1 - 4 * tid;
+      const uint32_t ukk = (uint32_t)kk;
+      if (ow < ukk && ox + c4.x >= ukk)
+        red[kRedBstar] = oz >= ukk ? top : oy >= ukk ? top - 1 : ox >= ukk ? top - 2 : top - 3;
+    }
+    __syncthreads();
+    const uint32_t bstar = red[kRedBstar];
+
+    // 6. Regroup bins >= b* by bin (offs[b] then ends at the bin's end); the
+    // position word carries the bin above its 15 position bits.
+#pragma unroll
+    for (int q = 0; q < kLaneEntries; ++q)
+      if (eb[q] != 0xffffffffu && eb[q] >= bstar) {
+        const uint32_t i = atomicAdd(&offs[eb[q]], 1u);
+        lv[i] = __float_as_uint(ev[q]);
+        lp[i] = (eb[q] << kPosBits) | ep[q];
+      }
+    __syncthreads();
+
+    // 7. Rank inside the bin; sorted position = bin start + entries of the bin
+    // that beat this one.  Entry p of the regrouped list lands within its bin's
+    // range, so the stores stay nearly coalesced.
+    const uint32_t list_n = offs[bstar];
+    for (uint32_t p = (uint32_t)tid; p < list_n; p += kTopkThreads) {
+      const float val = __uint_as_float(lv[p]);
+      const uint32_t bp = lp[p];
+      const uint32_t b = bp >> kPosBits;
+      const uint32_t nb = cnt[b];
+      const uint32_t start = offs[b] - nb;
+      uint32_t rank = 0;
+      if (nb > 1) {
+        if (nb > (uint32_t)kBinCap) {
+          red[kRedFlag] = 1;
+          continue;
+        }
+        for (uint32_t j = start; j < start + nb; ++j) {
+          const float u = __uint_as_float(lv[j]);
+          rank += (u > val || (u == val && lp[j] < bp));  // same bin bits: compares positions
+        }
+      }
+      const uint32_t fin = start + rank;
+      if (fin < (uint32_t)kk) {
+        const uint32_t pp = bp & ((1u << kPosBits) - 1);
+        oi[fin] = imap ? imap[pp] : base + (int)pp;
+        if (ov) ov[fin] = val;
+      }
     }
   }
   for (int i = kk + tid; i < k; i += kTopkThreads) {
     oi[i] = -1;
     if (ov) ov[i] = -__builtin_huge_valf();
+  }
+  if (kk > 0) {
+    __syncthreads();
+    if (tid == 0 && red[kRedFlag]) oi[0] = kFallbackFlag;
   }
 }
 
@@ -429,13 +667,20 @@ static hipError_t launch_reg(const float* x, int64_t ld, int64_t rows, int64_t n
                              int32_t* out_idx, float* out_val, int nseg, int64_t seg_len, const int32_t* idx_map,
                              hipStream_t stream) {
   const dim3 grid((unsigned)rows), block(kTopkThreads);
-#define DSA_REG(C)                                                                                                \
-  hipLaunchKernelGGL((topk_reg_kernel<C>), grid, block, 0, stream, x, ld, (int)n, (int)k, row_len, out_idx, out_val, \
-                     nseg, (int)seg_len, idx_map)
-  if (seg_len <= 4 * kTopkThreads) DSA_REG(1);
-  else if (seg_len <= 8 * kTopkThreads) DSA_REG(2);
-  else if (seg_len <= 16 * kTopkThreads) DSA_REG(4);
-  else DSA_REG(8);
+  const int chunks = seg_len <= 4 * kTopkThreads ? 1 : seg_len <= 8 * kTopkThreads ? 2 : seg_len <= 16 * kTopkThreads ? 4 : 8;
+  // Every row (segment) whole and 16-byte aligned: the straight-line load path.
+  const bool full = row_len == nullptr && seg_len == 4 * kTopkThreads * chunks && n == nseg * seg_len &&
+                    (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (ld & 3) == 0;
+#define DSA_REG(C, F)                                                                                         \
+  hipLaunchKernelGGL((topk_reg_kernel<C, F>), grid, block, 0, stream, x, ld, (int)n, (int)k, row_len, out_idx, \
+                     out_val, nseg, (int)seg_len, idx_map)
+#define DSA_REG2(C) \
+  if (full) DSA_REG(C, true); else DSA_REG(C, false)
+  if (chunks == 1) DSA_REG2(1);
+  else if (chunks == 2) DSA_REG2(2);
+  else if (chunks == 4) DSA_REG2(4);
+  else DSA_REG2(8);
+#undef DSA_REG2
 #undef DSA_REG
   return hipGetLastError();
 }
