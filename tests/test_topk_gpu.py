@@ -155,3 +155,24 @@ def test_long_rows_ws_matches_plain_entry(dsa, dev):
                                    ws.data_ptr(), nws, st), "ws")
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+def test_structured_rows_crowd_waves(dsa, dev):
+    # Rows whose top scores sit in a few threads' registers: sorted rows, sorted
+    # runs (the shape of the second stage over segment candidates), and a
+    # pattern repeating every 4096 positions.  The fast path then compacts the
+    # candidates densely instead of per wave; results stay exact.
+    g = torch.Generator().manual_seed(91)
+    n = 32768
+    pos = torch.arange(n)
+    rows = [
+        pos.float(),                                            # ascending
+        -pos.float(),                                           # descending
+        torch.cat([torch.sort(torch.randn(n // 4, generator=g), descending=True).values for _ in range(4)]),
+        torch.randn(n, generator=g) + 10.0 * ((pos % 4096) < 256).float(),
+        torch.randn(n, generator=g) + 10.0 * ((pos % 4096) >= 3840).float(),
+    ]
+    _check(dsa, dev, torch.stack(rows), 2048)
+    runs = torch.stack([torch.cat([torch.sort(torch.randn(2048, generator=g), descending=True).values
+                                   for _ in range(4)]) for _ in range(6)])
+    _check(dsa, dev, runs, 2048)                                # n = 8192: four sorted runs of 2048

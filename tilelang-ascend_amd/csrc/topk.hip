@@ -336,6 +336,13 @@ __device__ __forceinline__ uint32_t wave_all_umax(uint32_t x) {
   return (uint32_t)__builtin_amdgcn_readlane((int)x, kWave - 1);
 }
 
+// The lane index computed afresh (not a value kept live across a loop).
+__device__ __forceinline__ uint32_t fresh_lane() {
+  uint32_t l;
+  __asm__ volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 __device__ __forceinline__ uint32_t lane_prefix(uint64_t m, uint32_t add) {  // add + set bits of m below this lane
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, add));
 }
@@ -344,6 +351,33 @@ __device__ __forceinline__ uint32_t lane_prefix(uint64_t m, uint32_t add) {  // 
 __device__ __forceinline__ uint32_t cand_key(float x) {
   const uint32_t u = __float_as_uint(x + 0.0f);
   return u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
+}
+
+// Ballot compaction of the scores >= t among a thread's registers into
+// lv/lp from index `base` on (wave-uniform), in register order; returns the
+// wave's count.  Position of register (c, j): e4 + 4096 c + j.
+template <int kChunks>
+__device__ __forceinline__ uint32_t compact_scores(const float (&v)[kChunks][4], float t, uint32_t base, uint32_t e4,
+                                                   uint32_t* lv, uint32_t* lp) {
+  uint32_t wcnt = 0;  // wave-uniform
+  // Opaque copy: keeps the 32 positions from being hoisted out of a retry loop as live registers.
+  uint32_t e4o;
+  __asm__ volatile("v_mov_b32 %0, %1" : "=v"(e4o) : "v"(e4));
+#pragma unroll
+  for (int c = 0; c < kChunks; ++c)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float val = v[c][j];
+      const bool p = val >= t;
+      const uint64_t m = __builtin_amdgcn_ballot_w64(p);
+      if (p) {
+        const uint32_t i = lane_prefix(m, base + wcnt);
+        lv[i] = __float_as_uint(val);
+        lp[i] = e4o + (uint32_t)(4 * kTopkThreads * c + j);
+      }
+      wcnt += (uint32_t)__builtin_popcountll(m);
+    }
+  return wcnt;
 }
 
 // One wave: the bin of a 1024-bin histogram holding the r-th largest entry
@@ -486,10 +520,11 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
   const uint32_t e4 = 4u * (uint32_t)tid;
   const uint32_t wreg = (uint32_t)wave * kWaveCap;
   uint32_t total = 0, held = 0;
-  bool all_present = false;
+  bool all_present = false, dense = false;
+  float t = floor_t;
   for (int tries = 0;; ++tries) {
     all_present = r > s_present;
-    float t = floor_t;
+    t = floor_t;
     if (!all_present) {  // block-uniform
       if (wave == 0) {
         if (tries > 0) reinterpret_cast<u32x4*>(shf)[lane] = u32x4{0u, 0u, 0u, 0u},
@@ -513,33 +548,24 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
       __syncthreads();
       t = fmaxf(key_to_float(red[kRedThresh]), floor_t);
     }
-    uint32_t wcnt = 0;  // wave-uniform
-    // Opaque copy: keeps the 32 positions from being hoisted out of the retry loop as live registers.
-    uint32_t e4o;
-    __asm__ volatile("v_mov_b32 %0, %1" : "=v"(e4o) : "v"(e4));
-#pragma unroll
-    for (int c = 0; c < kChunks; ++c)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float val = v[c][j];
-        const bool p = val >= t;
-        const uint64_t m = __builtin_amdgcn_ballot_w64(p);
-        if (p) {
-          const uint32_t i = lane_prefix(m, wreg + wcnt);
-          lv[i] = __float_as_uint(val);
-          lp[i] = e4o + (uint32_t)(4 * kTopkThreads * c + j);
-        }
-        wcnt += (uint32_t)__builtin_popcountll(m);
-      }
+    const uint32_t wcnt = compact_scores<kChunks>(v, t, wreg, e4, lv, lp);
     // cnt may hold an overrun's positions; clear it for the candidate histogram.
     reinterpret_cast<u32x4*>(cnt)[tid] = u32x4{0u, 0u, 0u, 0u};
     if (lane == 0) red[kRedCount + wave] = wcnt;
     held = min(wcnt, (uint32_t)kWaveCap);
     __syncthreads();
-    const uint32_t cw = lane < kTopkWaves ? red[kRedCount + lane] : 0u;
+    const uint32_t fl = fresh_lane();
+    const uint32_t cw = fl < kTopkWaves ? red[kRedCount + fl] : 0u;
     total = row0_sum(cw);
     const bool over = __builtin_amdgcn_ballot_w64(cw > (uint32_t)kWaveCap) != 0;
-    if (!over && (all_present || total >= (uint32_t)k)) break;  // block-uniform
+    const bool enough = all_present || total >= (uint32_t)k;
+    if (!over && enough) break;  // block-uniform
+    // Candidates crowded into some waves (sorted runs, say) but few enough in
+    // all: compact them again, densely at per-wave prefix offsets.
+    if (enough && total <= (uint32_t)kCandCap) {
+      dense = true;
+      break;
+    }
     if (over) hi = r;
     else lo = r;
     if (hi - lo <= 1 || tries + 1 == kMaxTries) {
@@ -549,21 +575,34 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
     r = (lo + hi + 1) / 2;
   }
   const int kk = all_present ? min((int)total, k) : k;
+  if (dense) {  // block-uniform
+    uint32_t cw = lane < kTopkWaves ? red[kRedCount + lane] : 0u;
+    const uint32_t own = cw;
+    cw += (uint32_t)DSA_DPP(0, cw, 0x111, 0xf);
+    cw += (uint32_t)DSA_DPP(0, cw, 0x112, 0xf);
+    cw += (uint32_t)DSA_DPP(0, cw, 0x114, 0xf);
+    cw += (uint32_t)DSA_DPP(0, cw, 0x118, 0xf);
+    const uint32_t start = (uint32_t)__builtin_amdgcn_readlane((int)(cw - own), wave);
+    (void)compact_scores<kChunks>(v, t, start, e4, lv, lp);
+    reinterpret_cast<u32x4*>(cnt)[tid] = u32x4{0u, 0u, 0u, 0u};  // the regions' overrun reached it
+    __syncthreads();
+  }
 
   // Each lane takes entries lane + 64 q of its wave's region (a wave's LDS
-  // accesses stay in order), and the block the candidates' key range.
+  // accesses stay in order), or, after a dense compaction, entries tid + 1024 q
+  // of the whole list; and the block the candidates' key range.
   float ev[kLaneEntries];
   uint32_t ep[kLaneEntries];
   {
     uint32_t lmin = 0xffffffffu, lmax = 0u;
 #pragma unroll
     for (int q = 0; q < kLaneEntries; ++q) {
-      const uint32_t i = (uint32_t)(lane + kWave * q);
-      const uint32_t a = wreg + min(i, (uint32_t)kWaveCap - 1);
+      const uint32_t i = dense ? (uint32_t)(tid + kTopkThreads * q) : (uint32_t)(lane + kWave * q);
+      const uint32_t a = dense ? min(i, (uint32_t)kCandCap - 1) : wreg + min(i, (uint32_t)kWaveCap - 1);
       ev[q] = __uint_as_float(lv[a]);
       ep[q] = lp[a];
       const uint32_t key = cand_key(ev[q]);
-      if (i < held) { lmin = min(lmin, key); lmax = max(lmax, key); }
+      if (i < (dense ? total : held)) { lmin = min(lmin, key); lmax = max(lmax, key); }
       else ev[q] = -__builtin_huge_valf();
     }
     lmax = wave_all_umax(lmax);
