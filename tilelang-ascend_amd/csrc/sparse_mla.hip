@@ -20,22 +20,27 @@
 // Gather.  The workgroup first turns its slots into physical KV row numbers
 // (index -> validity -> block table) in LDS, once.  Tiles of 32 slots then
 // stream HBM -> LDS with global_load_lds_dwordx4 (no VGPR staging) through a
-// 4-stage ring, three tiles ahead of the MFMAs; each wave waits on its own
-// vmcnt, then a barrier publishes the tile.  A tile is chunk-major: the
-// 16-byte chunk c of all 32 slots is contiguous (slot index XOR-swizzled by
-// 4*(c & 1)), so a lane always serves the same slot, and both the 16-slot MFMA
+// 4-stage ring, up to three tiles ahead of the MFMAs; each wave waits on its
+// own vmcnt, then a barrier publishes the tile.  A tile is 36 blocks of 1 KB,
+// each 8 slots x 8 chunks of 16 bytes, XOR-swizzled (lds_swizzle below): one
+// DMA instruction fetches 8 whole 128-byte lines, and both the 16-slot MFMA
 // operand reads and the transposed V reads are bank-conflict free.  Empty /
-// masked slots re-load a valid row of the same workgroup and get probability 0.
+// masked slots re-load a valid row of the same workgroup and get probability 0;
+// leading tiles with no valid slot are skipped.
 //
 // Math per tile and wave: S^T = K Q^T with the 32 keys on the MFMA M axis
-// (18 x 2 v_mfma_f32_16x16x32_bf16 over d = 576), so each lane ends up with 8
-// scores of one head; softmax in base 2 against a reference max fixed by the
-// first valid tile (plus a bias: 2^60 for bf16), so O is never rescaled in the loop (a
-// score beyond the representable headroom sends the workgroup to an exact
-// two-pass fallback); P to bf16 is the
-// lane's own A operand of O += P V, and V comes straight from the row-major
-// tile through ds_read_b64_tr_b16 (4x4 transposes across lane quads), two
-// reads per 16 output columns.  With more than one split a workgroup writes a
+// (18 x 2 v_mfma_f32_16x16x32_bf16 over d = 576, two accumulator chains), so
+// each lane ends up with 8 scores of one head; softmax in base 2 against a
+// reference max fixed by the first valid tile (plus a bias: 2^60 for bf16), so
+// O is never rescaled in the loop (a score beyond the representable headroom
+// sends the workgroup to an exact two-pass fallback).  P to bf16 is the lane's
+// own B operand of O^T += V^T P^T; V^T comes straight from the row-major tile
+// through ds_read_b64_tr_b16 (4x4 transposes across lane quads), two reads per
+// 16 output columns, and each lane ends up holding 8 consecutive output
+// columns of one head, stored straight from registers.  The tile loop runs in
+// two phases: the QK MFMAs of tile t+1 with the DMA of tile t+kDepth spread
+// between them, then the PV MFMAs of tile t with the softmax of tile t+1 cut
+// into slices between them.  With more than one split a workgroup writes a
 // normalised bf16 partial and its LSE; a combine kernel merges them.
 #include "common.hpp"
 
