@@ -16,10 +16,19 @@
 // 16 heads x 16 keys (K = D = 128 in a single instruction); fp16/bf16 inputs use
 // D/32 16x16x32 MFMAs.  The K dimension is read with the same lane -> byte
 // mapping for A and B, so the dot products do not depend on the hardware's
-// internal K order.  Epilogue in registers: ReLU, multiply by w[t, h], sum the
-// lane's 4 head rows, then two cross-lane adds over the 4 row groups; after
-// four 16-key slices lane l holds key l of the 64-key tile, so each token's
-// logits go out as one coalesced 256-byte store.
+// internal K order.  k tiles stream two ahead through a 3-buffer LDS ring,
+// one barrier per tile.
+//
+// Head reduction.  fp8: on the matrix cores.  The scores leave the QK MFMA
+// scaled by 2^-9 (its E8M0 A scale; fp8 scores are bounded, so they fit f16),
+// go to f16 and through ReLU in packed form (v_cvt_pk_f16_f32, v_pk_max_f16),
+// and form the B operand of a 16x16x32 f16 MFMA whose A operand holds the
+// token's 32 head weights (f16, times a per-token power of two) in every row:
+// every row of the result is sum_h w[h] ReLU(S[h][key]), accumulated in fp32,
+// two MFMAs per 64 heads.  bf16/fp16 inputs (unbounded scores): fp32 ReLU,
+// multiply by w[t, h], sum the lane's 4 head rows, then two cross-lane adds
+// over the 4 row groups.  After four 16-key slices lane l holds key l of the
+// 64-key tile, so each token's logits go out as one coalesced 256-byte store.
 #include "common.hpp"
 
 namespace dsa {
@@ -77,16 +86,21 @@ __device__ __forceinline__ void load_operand_lds(Operand<kKind, kD>& op, const u
   for (int c = 0; c < Operand<kKind, kD>::kPieces; ++c) set_piece(op, c, *reinterpret_cast<const u32x4*>(p + 16 * c));
 }
 
+// fp8 scores come out of the MFMA scaled by 2^-9 (the E8M0 block scale of A is
+// 127 - 9): |q . k| <= 128 * 448^2 < 2^25 for e4m3 inputs, so the scaled
+// score stays below 2^16 and fits f16 for the head-reduction MFMA.
+constexpr int kFp8ScoreShift = 9;
+
 template <int kKind, int kD>
 __device__ __forceinline__ f32x4 mfma_qk(const Operand<kKind, kD>& a, const Operand<kKind, kD>& b) {
   f32x4 c = {0.f, 0.f, 0.f, 0.f};
   if constexpr (Operand<kKind, kD>::kWhole) {
-    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a.v, b.v, c, 0, 0, 0, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a.v, b.v, c, 0, 0, 0, 127 - kFp8ScoreShift, 0, 127);
   } else if constexpr (kKind == kFp8) {
     // One 16x16x128 fp8 MFMA; a D = 64 row leaves half of each lane's K-slice zero.
     const i32x8 av = {(int)a.p[0].x, (int)a.p[0].y, (int)a.p[0].z, (int)a.p[0].w, 0, 0, 0, 0};
     const i32x8 bv = {(int)b.p[0].x, (int)b.p[0].y, (int)b.p[0].z, (int)b.p[0].w, 0, 0, 0, 0};
-    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 0, 0, 0, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 0, 0, 0, 127 - kFp8ScoreShift, 0, 127);
   } else {
 #pragma unroll
     for (int s = 0; s < Operand<kKind, kD>::kPieces; ++s) {
@@ -105,6 +119,28 @@ __device__ __forceinline__ f32x4 mfma_qk(const Operand<kKind, kD>& a, const Oper
 // inputs is far below it.
 __device__ __forceinline__ float relu(float x) { return __builtin_amdgcn_fmed3f(x, 0.f, 3.0e38f); }
 
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// One v_cvt_pk_f16_f32 (round to nearest even).
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+  const f16x2 r = {(_Float16)a, (_Float16)b};
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+// Two scaled scores to f16 (v_cvt_pk_f16_f32), then ReLU on the pair
+// (v_pk_max_f16).
+__device__ __forceinline__ uint32_t relu_f16x2(float a, float b) {
+  const f16x2 r = {(_Float16)a, (_Float16)b};
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(r, f16x2{(_Float16)0.f, (_Float16)0.f}));
+}
+
+// B operand of the head-reduction MFMA for head blocks hb0, hb1: lane (g, r)
+// holds key r's ReLU'd scores of heads 16*hb0 + 4g + i and 16*hb1 + 4g + i
+// (i < 4) as its K = 8g .. 8g+7.
+__device__ __forceinline__ u32x4 relu_operand(const f32x4& c0, const f32x4& c1) {
+  return u32x4{relu_f16x2(c0.x, c0.y), relu_f16x2(c0.z, c0.w), relu_f16x2(c1.x, c1.y), relu_f16x2(c1.z, c1.w)};
+}
+
 struct IdxArgs {
   const uint8_t* q;        // [B, S1, H, 128]
   const uint8_t* k;        // [B, S2, 128] or paged [blocks, block_size, 128]
@@ -121,7 +157,10 @@ struct IdxArgs {
   int key_chunk;
 };
 
-template <int kKind, int kD, int kTokPW>
+// kNhb = H / 16 head blocks, a compile-time count: no branch between the MFMAs.
+// kPaged: keys (and their scales) through the block table; otherwise one
+// contiguous [B, S2] run, addressed from per-thread bases and tile offsets.
+template <int kKind, int kD, int kTokPW, int kNhb, bool kPaged>
 __global__ __launch_bounds__(kIdxThreads) void indexer_logits_kernel(IdxArgs a) {
   constexpr int kRB = IdxTraits<kKind, kD>::kRowBytes;
   constexpr int kLB = IdxTraits<kKind, kD>::kLaneBytes;
@@ -130,7 +169,7 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_logits_kernel(IdxArgs a) 
   constexpr int kTileBytes = kIdxKeyTile * kRB;
   constexpr int kLoads = kTileBytes / 16 / kIdxThreads;  // 16-byte loads per thread per tile
   static_assert(kLoads >= 1, "tile too small");
-  __shared__ __align__(16) uint8_t ktile[2][kIdxKeyTile * kPitch];
+  __shared__ __align__(16) uint8_t ktile[3][kIdxKeyTile * kPitch];  // ring: tile t in buffer t % 3
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -143,7 +182,7 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_logits_kernel(IdxArgs a) 
   const int key1 = min(a.S2, key0 + a.key_chunk);
   const int aq = a.aq_len ? min(max(a.aq_len[b], 0), a.S1) : a.S1;
   const int ak = a.ak_len ? min(max(a.ak_len[b], 0), a.S2) : a.S2;
-  const int nhb = a.H >> 4;
+  constexpr int nhb = kNhb;
 
   // Valid key count per token of this wave (0 for padded rows).
   int nvalid[kTokPW];
@@ -176,68 +215,110 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_logits_kernel(IdxArgs a) 
     }
   }
 
-  // Stationary q operands and head weights.
+  // Stationary q operands and head weights.  fp8: the weights become the A
+  // operands of the head-reduction MFMAs -- every row of A is w (f16), K =
+  // 8g + i standing for head 16*hb0 + 4g + i (i < 4) or 16*hb1 + 4g + i - 4 of
+  // the block pair (hb0, hb1) = (0, 1) or (2, 3), as in relu_operand -- scaled
+  // per token by a power of two that puts max |w| in [2^14, 2^15); post[j]
+  // undoes that scale and the score scale at the store.
+  constexpr bool kMfmaSum = kKind == kFp8;
   Operand<kKind, kD> qa[kTokPW][4];
-  f32x4 wv[kTokPW][4];
+  f32x4 wv[kMfmaSum ? 1 : kTokPW][4];
+  u32x4 wa[kTokPW][2];
+  float post[kTokPW];
 #pragma unroll
   for (int j = 0; j < kTokPW; ++j) {
     const int t = t_base + wave * kTokPW + j;
     const bool tv = t < a.S1;
     const int64_t trow = (int64_t)b * a.S1 + (tv ? t : 0);
+    f32x4 wt[4];
 #pragma unroll
     for (int hb = 0; hb < 4; ++hb) {
       const bool hv = tv && hb < nhb;
       const uint8_t* p = a.q + (trow * a.H + hb * 16 + r) * kRB + g * kLB;
       load_operand_global<kKind, kD>(qa[j][hb], p, hv);
-      wv[j][hb] = hv ? *reinterpret_cast<const f32x4*>(a.w + trow * a.H + hb * 16 + 4 * g) : f32x4{0.f, 0.f, 0.f, 0.f};
+      wt[hb] = hv ? *reinterpret_cast<const f32x4*>(a.w + trow * a.H + hb * 16 + 4 * g) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    if constexpr (kMfmaSum) {
+      float m = 0.f;
+#pragma unroll
+      for (int hb = 0; hb < 4; ++hb)
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(wt[hb].x), fabsf(wt[hb].y)), fmaxf(fabsf(wt[hb].z), fabsf(wt[hb].w))));
+      m = fmaxf(m, __shfl_xor(m, 16, kWave));
+      m = fmaxf(m, __shfl_xor(m, 32, kWave));
+      // m = 2^e * f with f in [1, 2): weights x 2^(14 - e), results x 2^(e - 14 + shift).
+      const int e = m > 0.f ? (int)((__float_as_uint(m) >> 23) & 0xff) - 127 : 0;
+      const float up = __uint_as_float((uint32_t)(127 + 14 - e) << 23);
+      post[j] = __uint_as_float((uint32_t)(127 + e - 14 + kFp8ScoreShift) << 23);
+#pragma unroll
+      for (int pr = 0; pr < 2; ++pr)
+        wa[j][pr] = u32x4{pack_f16x2(wt[2 * pr].x * up, wt[2 * pr].y * up), pack_f16x2(wt[2 * pr].z * up, wt[2 * pr].w * up),
+                          pack_f16x2(wt[2 * pr + 1].x * up, wt[2 * pr + 1].y * up),
+                          pack_f16x2(wt[2 * pr + 1].z * up, wt[2 * pr + 1].w * up)};
+    } else {
+      post[j] = 1.f;
+#pragma unroll
+      for (int hb = 0; hb < 4; ++hb) wv[j][hb] = wt[hb];
     }
   }
 
   const int tile_end = min(key1, max_valid);  // keys at or past this are -inf for every token
   const int ntiles = tile_end > key0 ? (tile_end - key0 + kIdxKeyTile - 1) / kIdxKeyTile : 0;
 
-  // Global -> register staging for one key tile.
-  u32x4 stage[kLoads];
-  auto fetch = [&](int tile) {
+  // Global -> register staging, two tiles in flight: tile t lands in
+  // stage[t & 1] two tiles ahead of its use and goes to LDS one tile ahead.
+  u32x4 stage[2][kLoads];
+  // Thread tid stages 16-byte element tid + 256 i of a tile: key row
+  // tid / (kRB/16) + i * (256 / (kRB/16)), column tid % (kRB/16).
+  constexpr int kRowsPerLoad = kIdxThreads / (kRB / 16);
+  const int kr0 = tid / (kRB / 16);
+  const uint8_t* kthread = a.k + ((int64_t)b * a.S2 + key0 + kr0) * kRB + (tid % (kRB / 16)) * 16;
+  auto fetch = [&](auto slot_c, int tile) {
+    constexpr int slot = decltype(slot_c)::value;
+    const int rows_left = tile_end - key0 - tile * kIdxKeyTile;  // block-uniform
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
-      const int e = tid + i * kIdxThreads;      // 16-byte element of the tile
-      const int kr = e / (kRB / 16);            // key row in tile
-      const int kc = e % (kRB / 16);            // 16-byte column
-      const int s = key0 + tile * kIdxKeyTile + kr;
+      const int kr = kr0 + i * kRowsPerLoad;    // key row in tile
       u32x4 v = {0, 0, 0, 0};
-      if (s < tile_end) {
-        int64_t rowi;
-        if (a.block_table) {
+      if (kr < rows_left) {
+        if constexpr (kPaged) {
+          const int s = key0 + tile * kIdxKeyTile + kr;
           const int blk = a.block_table[(int64_t)b * a.max_blocks + s / a.block_size];
-          rowi = (int64_t)blk * a.block_size + s % a.block_size;
+          const int64_t rowi = (int64_t)blk * a.block_size + s % a.block_size;
+          v = *reinterpret_cast<const u32x4*>(a.k + rowi * kRB + (tid % (kRB / 16)) * 16);
         } else {
-          rowi = (int64_t)b * a.S2 + s;
+          v = *reinterpret_cast<const u32x4*>(kthread + ((int64_t)tile * kIdxKeyTile + i * kRowsPerLoad) * kRB);
         }
-        v = *reinterpret_cast<const u32x4*>(a.k + rowi * kRB + kc * 16);
       }
-      stage[i] = v;
+      stage[slot][i] = v;
     }
   };
-  auto commit = [&](int buf) {
+  auto commit = [&](auto slot_c, int buf) {
+    constexpr int slot = decltype(slot_c)::value;
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
       const int e = tid + i * kIdxThreads;
       const int kr = e / (kRB / 16);
       const int kc = e % (kRB / 16);
-      *reinterpret_cast<u32x4*>(&ktile[buf][kr * kPitch + kc * 16]) = stage[i];
+      *reinterpret_cast<u32x4*>(&ktile[buf][kr * kPitch + kc * 16]) = stage[slot][i];
     }
   };
+  using Slot0 = std::integral_constant<int, 0>;
+  using Slot1 = std::integral_constant<int, 1>;
 
   if (ntiles > 0) {
-    fetch(0);
-    commit(0);
+    fetch(Slot0{}, 0);
+    commit(Slot0{}, 0);
   }
+  if (ntiles > 1) fetch(Slot1{}, 1);
   __syncthreads();
 
-  for (int tile = 0; tile < ntiles; ++tile) {
-    const int buf = tile & 1;
-    if (tile + 1 < ntiles) fetch(tile + 1);
+  // One tile of work; kSlot = tile & 1 (the loop runs two tiles per trip, so
+  // the staging slots are compile-time).
+  auto step = [&](auto slot_c, int tile) {
+    constexpr int slot = decltype(slot_c)::value;
+    const int buf = tile % 3;
+    if (tile + 2 < ntiles) fetch(slot_c, tile + 2);
 
     float res[kTokPW];
 #pragma unroll
@@ -248,29 +329,45 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_logits_kernel(IdxArgs a) 
       load_operand_lds<kKind, kD>(kb, &ktile[buf][(sub * 16 + r) * kPitch + g * kLB]);
 #pragma unroll
       for (int j = 0; j < kTokPW; ++j) {
-        float acc2[2] = {0.f, 0.f};  // two chains: head blocks 0, 2 and 1, 3
+        if constexpr (kMfmaSum) {
+          // sum_h w[h] ReLU(S[h][key]) on the matrix cores: A = w in every row,
+          // B = the ReLU'd scores, so every row of D holds key r's logit.
+          f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int hb = 0; hb < 4; ++hb) {
-          if (hb < nhb) {
-            const f32x4 c = mfma_qk<kKind, kD>(qa[j][hb], kb);
-            float& acc = acc2[hb & 1];
-            acc = fmaf(wv[j][hb].x, relu(c.x), acc);
-            acc = fmaf(wv[j][hb].y, relu(c.y), acc);
-            acc = fmaf(wv[j][hb].z, relu(c.z), acc);
-            acc = fmaf(wv[j][hb].w, relu(c.w), acc);
+          for (int pr = 0; pr < 2; ++pr) {
+            if (2 * pr < nhb) {
+              const f32x4 c0 = mfma_qk<kKind, kD>(qa[j][2 * pr], kb);
+              const f32x4 c1 = 2 * pr + 1 < nhb ? mfma_qk<kKind, kD>(qa[j][2 * pr + 1], kb) : f32x4{0.f, 0.f, 0.f, 0.f};
+              d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, wa[j][pr]),
+                                                         __builtin_bit_cast(f16x8, relu_operand(c0, c1)), d, 0, 0, 0);
+            }
           }
+          res[j] = (g == sub) ? d.x : res[j];
+        } else {
+          float acc2[2] = {0.f, 0.f};  // two chains: head blocks 0, 2 and 1, 3
+#pragma unroll
+          for (int hb = 0; hb < 4; ++hb) {
+            if (hb < nhb) {
+              const f32x4 c = mfma_qk<kKind, kD>(qa[j][hb], kb);
+              float& acc = acc2[hb & 1];
+              acc = fmaf(wv[j][hb].x, relu(c.x), acc);
+              acc = fmaf(wv[j][hb].y, relu(c.y), acc);
+              acc = fmaf(wv[j][hb].z, relu(c.z), acc);
+              acc = fmaf(wv[j][hb].w, relu(c.w), acc);
+            }
+          }
+          float acc = acc2[0] + acc2[1];
+          acc += __shfl_xor(acc, 16, kWave);
+          acc += __shfl_xor(acc, 32, kWave);
+          res[j] = (g == sub) ? acc : res[j];
         }
-        float acc = acc2[0] + acc2[1];
-        acc += __shfl_xor(acc, 16, kWave);
-        acc += __shfl_xor(acc, 32, kWave);
-        res[j] = (g == sub) ? acc : res[j];
       }
     }
     // Lane l now holds key (tile*64 + l) for each token.
     const int s = key0 + tile * kIdxKeyTile + lane;
     float sc = 1.f;
     if (a.k_scale && s < tile_end) {
-      if (a.block_table) {
+      if constexpr (kPaged) {
         const int blk = a.block_table[(int64_t)b * a.max_blocks + s / a.block_size];
         sc = a.k_scale[(int64_t)blk * a.block_size + s % a.block_size];
       } else {
@@ -281,15 +378,17 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_logits_kernel(IdxArgs a) 
     for (int j = 0; j < kTokPW; ++j) {
       const int t = t_base + wave * kTokPW + j;
       if (t < a.S1 && s < key1) {
-        const float v = (s < nvalid[j]) ? res[j] * sc : -__builtin_huge_valf();
+        const float v = (s < nvalid[j]) ? res[j] * (sc * post[j]) : -__builtin_huge_valf();
         __builtin_nontemporal_store(v, &a.logits[((int64_t)b * a.S1 + t) * a.ld + s]);
       }
     }
-    if (tile + 1 < ntiles) {
-      __syncthreads();
-      commit(buf ^ 1);
-      __syncthreads();
-    }
+    // Buffer (tile + 1) % 3 was last read two tiles ago, before the previous barrier.
+    if (tile + 1 < ntiles) commit(std::integral_constant<int, slot ^ 1>{}, (tile + 1) % 3);
+    __syncthreads();
+  };
+  for (int tile = 0; tile < ntiles; tile += 2) {
+    step(Slot0{}, tile);
+    if (tile + 1 < ntiles) step(Slot1{}, tile + 1);
   }
 
   // Keys of this chunk past every token's bound: -inf.
@@ -309,7 +408,17 @@ static hipError_t launch_indexer_kind(const IdxArgs& a, int B, hipStream_t strea
   constexpr int kTokPW = 2;
   constexpr int kTok = kTokPW * kIdxWaves;
   const dim3 grid((unsigned)((a.S2 + a.key_chunk - 1) / a.key_chunk), (unsigned)((a.S1 + kTok - 1) / kTok), (unsigned)B);
-  hipLaunchKernelGGL((indexer_logits_kernel<kKind, kD, kTokPW>), grid, dim3(kIdxThreads), 0, stream, a);
+#define DSA_IDX(N, P) hipLaunchKernelGGL((indexer_logits_kernel<kKind, kD, kTokPW, N, P>), grid, dim3(kIdxThreads), 0, stream, a)
+#define DSA_IDX2(N) \
+  if (a.block_table) DSA_IDX(N, true); else DSA_IDX(N, false)
+  switch (a.H >> 4) {
+    case 1: DSA_IDX2(1); break;
+    case 2: DSA_IDX2(2); break;
+    case 3: DSA_IDX2(3); break;
+    default: DSA_IDX2(4); break;
+  }
+#undef DSA_IDX2
+#undef DSA_IDX
   return hipGetLastError();
 }
 
