@@ -85,7 +85,7 @@ int dsa_topk_select_ws(const float* x, int64_t ld, int64_t rows, int64_t n, int6
  *  block_table [B, max_blocks] int32 or NULL
  *  sparse_mode 0 (no mask) or 3 (causal, bottom-right aligned)
  *  logits   [B, S1, ld] fp32, ld >= S2
- * H % 16 == 0 and H <= 64.
+ * 1 <= H <= 64 (the reference's N1 <= 64, lightning_indexer.py:1282-1283).
  */
 int dsa_indexer_logits(int kind, const void* q, const void* k, const float* k_scale, const float* weights,
                        int64_t B, int64_t S1, int64_t S2, int64_t H, int64_t D, const int32_t* actual_q_len,
@@ -109,6 +109,47 @@ int dsa_lightning_indexer(int kind, const void* q, const void* k, const float* k
                           const int32_t* actual_k_len, const int32_t* block_table, int64_t block_size,
                           int64_t max_blocks, int sparse_mode, int64_t sparse_count, int32_t* out_idx,
                           float* out_val, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Packed (TND) query rows.  The reference converts TND to padded BSND on the
+ * host and back (examples/deepseek_v4/lightning_indexer.py:48-190 helpers,
+ * used at :1257-1268 and :1363-1368); here the kernels address the packed rows
+ * directly.  Batch b owns query rows cu_q[b-1] .. cu_q[b]-1 (cu_q[-1] = 0):
+ *  q        [T, H, D], weights [T, H] fp32, T = cu_q[B-1]
+ *  cu_q     [B] int32 inclusive prefix sums of the query lengths
+ *           (actual_seq_lengths_query of layout "TND")
+ *  keys, either packed (cu_k != NULL, layout "TND"):
+ *           k [Tk, D], k_scale [Tk] or NULL, cu_k [B] prefix sums
+ *  or paged (block_table != NULL, layout "PA_BSND"):
+ *           k [num_blocks, block_size, D], actual_k_len [B] per-batch lengths
+ *  S1_max   >= every query length; S2_max >= every key length (grid bounds)
+ *  logits   [T, ld] fp32, ld >= S2_max
+ * The logits of a row are those of its (b, t) row in the padded layout.
+ */
+int dsa_indexer_logits_tnd(int kind, const void* q, const void* k, const float* k_scale, const float* weights,
+                           int64_t B, int64_t T, int64_t S1_max, int64_t S2_max, int64_t H, int64_t D,
+                           const int32_t* cu_q, const int32_t* cu_k, const int32_t* actual_k_len,
+                           const int32_t* block_table, int64_t block_size, int64_t max_blocks, int sparse_mode,
+                           float* logits, int64_t ld, void* stream);
+
+/* Workspace bytes dsa_lightning_indexer_tnd needs for T packed query rows. */
+size_t dsa_lightning_indexer_tnd_workspace_size(int64_t T, int64_t S2_max, int64_t sparse_count);
+
+/*
+ * Lightning indexer over packed (TND) query rows: the `lightning_indexer`
+ * wrapper with layout_query "TND" (examples/deepseek_v4/lightning_indexer.py:1202-1370),
+ * arguments as dsa_indexer_logits_tnd.
+ *  out_idx [T, sparse_count] int32 (the reference's [T, 1, K])
+ *  out_val [T, sparse_count] fp32 or NULL
+ * With S2_max == 0 nothing is launched and the outputs are left to the caller
+ * (the reference fills -1 / -inf on that early exit, :1287-1294).
+ */
+int dsa_lightning_indexer_tnd(int kind, const void* q, const void* k, const float* k_scale, const float* weights,
+                              int64_t B, int64_t T, int64_t S1_max, int64_t S2_max, int64_t H, int64_t D,
+                              const int32_t* cu_q, const int32_t* cu_k, const int32_t* actual_k_len,
+                              const int32_t* block_table, int64_t block_size, int64_t max_blocks, int sparse_mode,
+                              int64_t sparse_count, int32_t* out_idx, float* out_val, void* workspace,
+                              size_t workspace_bytes, void* stream);
 
 /* Workspace bytes dsa_sparse_mla_fwd needs (0 when no split of the index list is used). */
 size_t dsa_sparse_mla_workspace_size(int64_t B, int64_t S, int64_t H, int64_t topk);

@@ -40,6 +40,9 @@ How each function is pinned (see ``tests/test_oracle.py``):
   ``torch.logsumexp``.
 * ``fp8_quantize_per_token``: absmax maps to 448, representable values round
   trip exactly.
+* ``tnd_to_padded`` / ``padded_to_tnd`` (packed TND layout,
+  ``examples/deepseek_v4/lightning_indexer.py:48-190``): a hand-worked row map
+  with an empty batch, round trips both ways, and the zero fill of padding.
 """
 from __future__ import annotations
 
@@ -193,6 +196,78 @@ def lightning_indexer(
     B, S1, S2 = logits.shape
     idx, val = topk_stable(logits.view(B * S1, S2), sparse_count)
     return idx.view(B, S1, 1, sparse_count), val.view(B, S1, 1, sparse_count), logits
+
+
+# ----------------------------------------------------------------------------
+# Packed (TND) layout: prefix sums <-> padded BSND rows
+# ----------------------------------------------------------------------------
+def prefix_to_lengths(cu: Sequence[int]) -> list:
+    """Inclusive prefix sums -> per-batch lengths
+    (examples/deepseek_v4/lightning_indexer.py:68-71, :136-138)."""
+    cu = [int(x) for x in cu]
+    return [cu[0]] + [cu[i] - cu[i - 1] for i in range(1, len(cu))]
+
+
+def tnd_to_padded(x: torch.Tensor, cu: Sequence[int], S: Optional[int] = None) -> Tuple[torch.Tensor, list]:
+    """Packed rows [T, ...] -> padded [B, S, ...] (zero fill) and the lengths.
+
+    Batch b owns packed rows cu[b-1] .. cu[b]-1 (cu[-1] = 0); padded row (b, s)
+    is packed row cu[b-1] + s for s < len[b].  S defaults to the longest length
+    (examples/deepseek_v4/lightning_indexer.py:48-94, :127-163).
+    """
+    lens = prefix_to_lengths(cu)
+    S = max(lens) if S is None else S
+    out = torch.zeros((len(lens), S) + tuple(x.shape[1:]), dtype=x.dtype)
+    start = 0
+    for b, n in enumerate(lens):
+        out[b, :n] = x[start:start + n]
+        start += n
+    return out, lens
+
+
+def padded_to_tnd(x: torch.Tensor, lens: Sequence[int]) -> torch.Tensor:
+    """Padded [B, S, ...] -> packed [sum(lens), ...], dropping padding rows
+    (examples/deepseek_v4/lightning_indexer.py:166-190)."""
+    parts = [x[b, :int(n)] for b, n in enumerate(lens)]
+    return torch.cat(parts) if parts else x.reshape((0,) + tuple(x.shape[2:]))
+
+
+def lightning_indexer_tnd(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    weights: torch.Tensor,
+    cu_q: Sequence[int],
+    k_scale: Optional[torch.Tensor] = None,
+    *,
+    cu_k: Optional[Sequence[int]] = None,
+    actual_k_len: Optional[Sequence[int]] = None,
+    sparse_count: int = 2048,
+    sparse_mode: int = 3,
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """TND query rows: (indices [T, 1, K], values [T, 1, K], logits [T, S2]).
+
+    q [T, H, D], weights [T, H], cu_q prefix sums.  Keys either packed
+    (k [Tk, D] or [Tk, 1, D], k_scale [Tk], cu_k prefix sums) or padded per
+    batch (k [B, S2, D], k_scale [B, S2], actual_k_len lengths) -- the paged
+    layout reduces to the latter.  The wrapper's conversion, then the BSND
+    golden, then the packed output (examples/deepseek_v4/lightning_indexer.py:1257-1368).
+    """
+    qp, q_lens = tnd_to_padded(q, cu_q)
+    wp, _ = tnd_to_padded(weights, cu_q)
+    if cu_k is not None:
+        if k.dim() == 3:
+            k = k[:, 0, :]
+        kp, k_lens = tnd_to_padded(k, cu_k)
+        sp = None if k_scale is None else tnd_to_padded(k_scale, cu_k)[0]
+    else:
+        kp, sp = (k[:, :, 0, :] if k.dim() == 4 else k), k_scale
+        k_lens = [int(x) for x in actual_k_len]
+    logits = indexer_logits(qp, kp, wp, sp, actual_q_len=q_lens, actual_k_len=k_lens, sparse_mode=sparse_mode)
+    B, S1, S2 = logits.shape
+    idx, val = topk_stable(logits.reshape(B * S1, S2), sparse_count)
+    idx, val = idx.view(B, S1, sparse_count), val.view(B, S1, sparse_count)
+    return (padded_to_tnd(idx, q_lens).unsqueeze(1), padded_to_tnd(val, q_lens).unsqueeze(1),
+            padded_to_tnd(logits, q_lens))
 
 
 # ----------------------------------------------------------------------------

@@ -241,3 +241,39 @@ def test_causal_sparse_indices_are_unique_and_in_range():
         assert torch.unique(valid).numel() == valid.numel()
         assert int(valid.max()) <= 256 - 64 + t
         assert torch.all(row[valid.numel():] == -1)
+
+
+def test_tnd_row_map_hand_worked():
+    # Prefix sums [2, 2, 5]: lengths [2, 0, 3]; packed rows 0,1 -> batch 0, rows 2..4 -> batch 2.
+    x = torch.tensor([[1.0], [2.0], [3.0], [4.0], [5.0]])
+    padded, lens = ref.tnd_to_padded(x, [2, 2, 5])
+    assert lens == [2, 0, 3]
+    assert torch.equal(padded[..., 0], torch.tensor([[1.0, 2.0, 0.0], [0.0, 0.0, 0.0], [3.0, 4.0, 5.0]]))
+    assert torch.equal(ref.padded_to_tnd(padded, lens), x)
+    # Uniform lengths: packing is a reshape.
+    y = torch.randn(12, 3, 4)
+    p2, l2 = ref.tnd_to_padded(y, [4, 8, 12])
+    assert l2 == [4, 4, 4] and torch.equal(p2, y.view(3, 4, 3, 4))
+
+
+def test_tnd_indexer_equals_per_batch_bsnd():
+    # Each batch of a ragged packed call equals a one-batch BSND call on its own rows.
+    g = torch.Generator().manual_seed(5)
+    q_lens, k_lens = [3, 0, 5], [9, 4, 12]
+    H, D, K = 2, 8, 6
+    q = torch.randn(sum(q_lens), H, D, generator=g)
+    k = torch.randn(sum(k_lens), D, generator=g)
+    w = torch.randn(sum(q_lens), H, generator=g)
+    cu_q = list(np.cumsum(q_lens))
+    cu_k = list(np.cumsum(k_lens))
+    idx, val, logits = ref.lightning_indexer_tnd(q, k, w, cu_q, cu_k=cu_k, sparse_count=K, sparse_mode=3)
+    assert idx.shape == (sum(q_lens), 1, K) and logits.shape == (sum(q_lens), max(k_lens))
+    q0 = k0 = 0
+    for aq, ak in zip(q_lens, k_lens):
+        if aq:
+            bi, bv, bl = ref.lightning_indexer(q[q0:q0 + aq][None], k[k0:k0 + ak][None], w[q0:q0 + aq][None],
+                                               sparse_count=K, sparse_mode=3)
+            assert torch.equal(idx[q0:q0 + aq], bi[0])
+            assert torch.equal(logits[q0:q0 + aq, :ak], bl[0])
+            assert torch.all(torch.isneginf(logits[q0:q0 + aq, ak:]))
+        q0, k0 = q0 + aq, k0 + ak

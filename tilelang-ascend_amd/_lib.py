@@ -39,6 +39,13 @@ SIGNATURES = {
     "dsa_lightning_indexer": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                        _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_i64, _c_vp, _c_vp, _c_vp,
                                        _c_size, _c_vp]),
+    "dsa_indexer_logits_tnd": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                        _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_vp, _c_i64,
+                                        _c_vp]),
+    "dsa_lightning_indexer_tnd_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64]),
+    "dsa_lightning_indexer_tnd": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                           _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_i64, _c_vp,
+                                           _c_vp, _c_vp, _c_size, _c_vp]),
     "dsa_sparse_mla_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64]),
     "dsa_sparse_mla_fwd": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64,
                                     _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_float, _c_int, _c_vp, _c_vp, _c_vp,

@@ -11,8 +11,9 @@ hipError_t launch_topk(const float* x, int64_t ld, int64_t rows, int64_t n, int6
 size_t topk_workspace_bytes(int64_t rows, int64_t n, int64_t k);
 hipError_t launch_indexer_logits(int kind, const void* q, const void* k, const float* k_scale, const float* w,
                                  int64_t B, int64_t S1, int64_t S2, int64_t H, int64_t D, const int32_t* aq_len,
-                                 const int32_t* ak_len, const int32_t* block_table, int64_t block_size,
-                                 int64_t max_blocks, int sparse_mode, float* logits, int64_t ld, hipStream_t stream);
+                                 const int32_t* ak_len, const int32_t* cu_q, const int32_t* cu_k,
+                                 const int32_t* block_table, int64_t block_size, int64_t max_blocks, int sparse_mode,
+                                 float* logits, int64_t ld, hipStream_t stream);
 hipError_t launch_sparse_mla(int is_fp16, const void* q, const void* kv, const int32_t* indices, const int32_t* block_table,
                              const int32_t* q_len, const int32_t* kv_len, int64_t B, int64_t S, int64_t H,
                              int64_t Skv, int64_t block_size, int64_t max_blocks, int64_t topk, float sm_scale,
@@ -38,7 +39,7 @@ constexpr int64_t kMaxInt = 0x7fffffff;
 
 extern "C" {
 
-int dsa_abi_version(void) { return 101; }
+int dsa_abi_version(void) { return 102; }
 
 const char* dsa_last_error_message(void) { return g_msg; }
 
@@ -80,7 +81,7 @@ static int check_indexer(int kind, const void* q, const void* k, const float* we
                          int64_t max_blocks, int sparse_mode) {
   if (kind != DSA_KIND_FP8_E4M3 && kind != DSA_KIND_BF16 && kind != DSA_KIND_FP16) return reject("indexer: bad kind");
   if (D != 128 && D != 64) return reject("indexer: head dim D must be 64 or 128");
-  if (H < 16 || H > 64 || H % 16 != 0) return reject("indexer: H must be 16, 32, 48 or 64");
+  if (H < 1 || H > 64) return reject("indexer: H must be in [1, 64]");
   if (B < 0 || S1 < 0 || S2 < 0 || B > 65535 || S1 > kMaxInt || S2 > kMaxInt) return reject("indexer: bad sizes");
   if (sparse_mode != 0 && sparse_mode != 3) return reject("indexer: sparse_mode must be 0 or 3");
   if (block_table && (block_size <= 0 || max_blocks <= 0 || block_size * max_blocks < S2))
@@ -98,7 +99,7 @@ int dsa_indexer_logits(int kind, const void* q, const void* k, const float* k_sc
   if (ld < S2) return reject("indexer: ld < S2");
   if (B * S1 * S2 > 0 && !logits) return reject("indexer: null logits");
   return ok(dsa::launch_indexer_logits(kind, q, k, k_scale, weights, B, S1, S2, H, D, actual_q_len, actual_k_len,
-                                       block_table, block_size, max_blocks, sparse_mode, logits, ld,
+                                       nullptr, nullptr, block_table, block_size, max_blocks, sparse_mode, logits, ld,
                                        static_cast<hipStream_t>(stream)));
 }
 
@@ -130,12 +131,74 @@ int dsa_lightning_indexer(int kind, const void* q, const void* k, const float* k
   float* logits = static_cast<float*>(workspace);
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e = dsa::launch_indexer_logits(kind, q, k, k_scale, weights, B, S1, S2, H, D, actual_q_len, actual_k_len,
-                                            block_table, block_size, max_blocks, sparse_mode, logits, ld, st);
+                                            nullptr, nullptr, block_table, block_size, max_blocks, sparse_mode, logits, ld, st);
   if (e != hipSuccess) return ok(e);
   void* cand = dsa::topk_workspace_bytes(B * S1, S2, sparse_count) > 0
                    ? static_cast<void*>(static_cast<uint8_t*>(workspace) + indexer_logits_bytes(B, S1, S2))
                    : nullptr;
   return ok(dsa::launch_topk(logits, ld, B * S1, S2, sparse_count, nullptr, 1, out_idx, out_val, cand, st));
+}
+
+static int check_indexer_tnd(int kind, const void* q, const void* k, const float* weights, int64_t B, int64_t T,
+                             int64_t S1_max, int64_t S2_max, int64_t H, int64_t D, const int32_t* cu_q,
+                             const int32_t* cu_k, const int32_t* actual_k_len, const int32_t* block_table,
+                             int64_t block_size, int64_t max_blocks, int sparse_mode) {
+  int rc = check_indexer(kind, q, k, weights, B, S1_max, S2_max, H, D, block_table, block_size, max_blocks,
+                         sparse_mode);
+  if (rc) return rc;
+  if (T < 0 || T > kMaxInt) return reject("indexer: bad T");
+  if (B > 0 && !cu_q) return reject("indexer: TND query needs cu_q");
+  if ((cu_k != nullptr) == (block_table != nullptr))
+    return reject("indexer: TND keys need exactly one of cu_k (packed) and block_table (paged)");
+  if (block_table && !actual_k_len) return reject("indexer: paged keys need actual_k_len");
+  return 0;
+}
+
+int dsa_indexer_logits_tnd(int kind, const void* q, const void* k, const float* k_scale, const float* weights,
+                           int64_t B, int64_t T, int64_t S1_max, int64_t S2_max, int64_t H, int64_t D,
+                           const int32_t* cu_q, const int32_t* cu_k, const int32_t* actual_k_len,
+                           const int32_t* block_table, int64_t block_size, int64_t max_blocks, int sparse_mode,
+                           float* logits, int64_t ld, void* stream) {
+  int rc = check_indexer_tnd(kind, q, k, weights, B, T, S1_max, S2_max, H, D, cu_q, cu_k, actual_k_len, block_table,
+                             block_size, max_blocks, sparse_mode);
+  if (rc) return rc;
+  if (ld < S2_max) return reject("indexer: ld < S2_max");
+  if (T * S2_max > 0 && !logits) return reject("indexer: null logits");
+  if (T == 0) return 0;
+  return ok(dsa::launch_indexer_logits(kind, q, k, k_scale, weights, B, S1_max, S2_max, H, D, nullptr,
+                                       actual_k_len, cu_q, cu_k, block_table, block_size, max_blocks, sparse_mode,
+                                       logits, ld, static_cast<hipStream_t>(stream)));
+}
+
+size_t dsa_lightning_indexer_tnd_workspace_size(int64_t T, int64_t S2_max, int64_t sparse_count) {
+  return dsa_lightning_indexer_workspace_size(1, T, S2_max, sparse_count);
+}
+
+int dsa_lightning_indexer_tnd(int kind, const void* q, const void* k, const float* k_scale, const float* weights,
+                              int64_t B, int64_t T, int64_t S1_max, int64_t S2_max, int64_t H, int64_t D,
+                              const int32_t* cu_q, const int32_t* cu_k, const int32_t* actual_k_len,
+                              const int32_t* block_table, int64_t block_size, int64_t max_blocks, int sparse_mode,
+                              int64_t sparse_count, int32_t* out_idx, float* out_val, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  int rc = check_indexer_tnd(kind, q, k, weights, B, T, S1_max, S2_max, H, D, cu_q, cu_k, actual_k_len, block_table,
+                             block_size, max_blocks, sparse_mode);
+  if (rc) return rc;
+  if (sparse_count < 1 || sparse_count > 8192) return reject("indexer: sparse_count must be in [1, 8192]");
+  if (workspace_bytes < dsa_lightning_indexer_tnd_workspace_size(T, S2_max, sparse_count))
+    return reject("indexer: workspace too small");
+  if (T > 0 && !out_idx) return reject("indexer: null out_idx");
+  if (T == 0 || S2_max == 0 || B == 0) return 0;
+  const int64_t ld = (S2_max + 3) & ~int64_t(3);
+  float* logits = static_cast<float*>(workspace);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e = dsa::launch_indexer_logits(kind, q, k, k_scale, weights, B, S1_max, S2_max, H, D, nullptr,
+                                            actual_k_len, cu_q, cu_k, block_table, block_size, max_blocks,
+                                            sparse_mode, logits, ld, st);
+  if (e != hipSuccess) return ok(e);
+  void* cand = dsa::topk_workspace_bytes(T, S2_max, sparse_count) > 0
+                   ? static_cast<void*>(static_cast<uint8_t*>(workspace) + indexer_logits_bytes(1, T, S2_max))
+                   : nullptr;
+  return ok(dsa::launch_topk(logits, ld, T, S2_max, sparse_count, nullptr, 1, out_idx, out_val, cand, st));
 }
 
 size_t dsa_sparse_mla_workspace_size(int64_t B, int64_t S, int64_t H, int64_t topk) {

@@ -148,6 +148,11 @@ struct IdxArgs {
   const float* w;          // [B, S1, H] fp32
   const int32_t* aq_len;   // [B] nullable
   const int32_t* ak_len;   // [B] nullable
+  // Packed (TND) rows: inclusive prefix sums of the per-batch lengths, [B];
+  // batch b owns query rows cu_q[b-1] .. cu_q[b]-1 of q / weights / logits and
+  // key rows cu_k[b-1] .. cu_k[b]-1 of k / k_scale.  Null: padded [B, S1] / [B, S2].
+  const int32_t* cu_q;
+  const int32_t* cu_k;
   const int32_t* block_table;  // [B, max_blocks] nullable (non-paged)
   float* logits;           // [B, S1, ld]
   int64_t ld;
@@ -180,8 +185,15 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_logits_kernel(IdxArgs a) 
   const int t_base = blockIdx.y * kTok;
   const int key0 = blockIdx.x * a.key_chunk;
   const int key1 = min(a.S2, key0 + a.key_chunk);
-  const int aq = a.aq_len ? min(max(a.aq_len[b], 0), a.S1) : a.S1;
-  const int ak = a.ak_len ? min(max(a.ak_len[b], 0), a.S2) : a.S2;
+  // Row bases of batch b and its real lengths.  Padded layouts write -inf rows
+  // up to S1; packed rows past the batch's length belong to the next batch.
+  const int64_t q_base = a.cu_q ? (b ? (int64_t)a.cu_q[b - 1] : 0) : (int64_t)b * a.S1;
+  const int64_t k_base = a.cu_k ? (b ? (int64_t)a.cu_k[b - 1] : 0) : (int64_t)b * a.S2;
+  const int aq = a.cu_q ? min(max(a.cu_q[b] - (int)q_base, 0), a.S1)
+                        : (a.aq_len ? min(max(a.aq_len[b], 0), a.S1) : a.S1);
+  const int ak = a.cu_k ? min(max(a.cu_k[b] - (int)k_base, 0), a.S2)
+                        : (a.ak_len ? min(max(a.ak_len[b], 0), a.S2) : a.S2);
+  const int t_rows = a.cu_q ? aq : a.S1;  // rows of this batch that exist in the output
   constexpr int nhb = kNhb;
 
   // Valid key count per token of this wave (0 for padded rows).
@@ -229,15 +241,26 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_logits_kernel(IdxArgs a) 
 #pragma unroll
   for (int j = 0; j < kTokPW; ++j) {
     const int t = t_base + wave * kTokPW + j;
-    const bool tv = t < a.S1;
-    const int64_t trow = (int64_t)b * a.S1 + (tv ? t : 0);
+    const bool tv = t < t_rows;
+    const int64_t trow = q_base + (tv ? t : 0);
     f32x4 wt[4];
 #pragma unroll
     for (int hb = 0; hb < 4; ++hb) {
+      // H need not be a multiple of 16: the last block's missing heads are
+      // zero q rows with zero weight, so they add nothing.
       const bool hv = tv && hb < nhb;
       const uint8_t* p = a.q + (trow * a.H + hb * 16 + r) * kRB + g * kLB;
-      load_operand_global<kKind, kD>(qa[j][hb], p, hv);
-      wt[hb] = hv ? *reinterpret_cast<const f32x4*>(a.w + trow * a.H + hb * 16 + 4 * g) : f32x4{0.f, 0.f, 0.f, 0.f};
+      load_operand_global<kKind, kD>(qa[j][hb], p, hv && hb * 16 + r < a.H);
+      const float* wp = a.w + trow * a.H + hb * 16 + 4 * g;
+      if (!hv) {
+        wt[hb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      } else if ((a.H & 15) == 0) {
+        wt[hb] = *reinterpret_cast<const f32x4*>(wp);
+      } else {
+        const int h0 = hb * 16 + 4 * g;
+        wt[hb] = f32x4{h0 < a.H ? wp[0] : 0.f, h0 + 1 < a.H ? wp[1] : 0.f, h0 + 2 < a.H ? wp[2] : 0.f,
+                       h0 + 3 < a.H ? wp[3] : 0.f};
+      }
     }
     if constexpr (kMfmaSum) {
       float m = 0.f;
@@ -272,7 +295,7 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_logits_kernel(IdxArgs a) 
   // tid / (kRB/16) + i * (256 / (kRB/16)), column tid % (kRB/16).
   constexpr int kRowsPerLoad = kIdxThreads / (kRB / 16);
   const int kr0 = tid / (kRB / 16);
-  const uint8_t* kthread = a.k + ((int64_t)b * a.S2 + key0 + kr0) * kRB + (tid % (kRB / 16)) * 16;
+  const uint8_t* kthread = a.k + (k_base + key0 + kr0) * kRB + (tid % (kRB / 16)) * 16;
   auto fetch = [&](auto slot_c, int tile) {
     constexpr int slot = decltype(slot_c)::value;
     const int rows_left = tile_end - key0 - tile * kIdxKeyTile;  // block-uniform
@@ -371,15 +394,15 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_logits_kernel(IdxArgs a) 
         const int blk = a.block_table[(int64_t)b * a.max_blocks + s / a.block_size];
         sc = a.k_scale[(int64_t)blk * a.block_size + s % a.block_size];
       } else {
-        sc = a.k_scale[(int64_t)b * a.S2 + s];
+        sc = a.k_scale[k_base + s];
       }
     }
 #pragma unroll
     for (int j = 0; j < kTokPW; ++j) {
       const int t = t_base + wave * kTokPW + j;
-      if (t < a.S1 && s < key1) {
+      if (t < t_rows && s < key1) {
         const float v = (s < nvalid[j]) ? res[j] * (sc * post[j]) : -__builtin_huge_valf();
-        __builtin_nontemporal_store(v, &a.logits[((int64_t)b * a.S1 + t) * a.ld + s]);
+        __builtin_nontemporal_store(v, &a.logits[(q_base + t) * a.ld + s]);
       }
     }
     // Buffer (tile + 1) % 3 was last read two tiles ago, before the previous barrier.
@@ -396,8 +419,8 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_logits_kernel(IdxArgs a) 
 #pragma unroll
   for (int j = 0; j < kTokPW; ++j) {
     const int t = t_base + wave * kTokPW + j;
-    if (t < a.S1) {
-      float* row = a.logits + ((int64_t)b * a.S1 + t) * a.ld;
+    if (t < t_rows) {
+      float* row = a.logits + (q_base + t) * a.ld;
       for (int s = masked0 + lane; s < key1; s += kWave) __builtin_nontemporal_store(-__builtin_huge_valf(), &row[s]);
     }
   }
@@ -411,7 +434,7 @@ static hipError_t launch_indexer_kind(const IdxArgs& a, int B, hipStream_t strea
 #define DSA_IDX(N, P) hipLaunchKernelGGL((indexer_logits_kernel<kKind, kD, kTokPW, N, P>), grid, dim3(kIdxThreads), 0, stream, a)
 #define DSA_IDX2(N) \
   if (a.block_table) DSA_IDX(N, true); else DSA_IDX(N, false)
-  switch (a.H >> 4) {
+  switch ((a.H + 15) >> 4) {
     case 1: DSA_IDX2(1); break;
     case 2: DSA_IDX2(2); break;
     case 3: DSA_IDX2(3); break;
@@ -425,9 +448,9 @@ static hipError_t launch_indexer_kind(const IdxArgs& a, int B, hipStream_t strea
 // kind: 0 fp8 e4m3fn, 1 bf16, 2 fp16.  Caller validated: D in {64, 128}, H % 16 == 0, H <= 64.
 hipError_t launch_indexer_logits(int kind, const void* q, const void* k, const float* k_scale, const float* w,
                                  int64_t B, int64_t S1, int64_t S2, int64_t H, int64_t D,
-                                 const int32_t* aq_len, const int32_t* ak_len,
-                                 const int32_t* block_table, int64_t block_size, int64_t max_blocks,
-                                 int sparse_mode, float* logits, int64_t ld, hipStream_t stream) {
+                                 const int32_t* aq_len, const int32_t* ak_len, const int32_t* cu_q,
+                                 const int32_t* cu_k, const int32_t* block_table, int64_t block_size,
+                                 int64_t max_blocks, int sparse_mode, float* logits, int64_t ld, hipStream_t stream) {
   if (B == 0 || S1 == 0 || S2 == 0) return hipSuccess;
   IdxArgs a;
   a.q = static_cast<const uint8_t*>(q);
@@ -436,6 +459,8 @@ hipError_t launch_indexer_logits(int kind, const void* q, const void* k, const f
   a.w = w;
   a.aq_len = aq_len;
   a.ak_len = ak_len;
+  a.cu_q = cu_q;
+  a.cu_k = cu_k;
   a.block_table = block_table;
   a.logits = logits;
   a.ld = ld;
