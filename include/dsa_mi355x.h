@@ -177,6 +177,39 @@ int dsa_sparse_mla_fwd(int kind, const void* q, const void* kv, const int32_t* i
                        int64_t topk, float sm_scale, int is_causal, void* out, float* lse, void* workspace,
                        size_t workspace_bytes, void* stream);
 
+/*
+ * DeepSeek V4 sparse flash MLA (D = 512, K = V, paged caches, attention sinks).
+ * Replaces `sparse_flash_mla(...)` (examples/deepseek_v4/sparse_flash_mla/
+ * sparse_flash_mla_api.py:94-253; semantics of sparse_flash_mla_golden.py:55-160).
+ * Query row t of batch b (q_start[b] <= t < q_start[b] + q_len[b]; rows past a
+ * batch's length are padding: out = 0, lse = 0) at position
+ * s_global = seqused_kv[b] - q_len[b] + (t - q_start[b]) attends to
+ *  - the original rows s_global - ori_win_left .. s_global (clipped at 0),
+ *  - with cmp_kv and no cmp_sparse_indices ("hca"): compressed rows
+ *    0 .. floor((s_global + 1) / cmp_ratio) - 1, at most max_cmp of them,
+ *  - with cmp_sparse_indices [T, topk_cmp] ("csa"): the selected compressed
+ *    rows among the list's first min(topk_cmp, threshold) entries, up to the
+ *    first -1, skipping entries >= threshold,
+ * and the sink of each head adds exp(sinks[h]) to the softmax denominator.
+ *  q [T, H, 512]; caches [block_num, block_size, 512] with tables
+ *  [B, table_len] int32; q_start / q_len / seqused_kv [B] int32 (q_start
+ *  non-decreasing); sinks [H] fp32 (natural-log units) or NULL;
+ *  out [T, H, 512]; lse [T, H] fp32 (natural log, sink included).
+ * H % 16 == 0, H <= 1024 (the reference: H = 64); bf16 or fp16.
+ * cmp_slots of the workspace query: 0 (window only), max_cmp ("hca") or
+ * topk_cmp ("csa").
+ */
+size_t dsa_sparse_flash_mla_workspace_size(int64_t T, int64_t H, int64_t ori_win_left, int64_t cmp_slots);
+
+int dsa_sparse_flash_mla(int kind, const void* q, int64_t T, int64_t H, int64_t D, int64_t B, const int32_t* q_start,
+                         const int32_t* q_len, const int32_t* seqused_kv, const void* ori_kv, int64_t ori_block_num,
+                         int64_t ori_block_size, const int32_t* ori_block_table, int64_t ori_table_len,
+                         const void* cmp_kv, int64_t cmp_block_num, int64_t cmp_block_size,
+                         const int32_t* cmp_block_table, int64_t cmp_table_len, const int32_t* cmp_sparse_indices,
+                         int64_t topk_cmp, int64_t cmp_ratio, int64_t ori_win_left, int64_t max_cmp,
+                         const float* sinks, float softmax_scale, void* out, float* lse, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

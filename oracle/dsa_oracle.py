@@ -40,6 +40,12 @@ How each function is pinned (see ``tests/test_oracle.py``):
   ``torch.logsumexp``.
 * ``fp8_quantize_per_token``: absmax maps to 448, representable values round
   trip exactly.
+* ``v4_slots`` / ``sparse_flash_mla`` (DeepSeek V4 window + compressed
+  attention with sinks, ``examples/deepseek_v4/sparse_flash_mla/sparse_flash_mla_golden.py:15-160``):
+  hand-worked slot lists (window clipping, hca threshold, the csa walk that
+  stops at the first -1 and skips entries past the threshold), a single-key
+  closed form, ``torch.softmax`` / ``torch.logsumexp`` over scores with the
+  sink appended, and a vanishing sink reducing to plain softmax attention.
 * ``tnd_to_padded`` / ``padded_to_tnd`` (packed TND layout,
   ``examples/deepseek_v4/lightning_indexer.py:48-190``): a hand-worked row map
   with an empty batch, round trips both ways, and the zero fill of padding.
@@ -374,6 +380,151 @@ def sparse_mla_dense_ref(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tenso
     p = score.softmax(dim=-1)
     p = torch.nan_to_num(p, nan=0.0)
     return torch.einsum("bshn,bnd->bshd", p, kvf[..., :d_v]).to(torch.float32)
+
+
+# ----------------------------------------------------------------------------
+# DeepSeek V4 sparse flash MLA (window over original KV + compressed KV, sinks)
+# ----------------------------------------------------------------------------
+def v4_slots(s_global: int, *, win_left: int, cmp_ratio: Optional[int] = None, dense_cmp: bool = False,
+             sel: Optional[Sequence[int]] = None) -> Tuple[list, list]:
+    """(original positions, compressed positions) one query row attends to.
+
+    Window: max(s_global - win_left, 0) .. s_global (ori_win_right = 0,
+    sparse_flash_mla_golden.py:103-105); none when s_global < 0.  Compressed,
+    with threshold = floor((s_global + 1) / cmp_ratio) (cmp_mask_mode 3, :27-29):
+    ``dense_cmp`` ("hca") takes 0 .. threshold - 1 (:121-123); ``sel`` ("csa")
+    walks the first min(len(sel), threshold) entries, stops at the first -1 and
+    skips entries >= threshold (:31-45, sparse_block_size 1).  Entries below -1
+    are skipped (the golden would wrap them around as Python indices).
+    """
+    if s_global < 0:
+        return [], []
+    ori = list(range(max(s_global - win_left, 0), s_global + 1))
+    cmp: list = []
+    if cmp_ratio is not None and (dense_cmp or sel is not None):
+        thr = (s_global + 1) // cmp_ratio
+        if dense_cmp:
+            cmp = list(range(thr))
+        else:
+            for i in range(min(len(sel), thr)):
+                tid = int(sel[i])
+                if tid == -1:
+                    break
+                if 0 <= tid < thr:
+                    cmp.append(tid)
+    return ori, cmp
+
+
+def unpack_paged(pool: torch.Tensor, table: torch.Tensor, length: int, b: int) -> torch.Tensor:
+    """Logical rows 0 .. length-1 of batch b from a paged pool [blocks, bs, 1, D]
+    (sparse_flash_mla_golden.py:199-219)."""
+    bs = pool.shape[1]
+    pos = torch.arange(length)
+    blk = table[b].to(torch.int64)[pos // bs]
+    return pool[blk, pos % bs, 0]
+
+
+def _golden_row(q, ori_k, cmp_k, sinks, scale, p_dtype, tile=512):
+    """One row the golden's way (sparse_flash_mla_golden.py:125-150), float32."""
+    H, D = q.shape
+    row_max = sinks.clone() if sinks is not None else torch.full((H,), float("-inf"))
+    row_sum = torch.ones(H) if sinks is not None else torch.zeros(H)
+    acc = torch.zeros((H, D))
+    for part in (ori_k, cmp_k):
+        if part is None or part.shape[0] == 0:
+            continue
+        for t0 in range(0, part.shape[0], tile):
+            k = part[t0:t0 + tile]
+            score = (q @ k.T) * scale
+            old = row_max
+            row_max = torch.maximum(row_max, score.amax(dim=1))
+            alpha = torch.exp(old - row_max)
+            p = torch.exp(score - row_max[:, None])
+            row_sum = alpha * row_sum + p.sum(dim=1)
+            acc = acc * alpha[:, None] + p.to(p_dtype).float() @ k
+    if not torch.isfinite(row_max).all():
+        return torch.zeros((H, D), dtype=torch.float64), torch.full((H,), float("-inf"), dtype=torch.float64)
+    return ((acc / row_sum[:, None]).to(p_dtype).double(), (row_max + torch.log(row_sum)).double())
+
+
+def sparse_flash_mla(
+    q: torch.Tensor,
+    cu_seqlens_q: Sequence[int],
+    seqused_kv: Sequence[int],
+    ori_kv: torch.Tensor,
+    ori_block_table: torch.Tensor,
+    sinks: Optional[torch.Tensor],
+    softmax_scale: float,
+    *,
+    cmp_kv: Optional[torch.Tensor] = None,
+    cmp_block_table: Optional[torch.Tensor] = None,
+    cmp_sparse_indices: Optional[torch.Tensor] = None,
+    cmp_ratio: Optional[int] = None,
+    ori_win_left: int = 127,
+    golden_p_dtype: Optional[torch.dtype] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """V4 attention over packed query rows: (out fp32 [T, H, D], lse fp32 [T, H]).
+
+    q [T, H, D]; cu_seqlens_q [B+1]; paged caches [blocks, bs, 1, D] with
+    tables [B, n]; cmp_sparse_indices [T, 1, K] or [T, K].  For each row the
+    slot list of ``v4_slots`` is gathered (K = V = the row), scores are
+    scale * q.k, and the sink of head h enters the softmax as one more logit
+    with no value row: out = sum_j p_j v_j, p = exp(s - m) / (sum exp(s - m)
+    + exp(sink - m)), lse = m + ln(denominator)
+    (sparse_flash_mla_golden.py:125-150, sinks_softmax_reference :163-185).
+    Rows past cu_seqlens_q[-1] stay 0 (out and lse).
+
+    Exact (float64) by default.  With ``golden_p_dtype`` it instead follows
+    the golden's own arithmetic (:125-150): float32, online softmax over
+    512-key tiles (original rows, then compressed), P rounded to that dtype
+    before P V, out rounded to it at the end -- the reference's error profile,
+    used to calibrate how close a bf16 kernel can be to the exact result.
+    """
+    T, H, D = q.shape
+    out = torch.zeros((T, H, D), dtype=torch.float64)
+    lse = torch.zeros((T, H), dtype=torch.float64)
+    sk = None if sinks is None else sinks.to(torch.float64).view(H, 1)
+    cu = [int(x) for x in cu_seqlens_q]
+    sel_all = None
+    if cmp_sparse_indices is not None:
+        sel_all = cmp_sparse_indices.reshape(cmp_sparse_indices.shape[0], -1)
+    for b in range(len(cu) - 1):
+        aq, akv = cu[b + 1] - cu[b], int(seqused_kv[b])
+        if aq <= 0:
+            continue
+        ori_rows = unpack_paged(ori_kv, ori_block_table, akv, b).to(torch.float64)
+        cmp_rows = None
+        if cmp_kv is not None and cmp_ratio is not None:
+            cmp_rows = unpack_paged(cmp_kv, cmp_block_table, akv // cmp_ratio, b).to(torch.float64)
+        for s in range(aq):
+            t = cu[b] + s
+            sg = akv - aq + s
+            sel = None if sel_all is None else sel_all[t].tolist()
+            o_pos, c_pos = v4_slots(sg, win_left=ori_win_left, cmp_ratio=cmp_ratio if cmp_rows is not None else None,
+                                    dense_cmp=cmp_rows is not None and sel is None, sel=sel)
+            keys = [ori_rows[o_pos]]
+            if c_pos:
+                keys.append(cmp_rows[c_pos])
+            kmat = torch.cat(keys) if keys else torch.zeros((0, D), dtype=torch.float64)
+            if golden_p_dtype is not None:
+                out[t], lse[t] = _golden_row(q[t].float(), ori_rows[o_pos].float(),
+                                             cmp_rows[c_pos].float() if c_pos else None,
+                                             None if sinks is None else sinks.float(), softmax_scale, golden_p_dtype)
+                continue
+            qt = q[t].to(torch.float64)
+            score = (qt @ kmat.T) * softmax_scale                       # [H, n]
+            logits = score if sk is None else torch.cat([score, sk], dim=1)
+            if logits.shape[1] == 0:
+                out[t] = 0.0
+                lse[t] = float("-inf")
+                continue
+            m = logits.amax(dim=1, keepdim=True)
+            e = torch.exp(logits - m)
+            denom = e.sum(dim=1, keepdim=True)
+            p = e[:, :score.shape[1]] / denom
+            out[t] = p @ kmat
+            lse[t] = (m + torch.log(denom)).squeeze(1)
+    return out.to(torch.float32), lse.to(torch.float32)
 
 
 # ----------------------------------------------------------------------------

@@ -277,3 +277,78 @@ def test_tnd_indexer_equals_per_batch_bsnd():
             assert torch.equal(logits[q0:q0 + aq, :ak], bl[0])
             assert torch.all(torch.isneginf(logits[q0:q0 + aq, ak:]))
         q0, k0 = q0 + aq, k0 + ak
+
+
+def test_v4_slots_hand_worked():
+    # Window clipped at 0; win_left = 127.
+    o, c = ref.v4_slots(3, win_left=127)
+    assert o == [0, 1, 2, 3] and c == []
+    o, c = ref.v4_slots(300, win_left=127)
+    assert o == list(range(173, 301))
+    # hca: threshold floor((9 + 1) / 4) = 2.
+    assert ref.v4_slots(9, win_left=2, cmp_ratio=4, dense_cmp=True) == ([7, 8, 9], [0, 1])
+    # csa: threshold 3, only the first 3 entries are read; 5 >= 3 skipped, -1 ends the list.
+    assert ref.v4_slots(11, win_left=0, cmp_ratio=4, sel=[5, 1, -1, 0]) == ([11], [1])
+    assert ref.v4_slots(11, win_left=0, cmp_ratio=4, sel=[2, 0, 1, 0]) == ([11], [2, 0, 1])
+    # Rows before the cache start see nothing.
+    assert ref.v4_slots(-1, win_left=127, cmp_ratio=4, dense_cmp=True) == ([], [])
+
+
+def _v4_one_batch(q, rows_ori, sinks, scale, win_left=127):
+    """One batch, identity block table, a single query row at the end of the sequence."""
+    T, H, D = q.shape
+    n = rows_ori.shape[0]
+    pool = rows_ori.view(n, 1, 1, D)
+    table = torch.arange(n, dtype=torch.int32).view(1, n)
+    return ref.sparse_flash_mla(q, [0, T], [n], pool, table, sinks, scale, ori_win_left=win_left)
+
+
+def test_v4_sink_single_key_closed_form():
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn(1, 2, 8, generator=g, dtype=torch.float64).float()
+    k = torch.randn(1, 8, generator=g, dtype=torch.float64).float()
+    sinks = torch.tensor([0.5, -1.0])
+    out, lse = _v4_one_batch(q, k, sinks, 0.3)
+    s = (q[0].double() @ k[0].double()) * 0.3
+    w = torch.exp(s) / (torch.exp(s) + torch.exp(sinks.double()))
+    assert torch.allclose(out[0].double(), w.view(2, 1) * k.double(), rtol=1e-6, atol=1e-6)
+    assert torch.allclose(lse[0].double(), torch.log(torch.exp(s) + torch.exp(sinks.double())), rtol=1e-6)
+
+
+def test_v4_sink_matches_library_softmax_and_vanishes():
+    g = torch.Generator().manual_seed(4)
+    H, D, n = 4, 16, 40
+    q = torch.randn(1, H, D, generator=g)
+    k = torch.randn(n, D, generator=g)
+    sinks = torch.randn(H, generator=g)
+    out, lse = _v4_one_batch(q, k, sinks, 0.25, win_left=31)
+    keys = k[n - 32:].double()                       # window of 32 rows ending at the row's position
+    sc = (q[0].double() @ keys.T) * 0.25
+    full = torch.cat([sc, sinks.double().view(H, 1)], dim=1)
+    p = torch.softmax(full, dim=1)[:, :-1]
+    assert torch.allclose(out[0].double(), p @ keys, rtol=1e-5, atol=1e-6)
+    assert torch.allclose(lse[0].double(), torch.logsumexp(full, dim=1), rtol=1e-6)
+    # A sink far below every score leaves plain softmax attention.
+    out2, lse2 = _v4_one_batch(q, k, torch.full((H,), -1e4), 0.25, win_left=31)
+    p2 = torch.softmax(sc, dim=1)
+    assert torch.allclose(out2[0].double(), p2 @ keys, rtol=1e-5, atol=1e-6)
+    assert torch.allclose(lse2[0].double(), torch.logsumexp(sc, dim=1), rtol=1e-6)
+
+
+def test_v4_golden_mode_matches_exact_without_rounding():
+    # The golden-arithmetic mode with float32 P is the exact result up to float32 rounding.
+    g = torch.Generator().manual_seed(6)
+    H, D, n = 4, 32, 700
+    q = torch.randn(3, H, D, generator=g)
+    k = torch.randn(n, D, generator=g)
+    sinks = torch.randn(H, generator=g)
+    pool, table = k.view(n, 1, 1, D), torch.arange(n, dtype=torch.int32).view(1, n)
+    ex = ref.sparse_flash_mla(q, [0, 3], [n], pool, table, sinks, 0.2, ori_win_left=600)
+    gm = ref.sparse_flash_mla(q, [0, 3], [n], pool, table, sinks, 0.2, ori_win_left=600,
+                              golden_p_dtype=torch.float32)
+    assert torch.allclose(ex[0], gm[0], rtol=1e-4, atol=1e-5) and torch.allclose(ex[1], gm[1], rtol=1e-5)
+    # bf16 P: the golden's own deviation from exact, small but nonzero.
+    gb = ref.sparse_flash_mla(q, [0, 3], [n], pool, table, sinks, 0.2, ori_win_left=600,
+                              golden_p_dtype=torch.bfloat16)
+    d = (gb[0] - ex[0]).abs().max().item()
+    assert 0 < d < 2e-2

@@ -3,10 +3,12 @@
 Hand-written HIP kernels behind the C ABI of ``include/dsa_mi355x.h``; this
 package is the host-side mirror of the reference's Python operator interface
 (examples/lightning_indexer, examples/topk_selector,
-examples/sparse_flash_attention and examples/deepseek_v4 of tilelang-ascend).
+examples/sparse_flash_attention and examples/deepseek_v4 of tilelang-ascend,
+including the V4 ``sparse_flash_mla`` operator).
 """
 from ._lib import DSAError, load_library, library_path
 from .lightning_indexer import indexer, indexer_logits, lightning_indexer
+from .sparse_flash_mla import sparse_flash_mla
 from .sparse_mla import sparse_attention_fwd, sparse_mla_fwd
 from .topk_selector import simple_topk_selector, topk_selector
 
@@ -19,6 +21,7 @@ __all__ = [
     "load_library",
     "simple_topk_selector",
     "sparse_attention_fwd",
+    "sparse_flash_mla",
     "sparse_mla_fwd",
     "topk_selector",
 ]

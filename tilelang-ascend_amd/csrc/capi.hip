@@ -19,6 +19,15 @@ hipError_t launch_sparse_mla(int is_fp16, const void* q, const void* kv, const i
                              int64_t Skv, int64_t block_size, int64_t max_blocks, int64_t topk, float sm_scale,
                              int causal, void* out, float* lse, void* workspace, hipStream_t stream);
 size_t mla_workspace_bytes(int64_t tokens, int64_t H, int64_t topk);
+size_t v4_workspace_bytes(int64_t T, int64_t H, int64_t cap);
+hipError_t launch_sparse_flash_mla(int is_fp16, const void* q, int64_t T, int64_t H, int64_t B,
+                                   const int32_t* q_start, const int32_t* q_len, const int32_t* kv_len,
+                                   const void* ori_kv, int64_t ori_blocks, int64_t ori_bs, const int32_t* ori_bt,
+                                   int64_t ori_tl, const void* cmp_kv, int64_t cmp_blocks, int64_t cmp_bs,
+                                   const int32_t* cmp_bt, int64_t cmp_tl, const int32_t* cmp_idx, int64_t K,
+                                   int64_t cmp_ratio, int64_t win_left, int64_t max_cmp, int mode, int64_t cap,
+                                   const float* sinks, float sm_scale, void* out, float* lse, void* workspace,
+                                   hipStream_t stream);
 }  // namespace dsa
 
 namespace {
@@ -35,6 +44,8 @@ int ok(hipError_t e) {
 }
 
 constexpr int64_t kMaxInt = 0x7fffffff;
+// Physical rows of the V4 caches must stay below the gather kernel's source tag bit.
+constexpr int64_t dsa_kSrc2Limit = 0x40000000;
 }  // namespace
 
 extern "C" {
@@ -228,6 +239,61 @@ int dsa_sparse_mla_fwd(int kind, const void* q, const void* kv, const int32_t* i
   return ok(dsa::launch_sparse_mla(kind == DSA_KIND_FP16, q, kv, indices, block_table, actual_q_len, actual_kv_len, B, S, H, skv_eff,
                                    block_size, max_blocks, topk, sm_scale, is_causal ? 1 : 0, out, lse, workspace,
                                    static_cast<hipStream_t>(stream)));
+}
+
+// Row-list capacity of a V4 call: the window plus the compressed slots.
+static int64_t v4_cap(int64_t ori_win_left, int64_t cmp_slots) { return ori_win_left + 1 + cmp_slots; }
+
+size_t dsa_sparse_flash_mla_workspace_size(int64_t T, int64_t H, int64_t ori_win_left, int64_t cmp_slots) {
+  if (T <= 0 || H <= 0 || ori_win_left < 0 || cmp_slots < 0) return 0;
+  return dsa::v4_workspace_bytes(T, H, v4_cap(ori_win_left, cmp_slots));
+}
+
+int dsa_sparse_flash_mla(int kind, const void* q, int64_t T, int64_t H, int64_t D, int64_t B, const int32_t* q_start,
+                         const int32_t* q_len, const int32_t* seqused_kv, const void* ori_kv, int64_t ori_block_num,
+                         int64_t ori_block_size, const int32_t* ori_block_table, int64_t ori_table_len,
+                         const void* cmp_kv, int64_t cmp_block_num, int64_t cmp_block_size,
+                         const int32_t* cmp_block_table, int64_t cmp_table_len, const int32_t* cmp_sparse_indices,
+                         int64_t topk_cmp, int64_t cmp_ratio, int64_t ori_win_left, int64_t max_cmp,
+                         const float* sinks, float softmax_scale, void* out, float* lse, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  if (kind != DSA_KIND_BF16 && kind != DSA_KIND_FP16) return reject("sparse_flash_mla: kind must be bf16 or fp16");
+  if (D != 512) return reject("sparse_flash_mla: D must be 512");
+  if (H < 16 || H % 16 != 0 || H > 1024) return reject("sparse_flash_mla: H must be a multiple of 16 in [16, 1024]");
+  if (T < 0 || B < 1 || T > kMaxInt || B > kMaxInt) return reject("sparse_flash_mla: bad T / B");
+  if (ori_win_left < 0 || ori_win_left > 65535) return reject("sparse_flash_mla: ori_win_left must be in [0, 65535]");
+  if (ori_block_size <= 0 || ori_block_num <= 0 || ori_table_len <= 0 ||
+      ori_block_num * ori_block_size >= dsa_kSrc2Limit)
+    return reject("sparse_flash_mla: bad original KV pool");
+  if (T > 0 && (!q || !ori_kv || !ori_block_table || !q_start || !q_len || !seqused_kv || !out || !lse))
+    return reject("sparse_flash_mla: null pointer");
+  int mode = 1;
+  int64_t cmp_slots = 0;
+  if (cmp_kv) {
+    if (cmp_ratio < 1) return reject("sparse_flash_mla: cmp_ratio must be >= 1");
+    if (cmp_block_size <= 0 || cmp_block_num <= 0 || cmp_table_len <= 0 || !cmp_block_table ||
+        cmp_block_num * cmp_block_size >= dsa_kSrc2Limit)
+      return reject("sparse_flash_mla: bad compressed KV pool");
+    if (cmp_sparse_indices) {
+      if (topk_cmp < 1 || topk_cmp > 65536) return reject("sparse_flash_mla: topk_cmp must be in [1, 65536]");
+      mode = 3;
+      cmp_slots = topk_cmp;
+    } else {
+      if (max_cmp < 0 || max_cmp > 65536) return reject("sparse_flash_mla: max_cmp must be in [0, 65536]");
+      mode = 2;
+      cmp_slots = max_cmp;
+    }
+  }
+  const int64_t cap = v4_cap(ori_win_left, cmp_slots);
+  if (T * (cap + 1) > kMaxInt) return reject("sparse_flash_mla: T x slots too large");
+  if (workspace_bytes < dsa_sparse_flash_mla_workspace_size(T, H, ori_win_left, cmp_slots))
+    return reject("sparse_flash_mla: workspace too small");
+  if (T > 0 && !workspace) return reject("sparse_flash_mla: null workspace");
+  return ok(dsa::launch_sparse_flash_mla(kind == DSA_KIND_FP16, q, T, H, B, q_start, q_len, seqused_kv, ori_kv,
+                                         ori_block_num, ori_block_size, ori_block_table, ori_table_len, cmp_kv,
+                                         cmp_block_num, cmp_block_size, cmp_block_table, cmp_table_len,
+                                         cmp_sparse_indices, topk_cmp, cmp_ratio, ori_win_left, max_cmp, mode, cap,
+                                         sinks, softmax_scale, out, lse, workspace, static_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

@@ -46,19 +46,33 @@
 
 namespace dsa {
 
-constexpr int kMlaD = 576;
 constexpr int kMlaDV = 512;
 constexpr int kMlaTile = 32;                       // slots per tile
-constexpr int kRowBytes = kMlaD * 2;               // 1152
-constexpr int kRowChunks = kRowBytes / 16;         // 72
 constexpr int kStages = 4;
 constexpr int kAhead = kStages - 1;                // tiles in flight ahead of compute
-constexpr int kStageBytes = kMlaTile * kRowBytes;  // 36864
-constexpr int kTileInstr = kStageBytes / 1024;     // 36 wave-wide 16-byte DMA loads per tile
 constexpr int kSlotsCap = 2048;                    // slots per workgroup (physical rows kept in LDS)
-constexpr int kRowsOffset = kStages * kStageBytes; // 147456
-constexpr int kTileMaskOffset = kRowsOffset + kSlotsCap * 4 + 16;  // after rows, overflow flag, first valid slot
-constexpr int kMlaLds = kTileMaskOffset + (kSlotsCap / 32) * 4;       // + one valid-slot bitmask per tile
+// Rows with this bit set live in the second KV source (MlaArgs::kv2).
+constexpr int32_t kSrc2Bit = 0x40000000;
+
+// Geometry of a KV row of kD 16-bit elements: 576 (latent 512 + rope 64,
+// DeepSeek V3.2) or 512 (V4: K = V, no rope tail).  V is always the first 512.
+template <int kD>
+struct MlaGeom {
+  static_assert(kD == 576 || kD == 512, "row width");
+  static constexpr int kRowBytes = kD * 2;                      // 1152 / 1024
+  static constexpr int kRowChunks = kRowBytes / 16;             // 72 / 64
+  static constexpr int kStageBytes = kMlaTile * kRowBytes;      // 36864 / 32768
+  static constexpr int kTileInstr = kStageBytes / 1024;         // wave-wide 16-byte DMA loads per tile
+  static constexpr int kRowsOffset = kStages * kStageBytes;
+  static constexpr int kTileMaskOffset = kRowsOffset + kSlotsCap * 4 + 16;  // after rows, overflow flag, first valid slot
+  static constexpr int kLds = kTileMaskOffset + (kSlotsCap / 32) * 4;       // + one valid-slot bitmask per tile
+  static constexpr int kSteps = kD / 32;                        // 32-dim steps of Q K^T
+  static constexpr int kQkHalf = 2 * kSteps;                    // half-steps (one K operand read each)
+  // V4 (512) reads per-row lists of physical rows from two caches, with
+  // per-row slot counts and attention sinks; V3.2 (576) reads index lists into
+  // one cache.  Fixed per width, so neither pays for the other's features.
+  static constexpr bool kRowLists = kD == 512;
+};
 // Reference max = first valid tile's max + kRefBias (log2); the fast path accepts
 // P up to 2^kOverflowGuard.  bf16 shares fp32's exponent range; fp16 P must stay
 // within [2^-14, 65504].
@@ -70,9 +84,12 @@ template <bool kF16> constexpr float kOverflowSumOf = kF16 ? 32768.f : 115292150
 constexpr int kHeadsPerWave = 32;                  // two 16-head MFMA blocks share every K / V operand
 
 struct MlaArgs {
-  const uint16_t* q;          // [B, S, H, 576] bf16 / fp16
-  const uint16_t* kv;         // [B, Skv, 576] or paged [blocks, block_size, 576]
-  const int32_t* indices;     // [B, S, topk]
+  const uint16_t* q;          // [B, S, H, D] bf16 / fp16
+  const uint16_t* kv;         // [B, Skv, D] or paged [blocks, block_size, D]
+  const uint16_t* kv2;        // second row source (rows tagged kSrc2Bit) or null
+  const int32_t* indices;     // [B, S, topk]; physical rows with row lists (D = 512)
+  const int32_t* slot_count;  // [B*S] used slots per row (row lists)
+  const float* sinks;         // [H] attention-sink logits (natural log units) or null
   const int32_t* block_table; // [B, max_blocks] or null
   const int32_t* q_len;       // [B] or null
   const int32_t* kv_len;      // [B] or null
@@ -118,9 +135,10 @@ __device__ __forceinline__ void wait_tiles(int ahead) {
   }
 }
 
-template <int kNW>
+template <int kNW, int kD>
 struct MlaCfg {
   static constexpr int kThreads = kNW * kWave;
+  static constexpr int kTileInstr = MlaGeom<kD>::kTileInstr;
   // DMA instructions per tile for wave w: I = w, w + kNW, ... < kTileInstr.
   static constexpr int kMaxPerWave = (kTileInstr + kNW - 1) / kNW;
   static_assert(kTileInstr % kNW == 0, "every wave issues the same number of DMA loads per tile");
@@ -132,8 +150,8 @@ struct MlaCfg {
   static_assert(kDepth >= 2 && kDepth + 1 <= kStages, "DMA ring depth");
 };
 
-// Tile layout in a stage.  The tile is 32 slots x 72 16-byte chunks, stored
-// as 36 blocks of 1 KB: block a + 4b holds slots 8a .. 8a+7 x chunks
+// Tile layout in a stage.  The tile is 32 slots x 72 (64) 16-byte chunks, stored
+// as 36 (32) blocks of 1 KB: block a + 4b holds slots 8a .. 8a+7 x chunks
 // 8b .. 8b+7, with (slot 8a+u, chunk 8b+w) at 16-byte position
 // 8u + (w ^ lds_swizzle(u, a)) of the block.  One DMA instruction fills one
 // block, so its 64 lanes fetch 8 whole 128-byte lines (8 lanes per slot) --
@@ -153,21 +171,23 @@ __host__ __device__ constexpr int lds_swizzle(int u, int a) {
 // KV cache.
 // The same DMA, split so that its instructions can be spread over the
 // matrix work of an iteration: prepare() computes the lane's row addresses
-// (reading the slot -> row map from LDS), issue<D>() sends instruction D.
+// (reading the slot -> row map from LDS; a row tagged kSrc2Bit is read from
+// the second source), issue<D>() sends instruction D.
 // Sent in one burst, the instructions of the four waves queue behind each
 // other in the memory pipeline and stall the issuing waves.  Past the last
 // tile (`live` false) every lane re-reads `safe_row` into the stage nobody
 // uses any more, which keeps the matrix loop free of branches.
-template <int kNW>
+template <int kNW, int kD>
 struct TileDma {
+  static constexpr int kRowChunks = MlaGeom<kD>::kRowChunks;
   static constexpr int kGroups = 4 / kNW;                    // row groups per wave
   static constexpr int kCount = kGroups * (kRowChunks / 8);  // instructions per wave and tile
   const uint8_t* src[kGroups];
   uint8_t* stage;
   int wave;
 
-  __device__ __forceinline__ void prepare(const uint8_t* kv, const int32_t* rows, int safe_row, int tile,
-                                          uint8_t* stage_base, int wave_, int lane, bool live) {
+  __device__ __forceinline__ void prepare(const uint8_t* kv, const uint8_t* kv2, const int32_t* rows, int safe_row,
+                                          int tile, uint8_t* stage_base, int wave_, int lane, bool live) {
     wave = wave_;
     stage = stage_base;
     const int u = lane >> 3;
@@ -176,7 +196,12 @@ struct TileDma {
       const int a = wave + ag * kNW;
       int row = live ? rows[tile * kMlaTile + 8 * a + u] : -1;
       row = row >= 0 ? row : safe_row;
-      src[ag] = kv + (int64_t)row * kRowBytes + 16 * ((lane & 7) ^ lds_swizzle(u, a));
+      const uint8_t* base = kv;
+      if constexpr (MlaGeom<kD>::kRowLists) {
+        base = (row & kSrc2Bit) ? kv2 : kv;
+        row &= ~kSrc2Bit;
+      }
+      src[ag] = base + (int64_t)row * MlaGeom<kD>::kRowBytes + 16 * ((lane & 7) ^ lds_swizzle(u, a));
     }
   }
   template <int D>
@@ -300,71 +325,25 @@ __device__ __forceinline__ void b128_read(u32x4& out, uint32_t lds_addr) {
 }
 
 template <int N>
-__device__ __forceinline__ void lgkm_wait2(u32x4& a, u32x4& b) {
-  static_assert(N >= 0 && N < 16, "lgkmcnt range");
-  __asm__ __volatile__("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
-}
-
-// The K operands of QK step kSt: chunk 4*kSt + g of slots r (lo) and 16 + r
-// (hi), at bytes kbase[kSt % 2] + 4096*(kSt / 2) (+2048).
-template <int kSt>
-__device__ __forceinline__ void qk_step_reads(u32x4& lo, u32x4& hi, const uint32_t (&kbase)[2]) {
-  b128_read<4096 * (kSt / 2)>(lo, kbase[kSt % 2]);
-  b128_read<4096 * (kSt / 2) + 2048>(hi, kbase[kSt % 2]);
-}
-
-// S^T += K Q^T over d = 576: 18 steps of 32 dims; the K reads of steps
-// st + 1 and st + 2 are in flight while step st runs on the matrix cores.
-template <bool kF16, int kSt>
-__device__ __forceinline__ void qk_mfma(f32x4 (&c)[2][2], const u32x4 (&qb)[2][kMlaD / 32], const u32x4& k0,
-                                        const u32x4& k1) {
-#pragma unroll
-  for (int hb = 0; hb < 2; ++hb) {
-    c[hb][0] = mfma16<kF16>(k0, qb[hb][kSt], c[hb][0]);
-    c[hb][1] = mfma16<kF16>(k1, qb[hb][kSt], c[hb][1]);
-  }
-}
-
-template <bool kF16, int kSt>
-__device__ __forceinline__ void qk_pipeline(f32x4 (&c)[2][2], const u32x4 (&qb)[2][kMlaD / 32],
-                                            const uint32_t (&qa)[2], u32x4& a0, u32x4& a1, u32x4& b0, u32x4& b1) {
-  constexpr int kSteps = kMlaD / 32;
-  if constexpr (kSt + 2 < kSteps) {
-    u32x4 n0, n1;
-    qk_step_reads<kSt + 2>(n0, n1, qa);
-    lgkm_wait2<4>(a0, a1);
-    qk_mfma<kF16, kSt>(c, qb, a0, a1);
-    qk_pipeline<kF16, kSt + 1>(c, qb, qa, b0, b1, n0, n1);
-  } else if constexpr (kSt + 1 < kSteps) {
-    lgkm_wait2<2>(a0, a1);
-    qk_mfma<kF16, kSt>(c, qb, a0, a1);
-    lgkm_wait2<0>(b0, b1);
-    qk_mfma<kF16, kSt + 1>(c, qb, b0, b1);
-  }
-}
-
-constexpr int kQkHalf = 2 * (kMlaD / 32);  // 36 half-steps of Q K^T
-
-template <int N>
 __device__ __forceinline__ void lgkm_wait_k(u32x4& k) {
   static_assert(N >= 0 && N < 16, "lgkmcnt range");
   __asm__ __volatile__("s_waitcnt lgkmcnt(%1)" : "+v"(k) : "i"(N));
 }
 
-template <int kNW, int D = 0>
-__device__ __forceinline__ void il_dma_all(TileDma<kNW>& dma) {
-  if constexpr (D < TileDma<kNW>::kCount) {
+template <int kNW, int kD, int D = 0>
+__device__ __forceinline__ void il_dma_all(TileDma<kNW, kD>& dma) {
+  if constexpr (D < TileDma<kNW, kD>::kCount) {
     dma.template issue<D>();
-    il_dma_all<kNW, D + 1>(dma);
+    il_dma_all<kNW, kD, D + 1>(dma);
   }
 }
 
 // DMA instructions D with D * kQkHalf / kCount == J go out at half-step J.
-template <int kNW, int J, int D = 0>
-__device__ __forceinline__ void il_dma(TileDma<kNW>& dma) {
-  if constexpr (D < TileDma<kNW>::kCount) {
-    if constexpr (D * kQkHalf / TileDma<kNW>::kCount == J) dma.template issue<D>();
-    il_dma<kNW, J, D + 1>(dma);
+template <int kNW, int kD, int J, int D = 0>
+__device__ __forceinline__ void il_dma(TileDma<kNW, kD>& dma) {
+  if constexpr (D < TileDma<kNW, kD>::kCount) {
+    if constexpr (D * MlaGeom<kD>::kQkHalf / TileDma<kNW, kD>::kCount == J) dma.template issue<D>();
+    il_dma<kNW, kD, J, D + 1>(dma);
   }
 }
 
@@ -386,21 +365,22 @@ __device__ __forceinline__ void pv_only(f32x4 (&o)[2][kMlaDV / 16], const u32x4 
 // spread over the half-steps.
 constexpr int kQkAhead = 6;
 
-template <bool kF16, int kNW, bool kDma, int J>
-__device__ __forceinline__ void qk_half(f32x4 (&c)[2][2][2], const u32x4 (&qb)[2][kMlaD / 32],
-                                        const uint32_t (&qa)[2], u32x4 (&k)[kQkAhead + 1], TileDma<kNW>& dma) {
+template <bool kF16, int kNW, int kD, bool kDma, int J>
+__device__ __forceinline__ void qk_half(f32x4 (&c)[2][2][2], const u32x4 (&qb)[2][kD / 32],
+                                        const uint32_t (&qa)[2], u32x4 (&k)[kQkAhead + 1], TileDma<kNW, kD>& dma) {
+  constexpr int kQkHalf = MlaGeom<kD>::kQkHalf;
   constexpr int kNext = J + kQkAhead;
   if constexpr (kNext < kQkHalf) {
     b128_read<4096 * (kNext / 4) + 2048 * (kNext % 2)>(k[kNext % (kQkAhead + 1)], qa[(kNext / 2) % 2]);
   }
-  if constexpr (kDma) il_dma<kNW, J>(dma);
+  if constexpr (kDma) il_dma<kNW, kD, J>(dma);
   constexpr int kWait = (kQkHalf - 1 - J) < kQkAhead ? (kQkHalf - 1 - J) : kQkAhead;
   constexpr int kSlot = J % (kQkAhead + 1);
   lgkm_wait_k<kWait>(k[kSlot]);
   constexpr int kSet = (J / 2) % 2, kKb = J % 2, kSt = J / 2;
   c[kSet][0][kKb] = mfma16<kF16>(k[kSlot], qb[0][kSt], c[kSet][0][kKb]);
   c[kSet][1][kKb] = mfma16<kF16>(k[kSlot], qb[1][kSt], c[kSet][1][kKb]);
-  if constexpr (J + 1 < kQkHalf) qk_half<kF16, kNW, kDma, J + 1>(c, qb, qa, k, dma);
+  if constexpr (J + 1 < kQkHalf) qk_half<kF16, kNW, kD, kDma, J + 1>(c, qb, qa, k, dma);
 }
 
 template <int J>
@@ -411,9 +391,9 @@ __device__ __forceinline__ void qk_prologue(u32x4 (&k)[kQkAhead + 1], const uint
   }
 }
 
-template <bool kF16, int kNW, bool kDma>
-__device__ __forceinline__ void qk_phase(f32x4 (&s)[2][2], const u32x4 (&qb)[2][kMlaD / 32],
-                                         const uint32_t (&qa)[2], TileDma<kNW>& dma) {
+template <bool kF16, int kNW, int kD, bool kDma>
+__device__ __forceinline__ void qk_phase(f32x4 (&s)[2][2], const u32x4 (&qb)[2][kD / 32],
+                                         const uint32_t (&qa)[2], TileDma<kNW, kD>& dma) {
   f32x4 c[2][2][2];
 #pragma unroll
   for (int st = 0; st < 2; ++st)
@@ -421,7 +401,7 @@ __device__ __forceinline__ void qk_phase(f32x4 (&s)[2][2], const u32x4 (&qb)[2][
     for (int hb = 0; hb < 2; ++hb) c[st][hb][0] = c[st][hb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
   u32x4 k[kQkAhead + 1];
   qk_prologue<0>(k, qa);
-  qk_half<kF16, kNW, kDma, 0>(c, qb, qa, k, dma);
+  qk_half<kF16, kNW, kD, kDma, 0>(c, qb, qa, k, dma);
 #pragma unroll
   for (int hb = 0; hb < 2; ++hb)
 #pragma unroll
@@ -433,12 +413,17 @@ __device__ __forceinline__ void qk_phase(f32x4 (&s)[2][2], const u32x4 (&qb)[2][
 // P V pipeline, so its VALU work overlaps the matrix cores.  Lane (g, r)
 // holds scores of keys 4g+i (kb 0) and 16+4g+i (kb 1) of heads head0 + 16*hb
 // + r; scores of empty slots were set to -inf beforehand.
-template <bool kF16>
+// kRoundSum: also sum the probabilities as rounded to 16 bits (lsum_r), so O
+// can be normalised by the weights the P V products actually used: with a
+// fixed reference the dominant key's P is rounded too (a running max would
+// make it exactly 1), and dividing by the rounded sum cancels that error.
+template <bool kF16, bool kRoundSum = false>
 struct SoftmaxSlices {
   static constexpr int kSlices = 10;  // per head block: 4 x (2 exponentials), 1 x (sum, pack)
   const f32x4 (&c)[2][2];
   u32x4 (&pa)[2];
   float (&lsum)[2];
+  float (&lsum_r)[2];
   bool& overflow;
   float neg_m[2];
   float scale;
@@ -460,15 +445,20 @@ struct SoftmaxSlices {
         overflow = overflow || !(ps <= kOverflowSumOf<kF16>);
         pa[kHb] = u32x4{pack2<kF16>(q[0], q[1]), pack2<kF16>(q[2], q[3]), pack2<kF16>(q[4], q[5]),
                         pack2<kF16>(q[6], q[7])};
+        if constexpr (kRoundSum) {
+          const u32x4 w = pa[kHb];
+          lsum_r[kHb] += ((unpack_lo<kF16>(w.x) + unpack_hi<kF16>(w.x)) + (unpack_lo<kF16>(w.y) + unpack_hi<kF16>(w.y))) +
+                         ((unpack_lo<kF16>(w.z) + unpack_hi<kF16>(w.z)) + (unpack_lo<kF16>(w.w) + unpack_hi<kF16>(w.w)));
+        }
       }
     }
   }
 };
 
-template <bool kF16, int kGrp>
+template <bool kF16, int kGrp, bool kRoundSum>
 __device__ __forceinline__ void pv_softmax_pipeline(f32x4 (&o)[2][kMlaDV / 16], const u32x4 (&pa)[2],
                                                     const uint32_t (&vaddr)[2], u32x2 (&cur)[4], u32x2 (&nxt)[4],
-                                                    SoftmaxSlices<kF16>& sm) {
+                                                    SoftmaxSlices<kF16, kRoundSum>& sm) {
   constexpr int kGroups = kMlaDV / 32;
   if constexpr (kGrp + 2 < kGroups) {
     u32x2 n2[4];
@@ -476,7 +466,7 @@ __device__ __forceinline__ void pv_softmax_pipeline(f32x4 (&o)[2][kMlaDV / 16], 
     sm.template run<kGrp>();
     lgkm_wait<8>(cur);
     pv_group_mfma<kF16, kGrp>(o, pa, cur);
-    pv_softmax_pipeline<kF16, kGrp + 1>(o, pa, vaddr, nxt, n2, sm);
+    pv_softmax_pipeline<kF16, kGrp + 1, kRoundSum>(o, pa, vaddr, nxt, n2, sm);
   } else if constexpr (kGrp + 1 < kGroups) {
     sm.template run<kGrp>();
     lgkm_wait<4>(cur);
@@ -495,12 +485,24 @@ __device__ __forceinline__ uint32_t lds_u32(const void* p) {
 // Exact two-pass fallback for a workgroup whose scores outgrew the fast
 // path's fixed reference: per head, the scores of all slots go to LDS, then
 // max, sum and P V from them.  Slow (VALU, KV re-read per head) and only taken
-// for pathological score ranges.  Writes the same outputs as the fast path.
-// Arguments are passed by value (a reference to the kernel's argument block
-// would force that block into scratch memory for the whole kernel).
-template <bool kF16>
-__device__ __attribute__((noinline)) void mla_exact_fallback(const uint16_t* q, const uint8_t* kvb,
-                                                             uint16_t* obase, float* lbase, int H,
+// for pathological score ranges.  Writes the same outputs as the fast path
+// (with the attention sink of each head when `sinks` is given, in base-2
+// units).  Arguments are passed by value (a reference to the kernel's
+// argument block would force that block into scratch memory for the whole
+// kernel).
+template <bool kF16, int kD>
+__device__ __forceinline__ const uint16_t* mla_row(const uint8_t* kvb, const uint8_t* kvb2, int row) {
+  const uint8_t* base = kvb;
+  if constexpr (MlaGeom<kD>::kRowLists) {
+    base = (row & kSrc2Bit) ? kvb2 : kvb;
+    row &= ~kSrc2Bit;
+  }
+  return reinterpret_cast<const uint16_t*>(base + (int64_t)row * MlaGeom<kD>::kRowBytes);
+}
+
+template <bool kF16, int kD>
+__device__ __attribute__((noinline)) void mla_exact_fallback(const uint16_t* q, const uint8_t* kvb, const uint8_t* kvb2,
+                                                             const float* sinks, uint16_t* obase, float* lbase, int H,
                                                              float scale_log2, const int32_t* rows, int nslots,
                                                              int token, int head_begin, int nheads, float* sc,
                                                              int threads) {
@@ -509,15 +511,15 @@ __device__ __attribute__((noinline)) void mla_exact_fallback(const uint16_t* q, 
   for (int hl = 0; hl < nheads; ++hl) {
     const int h = head_begin + hl;
     if (h >= H) break;
-    const uint16_t* qh = q + ((int64_t)token * H + h) * kMlaD;
+    const uint16_t* qh = q + ((int64_t)token * H + h) * kD;
     float mx = -__builtin_huge_valf();
     for (int j = tid; j < nslots; j += threads) {
       const int row = rows[j];
       float sj = -__builtin_huge_valf();
       if (row >= 0) {
-        const uint16_t* kr = reinterpret_cast<const uint16_t*>(kvb + (int64_t)row * kRowBytes);
+        const uint16_t* kr = mla_row<kF16, kD>(kvb, kvb2, row);
         float acc = 0.f;
-        for (int d = 0; d < kMlaD; d += 2) {
+        for (int d = 0; d < kD; d += 2) {
           const uint32_t qv = *reinterpret_cast<const uint32_t*>(qh + d);
           const uint32_t kv = *reinterpret_cast<const uint32_t*>(kr + d);
           acc = fmaf(unpack_lo<kF16>(qv), unpack_lo<kF16>(kv), acc);
@@ -534,6 +536,8 @@ __device__ __attribute__((noinline)) void mla_exact_fallback(const uint16_t* q, 
     mx = -__builtin_huge_valf();
     for (int w = 0; w < threads / kWave; ++w) mx = fmaxf(mx, red[w]);
     __syncthreads();
+    const float sink = sinks ? sinks[h] * 1.4426950408889634f : -__builtin_huge_valf();
+    mx = fmaxf(mx, sink);
     const float m_use = mx == -__builtin_huge_valf() ? 0.f : mx;
     float l = 0.f;
     for (int j = tid; j < nslots; j += threads) l += fast_exp2(sc[j] - m_use);
@@ -541,7 +545,7 @@ __device__ __attribute__((noinline)) void mla_exact_fallback(const uint16_t* q, 
     for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, kWave);
     if ((tid & (kWave - 1)) == 0) red[tid / kWave] = l;
     __syncthreads();
-    l = 0.f;
+    l = sinks ? fast_exp2(sink - m_use) : 0.f;
     for (int w = 0; w < threads / kWave; ++w) l += red[w];
     const float inv = l > 0.f ? 1.f / l : 0.f;
     for (int c = tid; c < kMlaDV; c += threads) {
@@ -549,7 +553,7 @@ __device__ __attribute__((noinline)) void mla_exact_fallback(const uint16_t* q, 
       for (int j = 0; j < nslots; ++j) {
         const int row = rows[j];
         if (row < 0) continue;
-        const uint16_t v = reinterpret_cast<const uint16_t*>(kvb + (int64_t)row * kRowBytes)[c];
+        const uint16_t v = mla_row<kF16, kD>(kvb, kvb2, row)[c];
         acc = fmaf(fast_exp2(sc[j] - m_use), unpack_lo<kF16>(v), acc);
       }
       obase[((int64_t)token * H + h) * kMlaDV + c] = cvt1<kF16>(acc * inv);
@@ -559,11 +563,12 @@ __device__ __attribute__((noinline)) void mla_exact_fallback(const uint16_t* q, 
   }
 }
 
-template <int kNW, bool kF16>
+template <int kNW, bool kF16, int kD>
 __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
-  using Cfg = MlaCfg<kNW>;
+  using Cfg = MlaCfg<kNW, kD>;
+  using Geo = MlaGeom<kD>;
   extern __shared__ __align__(16) uint8_t lds[];
-  int32_t* rows = reinterpret_cast<int32_t*>(lds + kRowsOffset);
+  int32_t* rows = reinterpret_cast<int32_t*>(lds + Geo::kRowsOffset);
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform
@@ -587,13 +592,16 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   // that order), and the block-table lookups as soon as the indices are back.
   const int32_t* irow = a.indices + (int64_t)token * a.topk;
   const int slot_begin = split * a.keys_per_split;
-  const int slot_end = min(a.topk, slot_begin + a.keys_per_split);
+  // Row lists: a negative count marks a padded query row (out = 0, lse = 0).
+  const int count_raw = Geo::kRowLists ? a.slot_count[token] : 0;
+  const int row_slots = Geo::kRowLists ? min(max(count_raw, 0), a.topk) : a.topk;
+  const int slot_end = min(row_slots, slot_begin + a.keys_per_split);
   const int nslots = slot_end > slot_begin ? slot_end - slot_begin : 0;
   // Every load below is issued unconditionally, from a clamped valid address
   // (its value is discarded later if out of range): conditional loads would
   // make the compiler wait for them on the spot.
   constexpr int kIdxPerLane = kSlotsCap / (kNW * kWave);  // slot indices a lane may translate
-  const int last_slot = max(min(slot_end, a.topk) - 1, 0);
+  const int last_slot = max(min(slot_end, a.topk) - 1, 0);  // clamped: slot_end may be 0
   int idx_raw[kIdxPerLane];
 #pragma unroll
   for (int j = 0; j < kIdxPerLane; ++j) {
@@ -607,17 +615,17 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   __asm__ __volatile__("" ::: "memory");
 
   // Q operands (B of S^T = K Q^T): head head0 + 16*hb + r, dims 32*st + 8*g .. +8.
-  u32x4 qb[2][kMlaD / 32];
+  u32x4 qb[2][kD / 32];
 #pragma unroll
   for (int hb = 0; hb < 2; ++hb) {
     const int h = min(head0 + 16 * hb + r, a.H - 1);
-    const uint16_t* qp = a.q + ((int64_t)token * a.H + h) * kMlaD + 8 * g;
+    const uint16_t* qp = a.q + ((int64_t)token * a.H + h) * kD + 8 * g;
 #pragma unroll
-    for (int st = 0; st < kMlaD / 32; ++st) qb[hb][st] = *reinterpret_cast<const u32x4*>(qp + 32 * st);
+    for (int st = 0; st < kD / 32; ++st) qb[hb][st] = *reinterpret_cast<const u32x4*>(qp + 32 * st);
   }
   const int ql = min(max(ql_raw, 0), a.S);
-  const int kl = min(max(kl_raw, 0), a.Skv);
-  const bool row_active = s < ql;
+  const int kl = Geo::kRowLists ? 0x7fffffff : min(max(kl_raw, 0), a.Skv);
+  const bool row_active = Geo::kRowLists ? count_raw >= 0 : s < ql;
   const int lim = a.causal ? (kl - ql + s) : 0x7fffffff;
   int ntiles = row_active ? (nslots + kMlaTile - 1) / kMlaTile : 0;
 
@@ -631,7 +639,10 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
     const int idx = idx_raw[j];
     ok[j] = i < nslots && idx >= 0 && idx < kl && idx <= lim;
   }
-  if (a.block_table) {
+  if constexpr (Geo::kRowLists) {
+#pragma unroll
+    for (int j = 0; j < kIdxPerLane; ++j) row_of[j] = ok[j] ? idx_raw[j] : -1;
+  } else if (a.block_table) {
     // All lookups first (from a clamped valid entry), then the translation.
     int blk[kIdxPerLane];
     const int32_t* bt = a.block_table + (int64_t)b * a.max_blocks;
@@ -649,7 +660,7 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
 #pragma unroll
   for (int hb = 0; hb < 2; ++hb)
 #pragma unroll
-    for (int st = 0; st < kMlaD / 32; ++st) {
+    for (int st = 0; st < kD / 32; ++st) {
       if (!hb_on[hb]) qb[hb][st] = u32x4{0, 0, 0, 0};  // heads past H (wave-uniform)
       __asm__ __volatile__("" : "+v"(qb[hb][st]));
     }
@@ -660,7 +671,7 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   __syncthreads();
   // Each wave wrote 64 consecutive slots per pass; record, per tile of 32,
   // the bitmask of its valid slots.
-  uint32_t* tile_mask = reinterpret_cast<uint32_t*>(lds + kTileMaskOffset);
+  uint32_t* tile_mask = reinterpret_cast<uint32_t*>(lds + Geo::kTileMaskOffset);
   int wave_first = 0x7fffffff;  // lowest valid slot this wave saw (wave-uniform)
 #pragma unroll
   for (int j = 0; j < kIdxPerLane; ++j) {
@@ -690,6 +701,8 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   const uint32_t* tmask = tile_mask + t_first;
 
   const uint8_t* kvb = reinterpret_cast<const uint8_t*>(a.kv);
+  const uint8_t* kvb2 = reinterpret_cast<const uint8_t*>(a.kv2);
+  constexpr int kStageBytes = Geo::kStageBytes;
   constexpr int kDepth = Cfg::kDepth;
   constexpr int kL = Cfg::kMaxPerWave;
   // Every tile index below ntiles + kDepth gets a DMA (a dummy one past the
@@ -697,8 +710,8 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   if (ntiles > 0) {
 #pragma unroll
     for (int t = 0; t < kDepth; ++t) {
-      TileDma<kNW> dma;
-      dma.prepare(kvb, trows, safe_row, t, lds + (t % kStages) * kStageBytes, wave, lane, t < ntiles);
+      TileDma<kNW, kD> dma;
+      dma.prepare(kvb, kvb2, trows, safe_row, t, lds + (t % kStages) * kStageBytes, wave, lane, t < ntiles);
       il_dma_all(dma);
     }
   }
@@ -710,6 +723,8 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
     for (int i = 0; i < kMlaDV / 16; ++i) o[hb][i] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_ref[2] = {-__builtin_huge_valf(), -__builtin_huge_valf()};  // reference max (base 2)
   float lsum[2] = {0.f, 0.f};  // this lane's share of sum exp2(t - m_ref)
+  float lsum_r[2] = {0.f, 0.f};  // the same sum of P as rounded for P V (row lists only)
+  using Softmax = SoftmaxSlices<kF16, Geo::kRowLists>;
   int32_t* overflow_flag = rows + kSlotsCap;
   bool overflow = false;
 
@@ -785,8 +800,8 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
       f32x4 c[2][2];
       uint32_t qa[2];
       stage_k(0, qa);
-      TileDma<kNW> none;
-      qk_phase<kF16, kNW, false>(c, qb, qa, none);
+      TileDma<kNW, kD> none;
+      qk_phase<kF16, kNW, kD, false>(c, qb, qa, none);
       mask_scores(c, __builtin_amdgcn_readfirstlane(tmask[0]));
       // The first processed tile holds the first valid slot: it fixes m_ref.
 #pragma unroll
@@ -799,7 +814,7 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
         // sm_scale > 0, so the max commutes with the scaling.
         m_ref[hb] = cmax * scale_log2 + PRange<kF16>::kRefBias;
       }
-      SoftmaxSlices<kF16> sm{c, pa, lsum, overflow, {-m_ref[0], -m_ref[1]}, scale_log2, {}};
+      Softmax sm{c, pa, lsum, lsum_r, overflow, {-m_ref[0], -m_ref[1]}, scale_log2, {}};
       sm.template run<0>();
       sm.template run<1>();
       sm.template run<2>();
@@ -816,21 +831,21 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
       raw_barrier();
       // The DMA of tile + kDepth (into the stage tile - 1 left) goes out
       // spread over phase A.
-      TileDma<kNW> dma;
-      dma.prepare(kvb, trows, safe_row, tile + kDepth, lds + ((tile + kDepth) % kStages) * kStageBytes, wave, lane,
-                  tile + kDepth < ntiles);
+      TileDma<kNW, kD> dma;
+      dma.prepare(kvb, kvb2, trows, safe_row, tile + kDepth, lds + ((tile + kDepth) % kStages) * kStageBytes, wave,
+                  lane, tile + kDepth < ntiles);
       f32x4 c[2][2];
       uint32_t qa[2], va[2];
       stage_k(tile + 1, qa);
       stage_v(tile, va);
-      qk_phase<kF16, kNW, true>(c, qb, qa, dma);
+      qk_phase<kF16, kNW, kD, true>(c, qb, qa, dma);
       mask_scores(c, __builtin_amdgcn_readfirstlane(tmask[tile + 1]));
       u32x4 pa_next[2];
-      SoftmaxSlices<kF16> sm{c, pa_next, lsum, overflow, {-m_ref[0], -m_ref[1]}, scale_log2, {}};
+      Softmax sm{c, pa_next, lsum, lsum_r, overflow, {-m_ref[0], -m_ref[1]}, scale_log2, {}};
       u32x2 vg0[4], vg1[4];
       pv_group_reads<0>(vg0, va);
       pv_group_reads<1>(vg1, va);
-      pv_softmax_pipeline<kF16, 0>(o, pa, va, vg0, vg1, sm);
+      pv_softmax_pipeline<kF16, 0, Geo::kRowLists>(o, pa, va, vg0, vg1, sm);
       pa[0] = pa_next[0];
       pa[1] = pa_next[1];
     }
@@ -849,10 +864,13 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   const bool final_out = (a.splits == 1);
   uint16_t* obase = final_out ? a.out : a.part_o + (int64_t)split * T * a.H * kMlaDV;
   float* lbase = final_out ? a.lse : a.part_lse + (int64_t)split * T * a.H;
+  // Sinks join the softmax once: here when this workgroup writes the final
+  // output, in the combine kernel otherwise.
+  const float* sinks = Geo::kRowLists && final_out ? a.sinks : nullptr;
   if (*overflow_flag) {
-    mla_exact_fallback<kF16>(a.q, reinterpret_cast<const uint8_t*>(a.kv), obase, lbase, a.H, a.scale_log2, rows,
-                             nslots_all, token, blockIdx.y * (kNW * kHeadsPerWave), kNW * kHeadsPerWave,
-                             reinterpret_cast<float*>(lds), kNW * kWave);
+    mla_exact_fallback<kF16, kD>(a.q, kvb, kvb2, sinks, obase, lbase, a.H, a.scale_log2, rows, nslots_all, token,
+                                 blockIdx.y * (kNW * kHeadsPerWave), kNW * kHeadsPerWave,
+                                 reinterpret_cast<float*>(lds), kNW * kWave);
     return;
   }
 
@@ -864,8 +882,33 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
     float l_tot = lsum[hb];
     l_tot += __shfl_xor(l_tot, 16, kWave);
     l_tot += __shfl_xor(l_tot, 32, kWave);
-    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     const int h = head0 + 16 * hb + r;
+    float m_out = m_ref[hb];
+    if constexpr (Geo::kRowLists) {
+      // O is normalised by the rounded weights (see SoftmaxSlices), the LSE by
+      // the exact sum.
+      float l_r = lsum_r[hb];
+      l_r += __shfl_xor(l_r, 16, kWave);
+      l_r += __shfl_xor(l_r, 32, kWave);
+      inv = l_r > 0.f ? 1.f / l_r : 0.f;
+      if (sinks) {
+        // The sink adds exp(sink) to the denominator only: against M = max(m_ref,
+        // sink), l = l 2^(m_ref - M) + 2^(sink - M) and O scales by 2^(m_ref - M).
+        const float sink = sinks[min(h, a.H - 1)] * 1.4426950408889634f;
+        const float mm = fmaxf(m_ref[hb], sink);
+        const float so = fast_exp2(m_ref[hb] - mm);  // 0 when no slot was valid (m_ref = -inf)
+        const float es = fast_exp2(sink - mm);
+        l_tot = l_tot * so + es;
+        inv = so / (l_r * so + es);
+        m_out = mm;
+      }
+    }
+    if (Geo::kRowLists && !row_active) {  // padded row: out = 0, lse = 0
+      inv = 0.f;
+      l_tot = 1.f;
+      m_out = 0.f;
+    }
     if (hb_on[hb]) {
       uint16_t* orow = obase + ((int64_t)token * a.H + h) * kMlaDV + 8 * g;
 #pragma unroll
@@ -878,27 +921,35 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
       }
       if (g == 0) {
         lbase[(int64_t)token * a.H + h] =
-            l_tot > 0.f ? (m_ref[hb] + fast_log2(l_tot)) * 0.69314718055994531f : -__builtin_huge_valf();
+            l_tot > 0.f ? (m_out + fast_log2(l_tot)) * 0.69314718055994531f : -__builtin_huge_valf();
       }
     }
   }
 }
 
-// Merge split partials: lse = log(sum_i exp(lse_i)), out = sum_i exp(lse_i - lse) * o_i.
+// Merge split partials: lse = log(sum_i exp(lse_i) [+ exp(sink)]),
+// out = sum_i exp(lse_i - lse) * o_i.
 template <bool kF16>
 __global__ __launch_bounds__(256) void sparse_mla_combine_kernel(const uint16_t* __restrict__ part_o,
                                                                  const float* __restrict__ part_lse, int splits,
-                                                                 int64_t rows, uint16_t* __restrict__ out,
-                                                                 float* __restrict__ lse) {
+                                                                 int64_t rows, const float* __restrict__ sinks,
+                                                                 const int32_t* __restrict__ slot_count, int H,
+                                                                 uint16_t* __restrict__ out, float* __restrict__ lse) {
   // One thread per (row = token*H + head, 8 columns).
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t row = gid >> 6;
   const int c = (int)(gid & 63) * 8;
   if (row >= rows) return;
-  float mx = -__builtin_huge_valf();
+  if (slot_count && slot_count[row / H] < 0) {  // padded query row of a row-list call
+    *reinterpret_cast<u32x4*>(out + row * kMlaDV + c) = u32x4{0, 0, 0, 0};
+    if (c == 0) lse[row] = 0.f;
+    return;
+  }
+  const float sink = sinks ? sinks[row % H] : -__builtin_huge_valf();
+  float mx = sink;
   for (int i = 0; i < splits; ++i) mx = fmaxf(mx, part_lse[(int64_t)i * rows + row]);
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float wsum = 0.f;
+  float wsum = sinks && mx != -__builtin_huge_valf() ? __expf(sink - mx) : 0.f;
   if (mx != -__builtin_huge_valf()) {
     for (int i = 0; i < splits; ++i) {
       const float li = part_lse[(int64_t)i * rows + row];
@@ -944,31 +995,44 @@ size_t mla_workspace_bytes(int64_t tokens, int64_t H, int64_t topk) {
   return (size_t)splits * tokens * H * (kMlaDV * 2 + 4) + 256;
 }
 
-template <int kNW, bool kF16>
+template <int kNW, bool kF16, int kD>
 static hipError_t launch_mla_nw(const MlaArgs& a, int head_groups, hipStream_t stream) {
+  constexpr int kLds = MlaGeom<kD>::kLds;
   static bool attr = false;
   if (!attr) {
-    (void)hipFuncSetAttribute((const void*)sparse_mla_kernel<kNW, kF16>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              kMlaLds);
+    (void)hipFuncSetAttribute((const void*)sparse_mla_kernel<kNW, kF16, kD>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
     attr = true;
   }
   const dim3 grid((unsigned)((int64_t)a.B * a.S * a.splits), (unsigned)head_groups);
-  hipLaunchKernelGGL((sparse_mla_kernel<kNW, kF16>), grid, dim3(kNW * kWave), kMlaLds, stream, a);
+  hipLaunchKernelGGL((sparse_mla_kernel<kNW, kF16, kD>), grid, dim3(kNW * kWave), kLds, stream, a);
   return hipGetLastError();
 }
 
-template <bool kF16>
+template <bool kF16, int kD>
 static hipError_t launch_mla_dtype(const MlaArgs& a, int head_groups, int hpg, hipStream_t stream) {
   hipError_t e;
-  if (hpg > 64) e = launch_mla_nw<4, kF16>(a, head_groups, stream);
-  else if (hpg > 32) e = launch_mla_nw<2, kF16>(a, head_groups, stream);
-  else e = launch_mla_nw<1, kF16>(a, head_groups, stream);
+  if (hpg > 64) e = launch_mla_nw<4, kF16, kD>(a, head_groups, stream);
+  else if (hpg > 32) e = launch_mla_nw<2, kF16, kD>(a, head_groups, stream);
+  else e = launch_mla_nw<1, kF16, kD>(a, head_groups, stream);
   if (e != hipSuccess || a.splits == 1) return e;
   const int64_t rows = (int64_t)a.B * a.S * a.H;
   const int64_t threads = rows * (kMlaDV / 8);
   hipLaunchKernelGGL((sparse_mla_combine_kernel<kF16>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
-                     a.part_o, a.part_lse, a.splits, rows, a.out, a.lse);
+                     a.part_o, a.part_lse, a.splits, rows, a.sinks, a.slot_count, a.H, a.out, a.lse);
   return hipGetLastError();
+}
+
+static void mla_set_splits(MlaArgs& a, int64_t T, int64_t H, int64_t topk, void* workspace) {
+  const int head_groups = (int)((H + 127) / 128);
+  a.splits = mla_choose_splits(T, head_groups, topk);
+  a.keys_per_split = (int)mla_keys_per_split(topk, a.splits);
+  a.part_o = nullptr;
+  a.part_lse = nullptr;
+  if (a.splits > 1) {
+    a.part_o = static_cast<uint16_t*>(workspace);
+    a.part_lse = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + (size_t)a.splits * T * H * kMlaDV * 2);
+  }
 }
 
 // Caller validated: d_qk 576, d_v 512, H % 16 == 0, 16-bit inputs, workspace >= mla_workspace_bytes,
@@ -982,7 +1046,10 @@ hipError_t launch_sparse_mla(int is_fp16, const void* q, const void* kv, const i
   MlaArgs a;
   a.q = static_cast<const uint16_t*>(q);
   a.kv = static_cast<const uint16_t*>(kv);
+  a.kv2 = nullptr;
   a.indices = indices;
+  a.slot_count = nullptr;
+  a.sinks = nullptr;
   a.block_table = block_table;
   a.q_len = q_len;
   a.kv_len = kv_len;
@@ -998,17 +1065,47 @@ hipError_t launch_sparse_mla(int is_fp16, const void* q, const void* kv, const i
   a.causal = causal;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   const int head_groups = (int)((H + 127) / 128);
-  a.splits = mla_choose_splits(T, head_groups, topk);
-  a.keys_per_split = (int)mla_keys_per_split(topk, a.splits);
-  a.part_o = nullptr;
-  a.part_lse = nullptr;
-  if (a.splits > 1) {
-    a.part_o = static_cast<uint16_t*>(workspace);
-    a.part_lse = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + (size_t)a.splits * T * H * kMlaDV * 2);
-  }
+  mla_set_splits(a, T, H, topk, workspace);
   const int hpg = H >= 128 ? 128 : (int)H;  // heads per workgroup
-  return is_fp16 ? launch_mla_dtype<true>(a, head_groups, hpg, stream)
-                 : launch_mla_dtype<false>(a, head_groups, hpg, stream);
+  return is_fp16 ? launch_mla_dtype<true, 576>(a, head_groups, hpg, stream)
+                 : launch_mla_dtype<false, 576>(a, head_groups, hpg, stream);
+}
+
+// Attention of T query rows over per-row lists of physical KV rows (D = 512,
+// K = V): rows[t][0 .. count[t]) index kv, or kv2 when tagged kSrc2Bit, -1 =
+// empty; sinks [H] (natural log units) or null.  The V4 sparse_flash_mla
+// kernel below builds the lists.  Caller validated: H % 16 == 0, H <= 1024,
+// cap <= 2^31 / T, workspace >= mla_workspace_bytes(T, H, cap).
+hipError_t launch_sparse_mla_rows(int is_fp16, const void* q, const void* kv, const void* kv2, const int32_t* rows,
+                                  const int32_t* count, int64_t T, int64_t H, int64_t cap, const float* sinks,
+                                  float sm_scale, void* out, float* lse, void* workspace, hipStream_t stream) {
+  if (T == 0 || H == 0) return hipSuccess;
+  MlaArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.kv = static_cast<const uint16_t*>(kv);
+  a.kv2 = static_cast<const uint16_t*>(kv2);
+  a.indices = rows;
+  a.slot_count = count;
+  a.sinks = sinks;
+  a.block_table = nullptr;
+  a.q_len = nullptr;
+  a.kv_len = nullptr;
+  a.out = static_cast<uint16_t*>(out);
+  a.lse = lse;
+  a.B = 1;
+  a.S = (int)T;
+  a.H = (int)H;
+  a.Skv = 0x7fffffff;
+  a.topk = (int)cap;
+  a.block_size = 0;
+  a.max_blocks = 0;
+  a.causal = 0;
+  a.scale_log2 = sm_scale * 1.4426950408889634f;
+  const int head_groups = (int)((H + 127) / 128);
+  mla_set_splits(a, T, H, cap, workspace);
+  const int hpg = H >= 128 ? 128 : (int)H;
+  return is_fp16 ? launch_mla_dtype<true, 512>(a, head_groups, hpg, stream)
+                 : launch_mla_dtype<false, 512>(a, head_groups, hpg, stream);
 }
 
 }  // namespace dsa
