@@ -53,6 +53,19 @@ def _timed(torch, fn, reps, flush=None):
     return times
 
 
+def _timed_back_to_back(torch, fn, n):
+    """Device time (ms) per call of n calls queued back to back between two HIP events (no host
+    round trip between them: the gaps are the GPU's own launch gaps)."""
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(n):
+        fn()
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) / n
+
+
 def _median(x):
     s = sorted(x)
     return s[len(s) // 2]
@@ -296,6 +309,92 @@ STEP_KERNEL = "dsa::sparse_mla_kernel<4, false>"
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
 
 
+# Published device times of the reference's V4 sparse_flash_mla (TileLang on Ascend, msprof task
+# duration; examples/deepseek_v4/sparse_flash_mla/bench_mark.md), for the same shapes.
+V4_REFERENCE_US = {"swa_prefill": 1490.930, "hca_prefill": 3141.853, "csa_prefill": 6022.700,
+                   "swa_decode": 13.824, "hca_decode": 18.644, "csa_decode": 31.659}
+
+
+def run_v4(torch, pkg, dev, args, flush, H=64, D=512, bs=128, K=512, win=127):
+    """V4 sparse flash MLA at the reference benchmark's shapes (bench_mark.md: B=1, N1=64, D=512,
+    TND, bf16, block 128, window 127, K=512, cmp_ratio 4 (swa/csa) / 128 (hca); prefill S=8192,
+    decode one row against 8193 keys), through the C ABI on preallocated buffers.  Timed as the
+    reference times it (repeated launches, no cache flush between them: msprof task duration with
+    the first launch dropped): back-to-back launches between two events, so the figures compare
+    with V4_REFERENCE_US."""
+    from tilelang_ascend_amd import _lib as L
+    lib = pkg.load_library()
+    stream = L.stream_handle(dev)
+    g = torch.Generator(device=dev).manual_seed(20261205)
+    res = {"workload": "V4 sparse_flash_mla, B=1, N1=64, D=512, bf16, 128-row blocks, window 127, K=512, "
+                       "cmp_ratio 4 (swa, csa) / 128 (hca); prefill S=Skv=8192, decode 1 row x 8193 keys; "
+                       "warm (no flush between launches), as the reference's numbers are"}
+    for S, Skv, tag in ((8192, 8192, "prefill"), (1, 8193, "decode")):
+        q = (torch.randn((S, H, D), device=dev, generator=g) * 0.5).to(torch.bfloat16)
+        nb = (Skv + bs - 1) // bs
+        ori = (torch.randn((nb, bs, 1, D), device=dev, generator=g) * 0.5).to(torch.bfloat16)
+        obt = torch.randperm(nb, device=dev, generator=g).to(torch.int32).view(1, nb)
+        sinks = torch.randn(H, device=dev, generator=g)
+        qs = torch.zeros(1, dtype=torch.int32, device=dev)
+        ql = torch.full((1,), S, dtype=torch.int32, device=dev)
+        kl = torch.full((1,), Skv, dtype=torch.int32, device=dev)
+        out = torch.empty((S, H, D), dtype=torch.bfloat16, device=dev)
+        lse = torch.empty((S, H), dtype=torch.float32, device=dev)
+        for mode, ratio in (("swa", 4), ("hca", 128), ("csa", 4)):
+            ncmp = Skv // ratio
+            cmp = cbt = idx = None
+            if mode != "swa":
+                cnb = max(1, (ncmp + bs - 1) // bs)
+                cmp = (torch.randn((cnb, bs, 1, D), device=dev, generator=g) * 0.5).to(torch.bfloat16)
+                cbt = torch.randperm(cnb, device=dev, generator=g).to(torch.int32).view(1, cnb)
+            sg = torch.arange(S, device=dev) + (Skv - S)
+            thr = (sg + 1) // ratio
+            if mode == "csa":
+                # Row s selects min(K, thr) distinct compressed rows below its threshold, -1 padded.
+                u = torch.rand((S, max(ncmp, 1)), device=dev, generator=g)
+                u = torch.where(torch.arange(u.shape[1], device=dev)[None, :] < thr[:, None], u, -1.0)
+                v, i = torch.topk(u, min(K, u.shape[1]), dim=1)
+                idx = torch.where(v >= 0, i, -1).to(torch.int32).contiguous()
+            max_cmp = ncmp if mode == "hca" else 0
+            slots = {"swa": 0, "hca": max_cmp, "csa": K}[mode]
+            nws = lib.dsa_sparse_flash_mla_workspace_size(S, H, win, slots)
+            ws = torch.empty((max(nws, 1),), dtype=torch.uint8, device=dev)
+
+            def call():
+                rc = lib.dsa_sparse_flash_mla(
+                    L.KIND_BF16, q.data_ptr(), S, H, D, 1, qs.data_ptr(), ql.data_ptr(), kl.data_ptr(),
+                    ori.data_ptr(), nb, bs, obt.data_ptr(), nb, L.ptr(cmp), 0 if cmp is None else cmp.shape[0], bs,
+                    L.ptr(cbt), 0 if cbt is None else cbt.shape[1], L.ptr(idx), K, ratio, win, max_cmp,
+                    sinks.data_ptr(), D ** -0.5, out.data_ptr(), lse.data_ptr(), ws.data_ptr(), nws, stream)
+                L.check(rc, "sparse_flash_mla")
+
+            call()
+            torch.cuda.synchronize()
+            t = _median([_timed_back_to_back(torch, call, 10) for _ in range(max(3, args.reps // 4))])
+            keys = torch.clamp(sg, max=win) + 1
+            if mode == "hca":
+                keys = keys + thr
+            elif mode == "csa":
+                keys = keys + torch.clamp(thr, max=K)
+            n_keys = int(keys.sum().item())
+            flops = 4.0 * H * D * n_keys
+            name = f"{mode}_{tag}"
+            entry = {"us": round(t * 1e3, 2), "keys_per_row": round(n_keys / S, 1),
+                     "reference_ascend_us": V4_REFERENCE_US[name],
+                     "speedup_vs_reference": round(V4_REFERENCE_US[name] / (t * 1e3), 2)}
+            if tag == "prefill":
+                entry["tflops"] = round(flops / (t * 1e-3) / 1e12, 1)
+                entry["frac_bf16_peak"] = round(flops / (t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)
+            else:
+                nbytes = n_keys * D * 2 + q.numel() * 2 + out.numel() * 2
+                entry["gbs"] = round(nbytes / (t * 1e-3) / 1e9, 1)
+            res[name] = entry
+            _log(f"V4 {name}: {t * 1e3:.1f} us ({entry.get('tflops', entry.get('gbs'))})")
+            del cmp, cbt, idx, ws
+        del q, ori, obt, out, lse
+    return res
+
+
 def _rocpd(db):
     import sqlite3
 
@@ -390,7 +489,7 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--reps", type=int, default=20, help="repetitions of the secondary (flushed) benchmarks")
-    ap.add_argument("--skip", default="", help="comma list of parts to skip: step,indexer,decode,c5,cpu")
+    ap.add_argument("--skip", default="", help="comma list of parts to skip: step,indexer,decode,c5,v4,cpu")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy (HBM byte-counter calibration for rocprof)")
     args = ap.parse_args()
@@ -524,6 +623,10 @@ def main():
     # ---------------- full DSA layer at 128K context (C5) ----------------
     if "c5" not in skip:
         result["layer_128k"] = run_c5(torch, pkg, dev, args, flush)
+
+    # ---------------- V4 sparse flash MLA at the reference benchmark's shapes ----------------
+    if "v4" not in skip:
+        result["v4_sparse_flash_mla"] = run_v4(torch, pkg, dev, args, flush)
 
     del flush
     if "cpu" not in skip and cpu_inputs is not None:
