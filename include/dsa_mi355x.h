@@ -31,6 +31,8 @@ extern "C" {
 #define DSA_KIND_FP8_E4M3 0 /* OCP float8 e4m3fn (torch.float8_e4m3fn) */
 #define DSA_KIND_BF16 1
 #define DSA_KIND_FP16 2
+#define DSA_KIND_FP32 3 /* act_quant input */
+#define DSA_KIND_INT8 4 /* act_quant output */
 
 /* Library ABI version (major * 100 + minor). */
 int dsa_abi_version(void);
@@ -209,6 +211,20 @@ int dsa_sparse_flash_mla(int kind, const void* q, int64_t T, int64_t H, int64_t 
                          int64_t topk_cmp, int64_t cmp_ratio, int64_t ori_win_left, int64_t max_cmp,
                          const float* sinks, float softmax_scale, void* out, float* lse, void* workspace,
                          size_t workspace_bytes, void* stream);
+
+/*
+ * Per-row activation quantiser, the producer of the indexer's low-precision
+ * inputs.  Replaces `act_quant_kernel_int8_optimized` / `act_quant_torch`
+ * (examples/deepseek_v4/act_quant.py:33-92, :118-142) and extends it to fp8:
+ *   amax = max(max |x[r, :]|, 1e-4); scale[r] = amax / QMAX, or with round_scale
+ *   2^ceil(log2(amax / QMAX)); y[r, :] = clamp(x / scale, -QMAX, QMAX) converted
+ * with QMAX = 127 and round-half-to-even for DSA_KIND_INT8, QMAX = 448 and
+ * round-to-nearest-even for DSA_KIND_FP8_E4M3 (OCP e4m3fn).
+ *  x [rows, n] of in_kind (bf16, fp16 or fp32); y [rows, n] (1 byte each);
+ *  scales [rows] fp32.
+ */
+int dsa_act_quant(int in_kind, const void* x, int64_t rows, int64_t n, int out_kind, void* y, float* scales,
+                  int round_scale, void* stream);
 
 #ifdef __cplusplus
 }

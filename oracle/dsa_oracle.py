@@ -40,6 +40,11 @@ How each function is pinned (see ``tests/test_oracle.py``):
   ``torch.logsumexp``.
 * ``fp8_quantize_per_token``: absmax maps to 448, representable values round
   trip exactly.
+* ``act_quant`` (``examples/deepseek_v4/act_quant.py:118-142``, int8, extended
+  to fp8 e4m3fn): a hand-worked int8 row with half-way cases, the 1e-4 floor
+  of an all-zero row, power-of-two scales with ``round_scale``, the error bound
+  |x - y * scale| <= scale / 2 (int8), and fp8 values on the e4m3 grid (and
+  midpoints between grid points rounding to the even neighbour).
 * ``v4_slots`` / ``sparse_flash_mla`` (DeepSeek V4 window + compressed
   attention with sinks, ``examples/deepseek_v4/sparse_flash_mla/sparse_flash_mla_golden.py:15-160``):
   hand-worked slot lists (window clipping, hca threshold, the csa walk that
@@ -77,6 +82,28 @@ def fp8_quantize_per_token(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]
     scale = torch.where(amax > 0, amax / FP8_MAX, torch.ones_like(amax))
     q = (xf / scale.unsqueeze(-1)).clamp(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn)
     return q, scale.to(torch.float32)
+
+
+def act_quant(x: torch.Tensor, round_scale: bool = False,
+              dtype: torch.dtype = torch.int8) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-row quantiser (examples/deepseek_v4/act_quant.py:118-142): amax =
+    max(|x|) per row clamped to >= 1e-4, scale = amax / QMAX (round_scale:
+    2^ceil(log2(amax / QMAX))), y = clamp(x / scale, -QMAX, QMAX) rounded half
+    to even (int8, QMAX 127) or to nearest-even e4m3fn (fp8, QMAX 448).
+    Returns (y shaped like x, scales [M, 1] or [B, S, 1])."""
+    qmax = 127.0 if dtype == torch.int8 else FP8_MAX
+    shape = x.shape
+    x2 = x.reshape(-1, shape[-1]).float()
+    amax = torch.clamp(x2.abs().amax(dim=1, keepdim=True), min=1e-4)
+    scales = amax / qmax
+    if round_scale:
+        scales = torch.pow(2.0, torch.ceil(torch.log2(scales)))
+    clipped = torch.clamp(x2 / scales, -qmax, qmax)
+    if dtype == torch.int8:
+        y = torch.round(clipped).to(torch.float16).to(torch.int8)
+    else:
+        y = clipped.to(torch.float8_e4m3fn)
+    return y.reshape(shape), scales.reshape(shape[:-1] + (1,))
 
 
 # ----------------------------------------------------------------------------

@@ -352,3 +352,36 @@ def test_v4_golden_mode_matches_exact_without_rounding():
                               golden_p_dtype=torch.bfloat16)
     d = (gb[0] - ex[0]).abs().max().item()
     assert 0 < d < 2e-2
+
+
+def test_act_quant_int8_hand_worked():
+    # amax 127 -> scale exactly 1: half-way values go to the even integer.
+    x = torch.tensor([[127.0, 63.5, 62.5, -0.5, 0.5, 1.5, -2.5, -127.0]])
+    y, s = ref.act_quant(x)
+    assert s.item() == 1.0
+    assert y[0].tolist() == [127, 64, 62, 0, 0, 2, -2, -127]
+    # An all-zero row: the 1e-4 floor, y = 0.
+    y0, s0 = ref.act_quant(torch.zeros(1, 8))
+    assert torch.all(y0 == 0) and abs(s0.item() - 1e-4 / 127) < 1e-12
+    # round_scale: power-of-two scale at or above amax / 127.
+    g = torch.Generator().manual_seed(1)
+    xr = torch.randn(16, 64, generator=g)
+    _, sr = ref.act_quant(xr, round_scale=True)
+    m = torch.log2(sr)
+    assert torch.equal(m, torch.round(m)) and torch.all(sr >= xr.abs().amax(1, keepdim=True) / 127)
+    assert torch.all(sr < 2 * xr.abs().amax(1, keepdim=True) / 127)
+    # Error bound.
+    yq, sq = ref.act_quant(xr)
+    assert torch.all((xr - yq.float() * sq).abs() <= sq / 2 + 1e-7)
+
+
+def test_act_quant_fp8_grid():
+    # Row max 448 -> scale 1; e4m3 grid points stay, midpoints go to the even neighbour.
+    x = torch.tensor([[448.0, 1.0, 1.125, 1.0625, 1.1875, -3.5, 0.001953125, 0.0029296875]])
+    y, s = ref.act_quant(x, dtype=torch.float8_e4m3fn)
+    assert s.item() == 1.0
+    got = y.float()[0].tolist()
+    # 1.0625 is the midpoint of 1.0 and 1.125 (mantissa 000 / 001): even -> 1.0;
+    # 1.1875 is the midpoint of 1.125 and 1.25 (001 / 010): even -> 1.25;
+    # 2^-9 is the smallest subnormal; 1.5 * 2^-9 is a midpoint -> 2 * 2^-9 (even).
+    assert got == [448.0, 1.0, 1.125, 1.0, 1.25, -3.5, 0.001953125, 0.00390625]

@@ -18,6 +18,8 @@ LIB_PATH = PKG_DIR / "libdsa_mi355x.so"
 KIND_FP8_E4M3 = 0
 KIND_BF16 = 1
 KIND_FP16 = 2
+KIND_FP32 = 3
+KIND_INT8 = 4
 
 _c_i64 = ctypes.c_int64
 _c_int = ctypes.c_int
@@ -51,6 +53,7 @@ SIGNATURES = {
                                       _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp,
                                       _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_float, _c_vp, _c_vp, _c_vp, _c_size,
                                       _c_vp]),
+    "dsa_act_quant": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_int, _c_vp, _c_vp, _c_int, _c_vp]),
     "dsa_sparse_mla_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64]),
     "dsa_sparse_mla_fwd": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64,
                                     _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_float, _c_int, _c_vp, _c_vp, _c_vp,
@@ -85,6 +88,22 @@ def load_library() -> ctypes.CDLL:
         fn.argtypes = args
     _lib = lib
     return lib
+
+
+TORCH_OPS_PATH = PKG_DIR / "libdsa_torch_ops.so"
+_torch_ops_loaded = False
+
+
+def load_torch_ops():
+    """Register ``torch.ops.dsa.*`` (loads libdsa_torch_ops.so once) and return the namespace."""
+    global _torch_ops_loaded
+    if not _torch_ops_loaded:
+        load_library()
+        if not TORCH_OPS_PATH.exists():
+            raise ImportError(f"{TORCH_OPS_PATH} is missing: build it with `python tilelang-ascend_amd/build.py`")
+        torch.ops.load_library(str(TORCH_OPS_PATH))
+        _torch_ops_loaded = True
+    return torch.ops.dsa
 
 
 def check(rc: int, what: str) -> None:

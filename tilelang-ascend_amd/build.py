@@ -19,6 +19,9 @@ CSRC = PKG_DIR / "csrc"
 BUILD_DIR = PKG_DIR / "_build"
 LIB_NAME = "libdsa_mi355x.so"
 LIB_PATH = PKG_DIR / LIB_NAME
+# torch.ops.dsa.* registrations (csrc/torch_ops.cpp): host C++ over the C ABI, linked against
+# libdsa_mi355x.so and libtorch; built separately so the C-ABI library stays free of torch.
+TORCH_OPS_PATH = PKG_DIR / "libdsa_torch_ops.so"
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -69,7 +72,30 @@ def build(verbose: bool = False, jobs: int = 8) -> Path:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, LIB_PATH)
+    build_torch_ops(verbose)
     return LIB_PATH
+
+
+def build_torch_ops(verbose: bool = False) -> Path:
+    """Compile csrc/torch_ops.cpp (host only, g++) into libdsa_torch_ops.so."""
+    import torch
+    from torch.utils import cpp_extension
+
+    torch_lib = Path(torch.__file__).resolve().parent / "lib"
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    tmp = TORCH_OPS_PATH.with_suffix(".so.tmp")
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-DUSE_ROCM",
+           "-D__HIP_PLATFORM_AMD__", *[f"-I{d}" for d in cpp_extension.include_paths()], "-I/opt/rocm/include",
+           str(CSRC / "torch_ops.cpp"), "-o", str(tmp), f"-L{PKG_DIR}", "-ldsa_mi355x", f"-L{torch_lib}",
+           "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-lc10", "-lc10_hip", "-Wl,-rpath,$ORIGIN",
+           f"-Wl,-rpath,{torch_lib}"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"torch_ops.cpp failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, TORCH_OPS_PATH)
+    return TORCH_OPS_PATH
 
 
 if __name__ == "__main__":

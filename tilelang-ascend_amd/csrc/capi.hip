@@ -20,6 +20,8 @@ hipError_t launch_sparse_mla(int is_fp16, const void* q, const void* kv, const i
                              int causal, void* out, float* lse, void* workspace, hipStream_t stream);
 size_t mla_workspace_bytes(int64_t tokens, int64_t H, int64_t topk);
 size_t v4_workspace_bytes(int64_t T, int64_t H, int64_t cap);
+hipError_t launch_act_quant(int in_kind, const void* x, int64_t rows, int64_t n, int out_kind, void* y,
+                            float* scales, int round_scale, hipStream_t stream);
 hipError_t launch_sparse_flash_mla(int is_fp16, const void* q, int64_t T, int64_t H, int64_t B,
                                    const int32_t* q_start, const int32_t* q_len, const int32_t* kv_len,
                                    const void* ori_kv, int64_t ori_blocks, int64_t ori_bs, const int32_t* ori_bt,
@@ -294,6 +296,17 @@ int dsa_sparse_flash_mla(int kind, const void* q, int64_t T, int64_t H, int64_t 
                                          cmp_block_num, cmp_block_size, cmp_block_table, cmp_table_len,
                                          cmp_sparse_indices, topk_cmp, cmp_ratio, ori_win_left, max_cmp, mode, cap,
                                          sinks, softmax_scale, out, lse, workspace, static_cast<hipStream_t>(stream)));
+}
+
+int dsa_act_quant(int in_kind, const void* x, int64_t rows, int64_t n, int out_kind, void* y, float* scales,
+                  int round_scale, void* stream) {
+  if (in_kind != DSA_KIND_BF16 && in_kind != DSA_KIND_FP16 && in_kind != DSA_KIND_FP32)
+    return reject("act_quant: input kind must be bf16, fp16 or fp32");
+  if (out_kind != DSA_KIND_FP8_E4M3 && out_kind != DSA_KIND_INT8) return reject("act_quant: output kind must be fp8 or int8");
+  if (rows < 0 || n < 0 || n > kMaxInt || (n > 0 && rows > ((int64_t)1 << 62) / n)) return reject("act_quant: bad sizes");
+  if (rows * n > 0 && (!x || !y || !scales)) return reject("act_quant: null pointer");
+  return ok(dsa::launch_act_quant(in_kind, x, rows, n, out_kind, y, scales, round_scale ? 1 : 0,
+                                  static_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

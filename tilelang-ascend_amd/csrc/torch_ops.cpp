@@ -1,0 +1,269 @@
+// PyTorch operator registration of the DSA kernels: torch.ops.dsa.*.
+//
+// The pattern of examples/torch_tl_ascend/src/_inner.cpp:17-68 (a wrapper that
+// allocates outputs and workspaces with ATen, fetches the current stream and
+// calls the C entry point; TORCH_LIBRARY schemas; device and Meta
+// implementations), for a HIP device: the device implementations call the C
+// ABI of include/dsa_mi355x.h on the current HIP stream; the Meta
+// implementations only compute output shapes, so the ops trace under
+// torch.compile / FakeTensor.  No implementation synchronises with the host or
+// allocates outside ATen's caching allocator, so the calls can be captured in a
+// HIP graph.  Sizes that the Python wrappers read from device tensors (the
+// longest paged key length) are explicit arguments here.
+#include <ATen/ATen.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include "../../include/dsa_mi355x.h"
+
+namespace {
+
+void* ptr(const at::Tensor& t) { return t.data_ptr(); }
+template <typename T>
+T* ptr_or_null(const c10::optional<at::Tensor>& t) {
+  return t.has_value() ? static_cast<T*>(t->data_ptr()) : nullptr;
+}
+
+void* stream_of(const at::Tensor& t) { return c10::hip::getCurrentHIPStream(t.device().index()).stream(); }
+
+void check_rc(int rc, const char* what) {
+  TORCH_CHECK(rc == 0, "dsa.", what, ": ", dsa_last_error_message(), " (hipError ", rc, ")");
+}
+
+int kind_of(const at::Tensor& t) {
+  switch (t.scalar_type()) {
+    case at::kFloat8_e4m3fn: return DSA_KIND_FP8_E4M3;
+    case at::kBFloat16: return DSA_KIND_BF16;
+    case at::kHalf: return DSA_KIND_FP16;
+    case at::kFloat: return DSA_KIND_FP32;
+    case at::kChar: return DSA_KIND_INT8;
+    default: TORCH_CHECK(false, "dsa: unsupported dtype ", t.scalar_type());
+  }
+  return -1;
+}
+
+c10::optional<at::Tensor> i32(const c10::optional<at::Tensor>& t) {
+  if (!t.has_value()) return t;
+  return t->to(at::kInt).contiguous();
+}
+
+void require(const at::Tensor& t, const char* name) {
+  TORCH_CHECK(t.is_cuda(), "dsa: ", name, " must be on a HIP device");
+  TORCH_CHECK(t.is_contiguous(), "dsa: ", name, " must be contiguous");
+}
+
+// ---------------------------------------------------------------- top-k
+std::tuple<at::Tensor, at::Tensor> topk_select(const at::Tensor& x, int64_t k, bool sorted) {
+  require(x, "x");
+  TORCH_CHECK(x.dim() == 2 && x.scalar_type() == at::kFloat, "dsa.topk_select: x must be [rows, n] fp32");
+  c10::OptionalDeviceGuard guard(x.device());
+  const int64_t rows = x.size(0), n = x.size(1);
+  auto idx = at::empty({rows, k}, x.options().dtype(at::kInt));
+  auto val = at::empty({rows, k}, x.options());
+  const size_t ws_bytes = dsa_topk_select_workspace_size(rows, n, k);
+  auto ws = at::empty({(int64_t)(ws_bytes > 0 ? ws_bytes : 1)}, x.options().dtype(at::kByte));
+  check_rc(dsa_topk_select_ws(static_cast<const float*>(ptr(x)), n, rows, n, k, nullptr, sorted ? 1 : 0,
+                              static_cast<int32_t*>(ptr(idx)), static_cast<float*>(ptr(val)), ptr(ws), ws_bytes,
+                              stream_of(x)),
+           "topk_select");
+  return {idx, val};
+}
+
+std::tuple<at::Tensor, at::Tensor> topk_select_meta(const at::Tensor& x, int64_t k, bool) {
+  return {at::empty({x.size(0), k}, x.options().dtype(at::kInt)), at::empty({x.size(0), k}, x.options())};
+}
+
+// ---------------------------------------------------------------- lightning indexer (BSND query)
+// query [B, S1, H, D]; key [B, S2, 1, D] or paged [blocks, block_size, 1, D] with block_table, in
+// which case s2 (the longest key length) is required.
+std::tuple<at::Tensor, at::Tensor> lightning_indexer(const at::Tensor& query, const at::Tensor& key,
+                                                     const at::Tensor& weights,
+                                                     const c10::optional<at::Tensor>& key_scale,
+                                                     const c10::optional<at::Tensor>& actual_seq_lengths_query,
+                                                     const c10::optional<at::Tensor>& actual_seq_lengths_key,
+                                                     const c10::optional<at::Tensor>& block_table,
+                                                     int64_t sparse_count, int64_t sparse_mode, bool return_value,
+                                                     int64_t s2) {
+  require(query, "query");
+  require(key, "key");
+  TORCH_CHECK(query.dim() == 4 && key.dim() == 4, "dsa.lightning_indexer: query and key must be 4-D");
+  c10::OptionalDeviceGuard guard(query.device());
+  const int64_t B = query.size(0), S1 = query.size(1), H = query.size(2), D = query.size(3);
+  const bool paged = block_table.has_value();
+  TORCH_CHECK(!paged || s2 > 0, "dsa.lightning_indexer: paged keys need s2 (the longest key length)");
+  const int64_t S2 = paged ? s2 : key.size(1);
+  auto w = weights.to(at::kFloat).contiguous();
+  auto ks = key_scale.has_value() ? c10::optional<at::Tensor>(key_scale->to(at::kFloat).contiguous()) : key_scale;
+  auto aq = i32(actual_seq_lengths_query), ak = i32(actual_seq_lengths_key), bt = i32(block_table);
+  auto idx = at::empty({B, S1, 1, sparse_count}, query.options().dtype(at::kInt));
+  auto val = return_value ? at::empty({B, S1, 1, sparse_count}, query.options().dtype(at::kFloat))
+                          : at::empty({0}, query.options().dtype(at::kFloat));
+  if (B * S1 == 0) return {idx, val};
+  const size_t ws_bytes = dsa_lightning_indexer_workspace_size(B, S1, S2, sparse_count);
+  auto ws = at::empty({(int64_t)(ws_bytes > 0 ? ws_bytes : 1)}, query.options().dtype(at::kByte));
+  check_rc(dsa_lightning_indexer(kind_of(query), ptr(query), ptr(key), ptr_or_null<float>(ks),
+                                 static_cast<float*>(ptr(w)), B, S1, S2, H, D, ptr_or_null<int32_t>(aq),
+                                 ptr_or_null<int32_t>(ak), ptr_or_null<int32_t>(bt), paged ? key.size(1) : 0,
+                                 paged ? bt->size(1) : 0, (int)sparse_mode, sparse_count,
+                                 static_cast<int32_t*>(ptr(idx)), return_value ? static_cast<float*>(ptr(val)) : nullptr,
+                                 ptr(ws), ws_bytes, stream_of(query)),
+           "lightning_indexer");
+  return {idx, val};
+}
+
+std::tuple<at::Tensor, at::Tensor> lightning_indexer_meta(const at::Tensor& query, const at::Tensor&,
+                                                          const at::Tensor&, const c10::optional<at::Tensor>&,
+                                                          const c10::optional<at::Tensor>&,
+                                                          const c10::optional<at::Tensor>&,
+                                                          const c10::optional<at::Tensor>&, int64_t sparse_count,
+                                                          int64_t, bool return_value, int64_t) {
+  const int64_t B = query.size(0), S1 = query.size(1);
+  auto idx = at::empty({B, S1, 1, sparse_count}, query.options().dtype(at::kInt));
+  auto val = return_value ? at::empty({B, S1, 1, sparse_count}, query.options().dtype(at::kFloat))
+                          : at::empty({0}, query.options().dtype(at::kFloat));
+  return {idx, val};
+}
+
+// ---------------------------------------------------------------- sparse MLA (d_qk 576, d_v 512)
+std::tuple<at::Tensor, at::Tensor> sparse_mla_fwd(const at::Tensor& q, const at::Tensor& kv,
+                                                  const at::Tensor& indices, double sm_scale,
+                                                  const c10::optional<at::Tensor>& block_table,
+                                                  const c10::optional<at::Tensor>& actual_seq_lengths_query,
+                                                  const c10::optional<at::Tensor>& actual_seq_lengths_kv,
+                                                  bool is_causal) {
+  require(q, "q");
+  require(kv, "kv");
+  require(indices, "indices");
+  TORCH_CHECK(q.dim() == 4 && kv.dim() == 4 && indices.scalar_type() == at::kInt,
+              "dsa.sparse_mla_fwd: q [B, S, H, 576], kv 4-D, int32 indices");
+  c10::OptionalDeviceGuard guard(q.device());
+  const int64_t B = q.size(0), S = q.size(1), H = q.size(2), topk = indices.size(-1);
+  auto bt = i32(block_table), aq = i32(actual_seq_lengths_query), ak = i32(actual_seq_lengths_kv);
+  auto out = at::empty({B, S, H, 512}, q.options());
+  auto lse = at::empty({B, S, H}, q.options().dtype(at::kFloat));
+  const size_t ws_bytes = dsa_sparse_mla_workspace_size(B, S, H, topk);
+  auto ws = at::empty({(int64_t)(ws_bytes > 0 ? ws_bytes : 1)}, q.options().dtype(at::kByte));
+  const bool paged = bt.has_value();
+  const int64_t nblk = paged ? bt->size(1) : 0, bs = paged ? kv.size(1) : 0;
+  check_rc(dsa_sparse_mla_fwd(kind_of(q), ptr(q), ptr(kv), static_cast<const int32_t*>(ptr(indices)),
+                              ptr_or_null<int32_t>(bt), ptr_or_null<int32_t>(aq), ptr_or_null<int32_t>(ak), B, S, H,
+                              576, 512, paged ? nblk * bs : kv.size(1), bs, nblk, topk, (float)sm_scale,
+                              is_causal ? 1 : 0, ptr(out), static_cast<float*>(ptr(lse)), ptr(ws), ws_bytes,
+                              stream_of(q)),
+           "sparse_mla_fwd");
+  return {out, lse};
+}
+
+std::tuple<at::Tensor, at::Tensor> sparse_mla_fwd_meta(const at::Tensor& q, const at::Tensor&, const at::Tensor&,
+                                                       double, const c10::optional<at::Tensor>&,
+                                                       const c10::optional<at::Tensor>&,
+                                                       const c10::optional<at::Tensor>&, bool) {
+  return {at::empty({q.size(0), q.size(1), q.size(2), 512}, q.options()),
+          at::empty({q.size(0), q.size(1), q.size(2)}, q.options().dtype(at::kFloat))};
+}
+
+// ---------------------------------------------------------------- V4 sparse flash MLA (TND rows)
+// q [T, H, 512]; q_start / q_len / seqused_kv [B]; caches [blocks, block_size, 1, 512].
+std::tuple<at::Tensor, at::Tensor> sparse_flash_mla(
+    const at::Tensor& q, const at::Tensor& ori_kv, const at::Tensor& ori_block_table, const at::Tensor& q_start,
+    const at::Tensor& q_len, const at::Tensor& seqused_kv, const c10::optional<at::Tensor>& sinks,
+    double softmax_scale, const c10::optional<at::Tensor>& cmp_kv, const c10::optional<at::Tensor>& cmp_block_table,
+    const c10::optional<at::Tensor>& cmp_sparse_indices, int64_t cmp_ratio, int64_t ori_win_left, int64_t max_cmp) {
+  require(q, "q");
+  require(ori_kv, "ori_kv");
+  TORCH_CHECK(q.dim() == 3, "dsa.sparse_flash_mla: q must be [T, H, 512]");
+  c10::OptionalDeviceGuard guard(q.device());
+  const int64_t T = q.size(0), H = q.size(1), B = q_start.numel();
+  auto obt = ori_block_table.to(at::kInt).contiguous();
+  auto qs = q_start.to(at::kInt).contiguous(), ql = q_len.to(at::kInt).contiguous();
+  auto kl = seqused_kv.to(at::kInt).contiguous();
+  auto sk = sinks.has_value() ? c10::optional<at::Tensor>(sinks->to(at::kFloat).contiguous()) : sinks;
+  auto cbt = i32(cmp_block_table), idx = i32(cmp_sparse_indices);
+  const int64_t K = idx.has_value() ? idx->size(-1) : 0;
+  const int64_t cmp_slots = cmp_kv.has_value() ? (idx.has_value() ? K : max_cmp) : 0;
+  auto out = at::empty({T, H, 512}, q.options());
+  auto lse = at::empty({T, H}, q.options().dtype(at::kFloat));
+  const size_t ws_bytes = dsa_sparse_flash_mla_workspace_size(T, H, ori_win_left, cmp_slots);
+  auto ws = at::empty({(int64_t)(ws_bytes > 0 ? ws_bytes : 1)}, q.options().dtype(at::kByte));
+  const at::Tensor* c = cmp_kv.has_value() ? &*cmp_kv : nullptr;
+  check_rc(dsa_sparse_flash_mla(kind_of(q), ptr(q), T, H, 512, B, static_cast<int32_t*>(ptr(qs)),
+                                static_cast<int32_t*>(ptr(ql)), static_cast<int32_t*>(ptr(kl)), ptr(ori_kv),
+                                ori_kv.size(0), ori_kv.size(1), static_cast<int32_t*>(ptr(obt)), obt.size(1),
+                                c ? ptr(*c) : nullptr, c ? c->size(0) : 0, c ? c->size(1) : 0,
+                                ptr_or_null<int32_t>(cbt), cbt.has_value() ? cbt->size(1) : 0,
+                                ptr_or_null<int32_t>(idx), K, cmp_ratio, ori_win_left, max_cmp, ptr_or_null<float>(sk),
+                                (float)softmax_scale, ptr(out), static_cast<float*>(ptr(lse)), ptr(ws), ws_bytes,
+                                stream_of(q)),
+           "sparse_flash_mla");
+  return {out, lse};
+}
+
+std::tuple<at::Tensor, at::Tensor> sparse_flash_mla_meta(
+    const at::Tensor& q, const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&, const at::Tensor&,
+    const c10::optional<at::Tensor>&, double, const c10::optional<at::Tensor>&, const c10::optional<at::Tensor>&,
+    const c10::optional<at::Tensor>&, int64_t, int64_t, int64_t) {
+  return {at::empty({q.size(0), q.size(1), 512}, q.options()),
+          at::empty({q.size(0), q.size(1)}, q.options().dtype(at::kFloat))};
+}
+
+// ---------------------------------------------------------------- producer
+std::tuple<at::Tensor, at::Tensor> act_quant(const at::Tensor& x, bool round_scale,
+                                             c10::optional<at::ScalarType> dtype_opt) {
+  require(x, "x");
+  const at::ScalarType dtype = dtype_opt.value_or(at::kChar);
+  TORCH_CHECK(dtype == at::kChar || dtype == at::kFloat8_e4m3fn, "dsa.act_quant: dtype must be int8 or float8_e4m3fn");
+  c10::OptionalDeviceGuard guard(x.device());
+  const int64_t n = x.size(-1), rows = n ? x.numel() / n : 0;
+  auto y = at::empty(x.sizes(), x.options().dtype(dtype));
+  auto sizes = x.sizes().vec();
+  sizes.back() = 1;
+  auto s = at::empty(sizes, x.options().dtype(at::kFloat));
+  if (rows * n > 0)
+    check_rc(dsa_act_quant(kind_of(x), ptr(x), rows, n, dtype == at::kChar ? DSA_KIND_INT8 : DSA_KIND_FP8_E4M3,
+                           ptr(y), static_cast<float*>(ptr(s)), round_scale ? 1 : 0, stream_of(x)),
+             "act_quant");
+  return {y, s};
+}
+
+std::tuple<at::Tensor, at::Tensor> act_quant_meta(const at::Tensor& x, bool, c10::optional<at::ScalarType> dtype_opt) {
+  const at::ScalarType dtype = dtype_opt.value_or(at::kChar);
+  auto sizes = x.sizes().vec();
+  sizes.back() = 1;
+  return {at::empty(x.sizes(), x.options().dtype(dtype)), at::empty(sizes, x.options().dtype(at::kFloat))};
+}
+
+}  // namespace
+
+TORCH_LIBRARY(dsa, m) {
+  m.def("topk_select(Tensor x, int k, bool sorted=True) -> (Tensor, Tensor)");
+  m.def(
+      "lightning_indexer(Tensor query, Tensor key, Tensor weights, Tensor? key_scale=None, "
+      "Tensor? actual_seq_lengths_query=None, Tensor? actual_seq_lengths_key=None, Tensor? block_table=None, "
+      "int sparse_count=2048, int sparse_mode=3, bool return_value=False, int s2=-1) -> (Tensor, Tensor)");
+  m.def(
+      "sparse_mla_fwd(Tensor q, Tensor kv, Tensor indices, float sm_scale, Tensor? block_table=None, "
+      "Tensor? actual_seq_lengths_query=None, Tensor? actual_seq_lengths_kv=None, bool is_causal=True) "
+      "-> (Tensor, Tensor)");
+  m.def(
+      "sparse_flash_mla(Tensor q, Tensor ori_kv, Tensor ori_block_table, Tensor q_start, Tensor q_len, "
+      "Tensor seqused_kv, Tensor? sinks, float softmax_scale, Tensor? cmp_kv=None, Tensor? cmp_block_table=None, "
+      "Tensor? cmp_sparse_indices=None, int cmp_ratio=4, int ori_win_left=127, int max_cmp=0) -> (Tensor, Tensor)");
+  m.def("act_quant(Tensor x, bool round_scale=False, ScalarType? dtype=None) -> (Tensor, Tensor)");
+}
+
+TORCH_LIBRARY_IMPL(dsa, CUDA, m) {
+  m.impl("topk_select", &topk_select);
+  m.impl("lightning_indexer", &lightning_indexer);
+  m.impl("sparse_mla_fwd", &sparse_mla_fwd);
+  m.impl("sparse_flash_mla", &sparse_flash_mla);
+  m.impl("act_quant", &act_quant);
+}
+
+TORCH_LIBRARY_IMPL(dsa, Meta, m) {
+  m.impl("topk_select", &topk_select_meta);
+  m.impl("lightning_indexer", &lightning_indexer_meta);
+  m.impl("sparse_mla_fwd", &sparse_mla_fwd_meta);
+  m.impl("sparse_flash_mla", &sparse_flash_mla_meta);
+  m.impl("act_quant", &act_quant_meta);
+}

@@ -9,7 +9,9 @@ returning ``(indices [B, S1, 1, K] int32, values)``) and the builder
 Superset of the reference: fp8-e4m3 (``torch.float8_e4m3fn``) query/key with an
 optional per-key fp32 scale (``key_scale``); the logit is
 ``key_scale[s] * sum_h w[t, h] * ReLU(q[t, h] . k[s])``.  With fp16/bf16 inputs
-and no scale it is the reference formula.
+and no scale it is the reference formula.  A quantised query's per-(token,
+head) scale (``query_scale``, from ``act_quant``) is folded into the head
+weights: ReLU(s x) = s ReLU(x) for s >= 0.
 """
 from __future__ import annotations
 
@@ -83,6 +85,16 @@ def _paged_key(key, block_table, actual_seq_lengths_key, B, D, dev):
     return bt, block_size, max_blocks, ak, S2
 
 
+def _fold_query_scale(w, query_scale):
+    """Head weights times the query's per-(token, head) scale (non-negative)."""
+    if query_scale is None:
+        return w
+    qs = query_scale.to(device=w.device, dtype=torch.float32)
+    if qs.numel() != w.numel():
+        raise ValueError(f"query_scale must hold one fp32 per (token, head) ({w.numel()}), got {qs.numel()}")
+    return (w * qs.reshape(w.shape)).contiguous()
+
+
 def _key_scale(key_scale, rows):
     if key_scale is None:
         return None
@@ -110,7 +122,7 @@ def _prefix_sums(seq, total, what, dev):
 
 
 def _prepare_tnd(query, key, weights, key_scale, actual_seq_lengths_query, actual_seq_lengths_key, block_table,
-                 layout_key):
+                 layout_key, query_scale=None):
     """Packed query rows [T, N1, D] addressed in place through prefix sums
     (the reference pads them to BSND on the host, lightning_indexer.py:48-94)."""
     dev = _lib.require_device(query, key, weights, key_scale, block_table)
@@ -138,13 +150,13 @@ def _prepare_tnd(query, key, weights, key_scale, actual_seq_lengths_query, actua
         raise ValueError(f"TND weights must be [T, N1] = {(T, N1)}, got {tuple(weights.shape)}")
     for name, t in (("query", query), ("key", key)):
         _lib.require_contiguous(name, t)
-    w = weights.reshape(T, N1).to(torch.float32).contiguous()
+    w = _fold_query_scale(weights.reshape(T, N1).to(torch.float32).contiguous(), query_scale)
     T_rows = int(cu_q[-1].item())
     return dev, B, T, T_rows, S1, S2, N1, D, w, ks, cu_q, cu_k, ak, bt, block_size, max_blocks
 
 
 def _prepare(query, key, weights, key_scale, actual_seq_lengths_query, actual_seq_lengths_key, block_table,
-             layout_query, layout_key, sparse_mode):
+             layout_query, layout_key, sparse_mode, query_scale=None):
     _check_common(query, key, weights, layout_query, layout_key, sparse_mode)
     dev = _lib.require_device(query, key, weights, key_scale, block_table)
     if query.dim() != 4:
@@ -169,7 +181,7 @@ def _prepare(query, key, weights, key_scale, actual_seq_lengths_query, actual_se
         raise ValueError(f"weights must be [B, S1, N1] = {(B, S1, N1)}, got {tuple(weights.shape)}")
     for name, t in (("query", query), ("key", key)):
         _lib.require_contiguous(name, t)
-    w = weights.reshape(B, S1, N1).to(torch.float32).contiguous()
+    w = _fold_query_scale(weights.reshape(B, S1, N1).to(torch.float32).contiguous(), query_scale)
     ks = _key_scale(key_scale, key.shape[0] * key.shape[1])
     return dev, B, S1, S2, N1, D, w, ks, aq, ak, bt, block_size, max_blocks
 
@@ -179,7 +191,8 @@ def indexer_logits(query: torch.Tensor, key: torch.Tensor, weights: torch.Tensor
                    actual_seq_lengths_query: Optional[torch.Tensor] = None,
                    actual_seq_lengths_key: Optional[torch.Tensor] = None,
                    block_table: Optional[torch.Tensor] = None, layout_query: str = "BSND",
-                   layout_key: str = "BSND", sparse_mode: int = 3) -> torch.Tensor:
+                   layout_key: str = "BSND", sparse_mode: int = 3,
+                   query_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
     """fp32 logits [B, S1, S2] (masked positions -inf), the scores the top-k stage ranks.
 
     With ``layout_query="TND"`` the logits are [T, S2_max], one row per packed
@@ -188,7 +201,7 @@ def indexer_logits(query: torch.Tensor, key: torch.Tensor, weights: torch.Tensor
         _check_common(query, key, weights, layout_query, layout_key, sparse_mode)
         (dev, B, T, T_rows, S1, S2, N1, D, w, ks, cu_q, cu_k, ak, bt, bs,
          mb) = _prepare_tnd(query, key, weights, key_scale, actual_seq_lengths_query, actual_seq_lengths_key,
-                            block_table, layout_key)
+                            block_table, layout_key, query_scale)
         out = torch.full((T_rows, S2), float("-inf"), dtype=torch.float32, device=dev)
         if T_rows == 0 or S2 == 0:
             return out
@@ -201,7 +214,7 @@ def indexer_logits(query: torch.Tensor, key: torch.Tensor, weights: torch.Tensor
         return out
     dev, B, S1, S2, N1, D, w, ks, aq, ak, bt, bs, mb = _prepare(
         query, key, weights, key_scale, actual_seq_lengths_query, actual_seq_lengths_key, block_table,
-        layout_query, layout_key, sparse_mode)
+        layout_query, layout_key, sparse_mode, query_scale)
     out = torch.empty((B, S1, S2), dtype=torch.float32, device=dev)
     lib = _lib.load_library()
     rc = lib.dsa_indexer_logits(_KINDS[query.dtype], _lib.ptr(query), _lib.ptr(key), _lib.ptr(ks), _lib.ptr(w),
@@ -217,7 +230,8 @@ def lightning_indexer(query: torch.Tensor, key: torch.Tensor, weights: torch.Ten
                       block_table: Optional[torch.Tensor] = None, layout_query: str = "BSND",
                       layout_key: str = "BSND", sparse_count: int = 2048, sparse_mode: int = 3,
                       pre_tokens: int = _INT64_MAX, next_tokens: int = _INT64_MAX, return_value: bool = False,
-                      key_scale: Optional[torch.Tensor] = None, **tuning) -> Tuple[torch.Tensor, torch.Tensor]:
+                      key_scale: Optional[torch.Tensor] = None, query_scale: Optional[torch.Tensor] = None,
+                      **tuning) -> Tuple[torch.Tensor, torch.Tensor]:
     """Top-``sparse_count`` key positions per query row: (indices [B, S1, 1, K] int32, values).
 
     Validation follows lightning_indexer.py:1229-1257.  ``layout_query="TND"``
@@ -244,10 +258,10 @@ def lightning_indexer(query: torch.Tensor, key: torch.Tensor, weights: torch.Ten
     if layout_query == "TND":
         return _lightning_indexer_tnd(query, key, weights, key_scale, actual_seq_lengths_query,
                                       actual_seq_lengths_key, block_table, layout_key, sparse_count, sparse_mode,
-                                      return_value)
+                                      return_value, query_scale)
     dev, B, S1, S2, N1, D, w, ks, aq, ak, bt, bs, mb = _prepare(
         query, key, weights, key_scale, actual_seq_lengths_query, actual_seq_lengths_key, block_table,
-        layout_query, layout_key, sparse_mode)
+        layout_query, layout_key, sparse_mode, query_scale)
     idx = torch.empty((B, S1, 1, sparse_count), dtype=torch.int32, device=dev)
     vdt = torch.float32 if query.dtype == torch.float8_e4m3fn else query.dtype
     if B * S1 == 0 or S2 == 0:
@@ -270,11 +284,11 @@ def lightning_indexer(query: torch.Tensor, key: torch.Tensor, weights: torch.Ten
 
 
 def _lightning_indexer_tnd(query, key, weights, key_scale, actual_seq_lengths_query, actual_seq_lengths_key,
-                           block_table, layout_key, sparse_count, sparse_mode, return_value):
+                           block_table, layout_key, sparse_count, sparse_mode, return_value, query_scale=None):
     _check_common(query, key, weights, "TND", layout_key, sparse_mode)
     (dev, B, T, T_rows, S1, S2, N1, D, w, ks, cu_q, cu_k, ak, bt, bs,
      mb) = _prepare_tnd(query, key, weights, key_scale, actual_seq_lengths_query, actual_seq_lengths_key,
-                        block_table, layout_key)
+                        block_table, layout_key, query_scale)
     vdt = torch.float32 if query.dtype == torch.float8_e4m3fn else query.dtype
     if S1 == 0 or S2 == 0:
         idx = torch.full((T, 1, sparse_count), -1, dtype=torch.int32, device=dev)
