@@ -32,6 +32,15 @@ def test_config1_parity(dsa, dev):
     _check(out, lse, *ref.sparse_mla_fwd(q, kv, idx))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prefill_shaped_launch(dsa, dev, dtype):
+    # 768 rows x 16 heads: more workgroups than the decode-shaped (single-phase) loop takes, so
+    # this runs the two-phase software pipeline that the prefill benchmarks use.
+    q, kv, idx = _inputs(1, 768, 4096, 16, 256, seed=21, dtype=dtype)
+    out, lse = dsa.sparse_mla_fwd(q.to(dev), kv.to(dev), idx.to(dev), 1 / math.sqrt(576))
+    _check(out, lse, *ref.sparse_mla_fwd(q, kv, idx))
+
+
 @pytest.mark.parametrize("H", [32, 48, 64, 128, 160, 256])
 def test_head_counts(dsa, dev, H):
     q, kv, idx = _inputs(1, 4, 2048, H, 256, seed=H)
