@@ -410,6 +410,52 @@ def run_v4(torch, pkg, dev, args, flush, H=64, D=512, bs=128, K=512, win=127):
     return res
 
 
+# Published device times of the reference's sparse MLA (SFA) paged decode, TileLang and AscendC on
+# Ascend A3 (examples/sparse_flash_attention/bench_sfa/README.md:31-34), per KV pool size.
+SFA_REFERENCE_US = {2560: (109.760, 98.0), 6400: (109.100, 99.0), 48000: (108.980, 100.0)}
+
+
+def run_sfa_reference_shapes(torch, pkg, dev):
+    """The reference's SFA decode benchmark (bench_sfa.py:9-70, :104-140): T=1, B=1, 128 heads,
+    D=512 + 64 rope (one 576-wide latent row, V = its first 512), 2048 distinct indices drawn from
+    act_kv=2560, 128-row blocks with an identity table, scale 0.5, sparse_mode 0, bf16; the KV
+    pool holds 2560 / 6400 / 48000 rows.  Device time per call from a HIP graph, as the
+    reference's figures are device task durations."""
+    from tilelang_ascend_amd import _lib as L
+    lib = pkg.load_library()
+    g = torch.Generator(device=dev).manual_seed(20261206)
+    H, D, bs, K, act = 128, 576, 128, 2048, 2560
+    res = {"workload": "SFA paged decode of the reference benchmark: T=1, B=1, H=128, D=512+64, topk=2048 of "
+                       "act_kv=2560, block 128, scale 0.5, sparse_mode 0, bf16; device time per call (HIP graph)"}
+    q = (torch.randn((1, 1, H, D), device=dev, generator=g) * 0.5).to(torch.bfloat16)
+    idx = torch.topk(torch.rand((1, act), device=dev, generator=g), K, dim=-1).indices.to(torch.int32)
+    idx = idx.view(1, 1, 1, K).contiguous()
+    kvl = torch.full((1,), act, dtype=torch.int32, device=dev)
+    out = torch.empty((1, 1, H, 512), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((1, 1, H), dtype=torch.float32, device=dev)
+    nws = lib.dsa_sparse_mla_workspace_size(1, 1, H, K)
+    ws = torch.empty((max(nws, 1),), dtype=torch.uint8, device=dev)
+    for kv_s, (ref_tl, ref_ac) in SFA_REFERENCE_US.items():
+        nb = kv_s // bs
+        pool = (torch.randn((nb, bs, 1, D), device=dev, generator=g) * 0.5).to(torch.bfloat16)
+        table = torch.arange(nb, dtype=torch.int32, device=dev).view(1, nb)
+
+        def call():
+            rc = lib.dsa_sparse_mla_fwd(L.KIND_BF16, q.data_ptr(), pool.data_ptr(), idx.data_ptr(), table.data_ptr(),
+                                        None, kvl.data_ptr(), 1, 1, H, D, 512, nb * bs, bs, nb, K, 0.5, 0,
+                                        out.data_ptr(), lse.data_ptr(), ws.data_ptr(), nws, L.stream_handle(dev))
+            L.check(rc, "sfa decode")
+
+        call()
+        torch.cuda.synchronize()
+        t = _timed_graph(torch, call, 20)
+        res[f"kv_s_{kv_s}"] = {"us": round(t * 1e3, 2), "reference_tilelang_us": ref_tl, "reference_ascendc_us": ref_ac,
+                               "speedup_vs_reference": round(ref_tl / (t * 1e3), 2)}
+        _log(f"SFA decode KV_S={kv_s}: {t * 1e3:.1f} us (reference {ref_tl} us)")
+        del pool, table
+    return res
+
+
 def _rocpd(db):
     import sqlite3
 
@@ -504,7 +550,7 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--reps", type=int, default=20, help="repetitions of the secondary (flushed) benchmarks")
-    ap.add_argument("--skip", default="", help="comma list of parts to skip: step,indexer,decode,c5,v4,cpu")
+    ap.add_argument("--skip", default="", help="comma list of parts to skip: step,indexer,decode,c5,v4,sfa,cpu")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy (HBM byte-counter calibration for rocprof)")
     args = ap.parse_args()
@@ -642,6 +688,10 @@ def main():
     # ---------------- V4 sparse flash MLA at the reference benchmark's shapes ----------------
     if "v4" not in skip:
         result["v4_sparse_flash_mla"] = run_v4(torch, pkg, dev, args, flush)
+
+    # ---------------- the reference's own SFA decode benchmark shapes ----------------
+    if "sfa" not in skip:
+        result["sfa_decode_reference_shapes"] = run_sfa_reference_shapes(torch, pkg, dev)
 
     del flush
     if "cpu" not in skip and cpu_inputs is not None:

@@ -975,9 +975,15 @@ __global__ __launch_bounds__(256) void sparse_mla_combine_kernel(const uint16_t*
   if (c == 0) lse[row] = wsum > 0.f ? mx + __logf(wsum) : -__builtin_huge_valf();
 }
 
+// Few rows: split each row's slot list over workgroups until the grid fills
+// the CUs.  A split costs a partial write and a share of the combine, so past
+// 8 tiles a row keeps at least 4 tiles per split (one query row with 2048
+// slots: 64 one-tile splits take 65 us, 16 four-tile splits 36 us); short
+// lists (a V4 window) split down to single tiles.
 int mla_choose_splits(int64_t tokens, int64_t head_groups, int64_t topk) {
   const int64_t wgs = tokens * head_groups;
-  const int max_splits = (int)((topk + kMlaTile - 1) / kMlaTile);
+  const int tiles = (int)((topk + kMlaTile - 1) / kMlaTile);
+  const int max_splits = tiles > 8 ? tiles / 4 : tiles;
   int splits = (int)((topk + kSlotsCap - 1) / kSlotsCap);  // each split's slots must fit in LDS
   while (wgs * splits < 256 && splits * 2 <= max_splits) splits *= 2;
   return splits;
