@@ -319,7 +319,7 @@ def run_c5(torch, pkg, dev, args, flush, ctx=131072, chunk=4096, H=128, topk=204
 
 
 PROFILES = ROOT / "profiles"
-STEP_KERNEL = "dsa::sparse_mla_kernel<4, false>"
+STEP_KERNEL = "dsa::sparse_mla_kernel<4, false, 576>"
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
 
 
