@@ -213,6 +213,21 @@ int dsa_sparse_flash_mla(int kind, const void* q, int64_t T, int64_t H, int64_t 
                          size_t workspace_bytes, void* stream);
 
 /*
+ * V4 gathered-index attention with sinks: `sparse_attn_kernel(h, d, scale)` /
+ * `sparse_attn` (examples/deepseek_v4/sparse_attention.py:28-198).  Query row
+ * (b, m) attends to kv[b, topk_idxs[b, m, j]] (-1 = empty slot; duplicates
+ * count twice, as in the golden), K = V = the 512-wide row, and the sink of
+ * head h adds exp(sinks[h]) to the softmax denominator.
+ *  q [B, M, H, 512]; kv [B, N, 512]; topk_idxs [B, M, topk] int32;
+ *  sinks [H] fp32 or NULL; out [B, M, H, 512] (input dtype); lse [B, M, H] fp32.
+ */
+size_t dsa_sparse_attn_sink_workspace_size(int64_t B, int64_t M, int64_t H, int64_t topk);
+
+int dsa_sparse_attn_sink(int kind, const void* q, const void* kv, const int32_t* topk_idxs, int64_t B, int64_t M,
+                         int64_t H, int64_t N, int64_t D, int64_t topk, const float* sinks, float softmax_scale,
+                         void* out, float* lse, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Per-row activation quantiser, the producer of the indexer's low-precision
  * inputs.  Replaces `act_quant_kernel_int8_optimized` / `act_quant_torch`
  * (examples/deepseek_v4/act_quant.py:33-92, :118-142) and extends it to fp8:

@@ -51,6 +51,13 @@ How each function is pinned (see ``tests/test_oracle.py``):
   stops at the first -1 and skips entries past the threshold), a single-key
   closed form, ``torch.softmax`` / ``torch.logsumexp`` over scores with the
   sink appended, and a vanishing sink reducing to plain softmax attention.
+* ``sparse_attn_sink`` (gathered-index attention with sinks,
+  ``examples/deepseek_v4/sparse_attention.py:171-198``): all slots on one key
+  (closed form kv * K e^s / (K e^s + e^sink)), the sink identity
+  out = out_plain * sigmoid(lse_plain - sink) against the separately pinned
+  ``sparse_mla_fwd``, -1 slots equal to dropping them, a duplicated slot equal
+  to doubling that key's weight, and ``torch.softmax`` over scores with the
+  sink appended.
 * ``tnd_to_padded`` / ``padded_to_tnd`` (packed TND layout,
   ``examples/deepseek_v4/lightning_indexer.py:48-190``): a hand-worked row map
   with an empty batch, round trips both ways, and the zero fill of padding.
@@ -551,6 +558,54 @@ def sparse_flash_mla(
             p = e[:, :score.shape[1]] / denom
             out[t] = p @ kmat
             lse[t] = (m + torch.log(denom)).squeeze(1)
+    return out.to(torch.float32), lse.to(torch.float32)
+
+
+def sparse_attn_sink(
+    q: torch.Tensor,
+    kv: torch.Tensor,
+    attn_sink: Optional[torch.Tensor],
+    topk_idxs: torch.Tensor,
+    softmax_scale: float,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """V4 gathered-index attention with sinks: (out fp32 [b, m, h, d], lse fp32 [b, m, h]).
+
+    Restates ``examples/deepseek_v4/sparse_attention.py:171-198``: q [b, m, h, d],
+    kv [b, n, d] (K = V), topk_idxs [b, m, topk].  Slot j of row (b, t) holds
+    kv[b, idx] when idx != -1 (:171-177; duplicates count once per slot) and is
+    masked to -inf otherwise (:195); scores are scale * q.k; the sink of head h is
+    one more logit with no value row (:180-188): p = exp(s - M) / (sum exp(s - M)
+    + exp(sink - M)) with M the max over the slots; out = p V (:198).  lse = natural
+    log of the full denominator (sink included), in the convention of
+    ``sparse_flash_mla_golden.py:149`` (the reference kernel writes no LSE).
+
+    Out-of-contract rows, defined here the way the HIP kernel handles them: an
+    index outside [0, n) is masked like -1 (the reference would read out of
+    bounds), and a row with no valid slot gives out = 0, lse = sink (the
+    reference's golden is NaN there: exp(-inf - -inf)).  Exact, in float64.
+    """
+    B, M, H, D = q.shape
+    out = torch.zeros((B, M, H, D), dtype=torch.float64)
+    lse = torch.zeros((B, M, H), dtype=torch.float64)
+    n = kv.shape[1]
+    sk = None if attn_sink is None else attn_sink.to(torch.float64).reshape(H, 1)
+    idx_all = topk_idxs.to(torch.int64).cpu()
+    kvd = kv.to(torch.float64)
+    for b in range(B):
+        for t in range(M):
+            row = idx_all[b, t]
+            sel = row[(row >= 0) & (row < n)]
+            kmat = kvd[b, sel]                                          # [nv, d]
+            score = (q[b, t].to(torch.float64) @ kmat.T) * softmax_scale  # [H, nv]
+            logits = score if sk is None else torch.cat([score, sk], dim=1)
+            if logits.shape[1] == 0:
+                lse[b, t] = float("-inf")
+                continue
+            mx = logits.amax(dim=1, keepdim=True)
+            e = torch.exp(logits - mx)
+            denom = e.sum(dim=1, keepdim=True)
+            out[b, t] = (e[:, :score.shape[1]] / denom) @ kmat
+            lse[b, t] = (mx + torch.log(denom)).squeeze(1)
     return out.to(torch.float32), lse.to(torch.float32)
 
 

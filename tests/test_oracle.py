@@ -354,6 +354,68 @@ def test_v4_golden_mode_matches_exact_without_rounding():
     assert 0 < d < 2e-2
 
 
+# ----------------------------------------------------- V4 sparse_attn with sinks
+def test_sparse_attn_sink_one_key_closed_form():
+    # Every slot on one key j: p is uniform over the K slots, so
+    # out = kv[j] * K e^s / (K e^s + e^sink) and lse = log(K e^s + e^sink).
+    g = torch.Generator().manual_seed(21)
+    H, D, n, K = 3, 8, 5, 6
+    q = torch.randn(1, 1, H, D, generator=g, dtype=torch.float64).float()
+    kv = torch.randn(1, n, D, generator=g, dtype=torch.float64).float()
+    sink = torch.tensor([0.3, -2.0, 1.5])
+    idx = torch.full((1, 1, K), 2, dtype=torch.int32)
+    out, lse = ref.sparse_attn_sink(q, kv, sink, idx, 0.4)
+    s = (q[0, 0].double() @ kv[0, 2].double()) * 0.4
+    z = K * torch.exp(s) + torch.exp(sink.double())
+    w = K * torch.exp(s) / z
+    assert torch.allclose(out[0, 0].double(), w.view(H, 1) * kv[0, 2].double(), rtol=1e-6, atol=1e-7)
+    assert torch.allclose(lse[0, 0].double(), torch.log(z), rtol=1e-6)
+
+
+def test_sparse_attn_sink_identity_against_plain_mla():
+    # With a sink, out = out_plain * sigmoid(lse_plain - sink) and
+    # lse = logaddexp(lse_plain, sink), where (out_plain, lse_plain) is the
+    # separately pinned sparse_mla_fwd over the same unique slots (no causal mask).
+    g = torch.Generator().manual_seed(22)
+    B, M, H, D, n, K = 2, 3, 4, 16, 30, 10
+    q = torch.randn(B, M, H, D, generator=g)
+    kv = torch.randn(B, n, D, generator=g)
+    sink = torch.randn(H, generator=g)
+    idx = torch.stack([torch.randperm(n, generator=g)[:K] for _ in range(B * M)]).view(B, M, K).int()
+    out, lse = ref.sparse_attn_sink(q, kv, sink, idx, 0.3)
+    op, lp = ref.sparse_mla_fwd(q, kv.view(B, n, 1, D), idx.view(B, M, 1, K), 0.3, d_v=D, is_causal=False)
+    f = torch.sigmoid(lp.double() - sink.double().view(1, 1, H)).unsqueeze(-1)
+    assert torch.allclose(out.double(), op.double() * f, rtol=1e-5, atol=1e-6)
+    assert torch.allclose(lse.double(), torch.logaddexp(lp.double(), sink.double().view(1, 1, H)), rtol=1e-6)
+    # No sink: exactly the plain attention.
+    o0, l0 = ref.sparse_attn_sink(q, kv, None, idx, 0.3)
+    assert torch.allclose(o0, op, rtol=1e-5, atol=1e-6) and torch.allclose(l0, lp, rtol=1e-6)
+
+
+def test_sparse_attn_sink_masked_and_duplicate_slots():
+    g = torch.Generator().manual_seed(23)
+    H, D, n = 2, 8, 12
+    q = torch.randn(1, 1, H, D, generator=g)
+    kv = torch.randn(1, n, D, generator=g)
+    sink = torch.randn(H, generator=g)
+    a = torch.tensor([[[3, -1, 7, -1, 0]]], dtype=torch.int32)
+    b = torch.tensor([[[3, 7, 0]]], dtype=torch.int32)
+    oa, la = ref.sparse_attn_sink(q, kv, sink, a, 0.5)
+    ob, lb = ref.sparse_attn_sink(q, kv, sink, b, 0.5)
+    assert torch.equal(oa, ob) and torch.equal(la, lb)           # -1 slots drop out
+    # A key listed twice weighs twice: brute force with torch.softmax, sink appended.
+    d = torch.tensor([[[3, 3, 7]]], dtype=torch.int32)
+    od, ld = ref.sparse_attn_sink(q, kv, sink, d, 0.5)
+    keys = kv[0, [3, 3, 7]].double()
+    full = torch.cat([(q[0, 0].double() @ keys.T) * 0.5, sink.double().view(H, 1)], dim=1)
+    p = torch.softmax(full, dim=1)[:, :-1]
+    assert torch.allclose(od[0, 0].double(), p @ keys, rtol=1e-6, atol=1e-7)
+    assert torch.allclose(ld[0, 0].double(), torch.logsumexp(full, dim=1), rtol=1e-6)
+    # No valid slot: out 0, lse = sink.
+    oe, le = ref.sparse_attn_sink(q, kv, sink, torch.full((1, 1, 4), -1, dtype=torch.int32), 0.5)
+    assert torch.count_nonzero(oe) == 0 and torch.allclose(le[0, 0], sink)
+
+
 def test_act_quant_int8_hand_worked():
     # amax 127 -> scale exactly 1: half-way values go to the even integer.
     x = torch.tensor([[127.0, 63.5, 62.5, -0.5, 0.5, 1.5, -2.5, -127.0]])

@@ -1,0 +1,154 @@
+"""GPU parity of the gathered-index V4 attention with sinks (``sparse_attn``) and of the
+SFA decode entry ``sparse_attn_tilelang`` against the CPU oracle.
+
+``sparse_attn`` (examples/deepseek_v4/sparse_attention.py:171-241): the reference
+test's own shape (b=1, m=256, n=256, h=64, d=512, topk=128, indices from randint, so
+duplicates occur, bf16 randn inputs, fp32 sinks) at its own tolerance, atol = rtol =
+1e-2, plus -1 slots, batches, 128 heads, fp16 and the split path (long index lists
+on few rows).  LSE within 1e-3 of the exact oracle.
+
+``sparse_attn_tilelang`` (examples/sparse_flash_attention/bench_sfa/bench_sfa.py:10-120):
+the benchmark's inputs (T=1, 128 heads, 512 + 64 rope, paged KV in 128-row blocks,
+topk 2048 drawn by topk of uniform noise over act_kv_s = 2560, scale 0.5, values of
+std 0.5), out within atol = rtol = 2e-2 of the exact oracle (the benchmark itself
+compares two kernels at 1e-2).
+"""
+import pytest
+import torch
+
+from oracle import dsa_oracle as ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(b, m, n, h, d, topk, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn((b, m, h, d), generator=g).to(dtype)
+    kv = torch.randn((b, n, d), generator=g).to(dtype)
+    sink = torch.randn((h,), generator=g)
+    idx = torch.randint(0, n, (b, m, topk), generator=g, dtype=torch.int32)
+    return q, kv, sink, idx
+
+
+def _run(dsa, dev, q, kv, sink, idx, scale):
+    out = dsa.sparse_attn(q.to(dev), kv.to(dev), None if sink is None else sink.to(dev), idx.to(dev), scale)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+def _lse(dsa, dev, q, kv, sink, idx, scale):
+    """The LSE the kernel writes, read through the C ABI."""
+    b, m, h, d = q.shape
+    lib = dsa.load_library()
+    qd, kvd, idxd = q.to(dev), kv.to(dev), idx.to(dev)
+    sk = None if sink is None else sink.to(dev)
+    out = torch.empty((b, m, h, d), dtype=q.dtype, device=dev)
+    lse = torch.empty((b, m, h), dtype=torch.float32, device=dev)
+    nbytes = lib.dsa_sparse_attn_sink_workspace_size(b, m, h, idx.shape[2])
+    ws = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=dev)
+    kind = 1 if q.dtype == torch.bfloat16 else 2
+    rc = lib.dsa_sparse_attn_sink(kind, qd.data_ptr(), kvd.data_ptr(), idxd.data_ptr(), b, m, h, kv.shape[1], d,
+                                  idx.shape[2], None if sk is None else sk.data_ptr(), scale, out.data_ptr(),
+                                  lse.data_ptr(), ws.data_ptr(), nbytes, torch.cuda.current_stream(dev).cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    return lse.cpu()
+
+
+def test_reference_test_shape(dsa, dev):
+    """sparse_attention.py:216-241: shape 1, bf16, scale 512**-0.5, tolerance 1e-2."""
+    print("sparse_attn reference shape b=1 m=256 n=256 h=64 topk=128", flush=True)
+    q, kv, sink, idx = _inputs(1, 256, 256, 64, 512, 128, torch.bfloat16, 41)
+    scale = 512 ** -0.5
+    out = _run(dsa, dev, q, kv, sink, idx, scale)
+    want, want_lse = ref.sparse_attn_sink(q, kv, sink, idx, scale)
+    assert out.dtype == torch.float32 and out.shape == (1, 256, 64, 512)
+    torch.testing.assert_close(out, want, rtol=1e-2, atol=1e-2)
+    torch.testing.assert_close(_lse(dsa, dev, q, kv, sink, idx, scale), want_lse, rtol=1e-3, atol=1e-3)
+
+
+def test_reference_small_shape_via_builder(dsa, dev):
+    """Shape 2 of the reference test (b=1, m=6, n=6, h=16, topk=6) through the builder."""
+    q, kv, sink, idx = _inputs(1, 6, 6, 16, 512, 6, torch.bfloat16, 42)
+    kernel = dsa.sparse_attn_kernel(h=16, d=512, scale=512 ** -0.5)
+    out = kernel(q.to(dev), kv.to(dev), sink.to(dev), idx.to(dev)).cpu()
+    want, _ = ref.sparse_attn_sink(q, kv, sink, idx, 512 ** -0.5)
+    torch.testing.assert_close(out, want, rtol=1e-2, atol=1e-2)
+    # Default scale is 1/sqrt(d), as in the reference builder.
+    out2 = dsa.sparse_attn_kernel(h=16, d=512)(q.to(dev), kv.to(dev), sink.to(dev), idx.to(dev)).cpu()
+    torch.testing.assert_close(out2, out, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_masked_slots_batches_and_heads(dsa, dev, dtype):
+    """-1 slots (masked), out-of-range slots (masked), two batches (row bases b*n), 128 heads."""
+    print(f"sparse_attn masked b=2 h=128 {dtype}", flush=True)
+    q, kv, sink, idx = _inputs(2, 40, 300, 128, 512, 200, dtype, 43)
+    g = torch.Generator().manual_seed(44)
+    drop = torch.rand(idx.shape, generator=g) < 0.3
+    idx = torch.where(drop, torch.full_like(idx, -1), idx)
+    idx[0, 0, :] = -1                      # no valid slot: out 0, lse = sink
+    idx[1, 1, 5] = 300                     # past n: masked
+    scale = 0.05
+    out = _run(dsa, dev, q, kv, sink, idx, scale)
+    want, want_lse = ref.sparse_attn_sink(q, kv, sink, idx, scale)
+    torch.testing.assert_close(out, want, rtol=1e-2, atol=1e-2)
+    torch.testing.assert_close(_lse(dsa, dev, q, kv, sink, idx, scale), want_lse, rtol=1e-3, atol=1e-3)
+    assert torch.count_nonzero(out[0, 0]) == 0
+
+
+def test_split_path_and_no_sink(dsa, dev):
+    """Few rows with long index lists take the split + combine path (sinks join in the combine)."""
+    print("sparse_attn split path b=2 m=1 topk=4096", flush=True)
+    q, kv, sink, idx = _inputs(2, 1, 5000, 64, 512, 4096, torch.bfloat16, 45)
+    scale = 512 ** -0.5
+    for sk in (sink, None):
+        out = _run(dsa, dev, q, kv, sk, idx, scale)
+        want, want_lse = ref.sparse_attn_sink(q, kv, sk, idx, scale)
+        torch.testing.assert_close(out, want, rtol=1e-2, atol=1e-2)
+        torch.testing.assert_close(_lse(dsa, dev, q, kv, sk, idx, scale), want_lse, rtol=1e-3, atol=1e-3)
+
+
+def test_rejects_bad_shapes(dsa, dev):
+    q, kv, sink, idx = _inputs(1, 2, 8, 16, 512, 4, torch.bfloat16, 46)
+    with pytest.raises(ValueError):
+        dsa.sparse_attn(q[..., :256].contiguous().to(dev), kv[..., :256].contiguous().to(dev), sink.to(dev),
+                        idx.to(dev), 0.1)
+    with pytest.raises(ValueError):
+        dsa.sparse_attn(q.to(dev), kv.to(dev), sink[:8].to(dev), idx.to(dev), 0.1)
+    with pytest.raises(ValueError):
+        dsa.sparse_attn_kernel(h=16, d=256)
+
+
+# ------------------------------------------------------------- sparse_attn_tilelang
+def _bench_sfa_inputs(T, KV_S, act_kv_s, Q_N, topk, block_size, seed):
+    """bench_sfa.py:19-45 with a CPU generator."""
+    g = torch.Generator().manual_seed(seed)
+    nb = KV_S // block_size
+    query = (torch.randn((T, Q_N, 512), generator=g) * 0.5).to(torch.bfloat16)
+    key = (torch.randn((nb, block_size, 1, 512), generator=g) * 0.5).to(torch.bfloat16)
+    query_rope = (torch.randn((T, Q_N, 64), generator=g) * 0.5).to(torch.bfloat16)
+    key_rope = (torch.randn((nb, block_size, 1, 64), generator=g) * 0.5).to(torch.bfloat16)
+    _, ind = torch.topk(torch.rand((T, 1, act_kv_s), generator=g), topk, dim=-1)
+    block_table = torch.arange(nb, dtype=torch.int32).view(1, nb)
+    return query, key, query_rope, key_rope, ind.to(torch.int32), block_table
+
+
+@pytest.mark.parametrize("KV_S,T,sparse_mode", [(2560, 1, 0), (6400, 1, 0), (6400, 4, 3)])
+def test_sparse_attn_tilelang_bench_sfa(dsa, dev, KV_S, T, sparse_mode):
+    print(f"sparse_attn_tilelang KV_S={KV_S} T={T} mode={sparse_mode}", flush=True)
+    act_kv_s, block_size = 2560, 128
+    query, key, qr, kr, ind, bt = _bench_sfa_inputs(T, KV_S, act_kv_s, 128, 2048, block_size, 47 + KV_S + T)
+    aq = torch.tensor([T], dtype=torch.int32)
+    akv = torch.tensor([act_kv_s], dtype=torch.int32)
+    out = dsa.sparse_attn_tilelang(query.to(dev), key.to(dev), key.to(dev), ind.to(dev), 0.5, 1, aq.to(dev),
+                                   akv.to(dev), query_rope=qr.to(dev), key_rope=kr.to(dev), layout_query="TND",
+                                   layout_kv="PA_BSND", sparse_mode=sparse_mode, block_table=bt.to(dev),
+                                   attention_mode=2)
+    torch.cuda.synchronize()
+    assert out.shape == (T, 128, 512) and out.dtype == torch.bfloat16
+    q = torch.cat((query, qr), dim=-1).unsqueeze(0)
+    kv = torch.cat((key, kr), dim=-1)
+    want, _ = ref.sparse_mla_fwd(q, kv, ind.view(1, T, 1, -1), 0.5, block_table=bt, actual_seq_lengths_query=[T],
+                                 actual_seq_lengths_kv=[act_kv_s], is_causal=sparse_mode == 3)
+    torch.testing.assert_close(out.cpu().float(), want[0], rtol=2e-2, atol=2e-2)

@@ -53,6 +53,9 @@ SIGNATURES = {
                                       _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp,
                                       _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_float, _c_vp, _c_vp, _c_vp, _c_size,
                                       _c_vp]),
+    "dsa_sparse_attn_sink_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "dsa_sparse_attn_sink": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                      _c_vp, _c_float, _c_vp, _c_vp, _c_vp, _c_size, _c_vp]),
     "dsa_act_quant": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_int, _c_vp, _c_vp, _c_int, _c_vp]),
     "dsa_sparse_mla_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64]),
     "dsa_sparse_mla_fwd": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64,

@@ -20,6 +20,10 @@ hipError_t launch_sparse_mla(int is_fp16, const void* q, const void* kv, const i
                              int causal, void* out, float* lse, void* workspace, hipStream_t stream);
 size_t mla_workspace_bytes(int64_t tokens, int64_t H, int64_t topk);
 size_t v4_workspace_bytes(int64_t T, int64_t H, int64_t cap);
+size_t sparse_attn_sink_workspace_bytes(int64_t T, int64_t H, int64_t K);
+hipError_t launch_sparse_attn_sink(int is_fp16, const void* q, const void* kv, const int32_t* idx, int64_t B,
+                                   int64_t M, int64_t H, int64_t N, int64_t K, const float* sinks, float sm_scale,
+                                   void* out, float* lse, void* workspace, hipStream_t stream);
 hipError_t launch_act_quant(int in_kind, const void* x, int64_t rows, int64_t n, int out_kind, void* y,
                             float* scales, int round_scale, hipStream_t stream);
 hipError_t launch_sparse_flash_mla(int is_fp16, const void* q, int64_t T, int64_t H, int64_t B,
@@ -307,6 +311,27 @@ int dsa_act_quant(int in_kind, const void* x, int64_t rows, int64_t n, int out_k
   if (rows * n > 0 && (!x || !y || !scales)) return reject("act_quant: null pointer");
   return ok(dsa::launch_act_quant(in_kind, x, rows, n, out_kind, y, scales, round_scale ? 1 : 0,
                                   static_cast<hipStream_t>(stream)));
+}
+
+size_t dsa_sparse_attn_sink_workspace_size(int64_t B, int64_t M, int64_t H, int64_t topk) {
+  if (B <= 0 || M <= 0 || H <= 0 || topk <= 0) return 0;
+  return dsa::sparse_attn_sink_workspace_bytes(B * M, H, topk);
+}
+
+int dsa_sparse_attn_sink(int kind, const void* q, const void* kv, const int32_t* topk_idxs, int64_t B, int64_t M,
+                         int64_t H, int64_t N, int64_t D, int64_t topk, const float* sinks, float softmax_scale,
+                         void* out, float* lse, void* workspace, size_t workspace_bytes, void* stream) {
+  if (kind != DSA_KIND_BF16 && kind != DSA_KIND_FP16) return reject("sparse_attn: kind must be bf16 or fp16");
+  if (D != 512) return reject("sparse_attn: D must be 512");
+  if (H < 16 || H % 16 != 0 || H > 1024) return reject("sparse_attn: H must be a multiple of 16 in [16, 1024]");
+  if (B < 0 || M < 0 || N < 0 || topk < 1 || B * N >= dsa_kSrc2Limit || (topk + 1) * B * M > kMaxInt)
+    return reject("sparse_attn: bad sizes");
+  if (B * M > 0 && (!q || !kv || !topk_idxs || !out || !lse)) return reject("sparse_attn: null pointer");
+  const size_t need = dsa_sparse_attn_sink_workspace_size(B, M, H, topk);
+  if (workspace_bytes < need) return reject("sparse_attn: workspace too small");
+  if (need > 0 && !workspace) return reject("sparse_attn: null workspace");
+  return ok(dsa::launch_sparse_attn_sink(kind == DSA_KIND_FP16, q, kv, topk_idxs, B, M, H, N, topk, sinks,
+                                         softmax_scale, out, lse, workspace, static_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

@@ -114,6 +114,23 @@ __global__ __launch_bounds__(256) void v4_row_lists_kernel(V4Args a) {
   if (lane == 0) a.count[t] = n;
 }
 
+// Gathered-index lists of V4's sparse_attn (examples/deepseek_v4/sparse_attention.py:171-198):
+// query row t (batch t / M) attends to kv rows b * N + idx[t][j]; -1 (or an index outside
+// [0, N)) is an empty slot.  One wave per row.
+__global__ __launch_bounds__(256) void index_row_lists_kernel(const int32_t* __restrict__ idx, int T, int M, int N,
+                                                             int K, int32_t* __restrict__ rows,
+                                                             int32_t* __restrict__ count) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int t = blockIdx.x * (256 / kWave) + (int)(threadIdx.x / kWave);
+  if (t >= T) return;
+  const int64_t base = (int64_t)(t / M) * N;
+  for (int j = lane; j < K; j += kWave) {
+    const int id = idx[(int64_t)t * K + j];
+    rows[(int64_t)t * K + j] = (id >= 0 && id < N) ? (int32_t)(base + id) : -1;
+  }
+  if (lane == 0) count[t] = K;
+}
+
 static size_t v4_lists_bytes(int64_t T, int64_t cap) {
   return ((size_t)T * (cap + 1) * sizeof(int32_t) + 255) & ~size_t(255);
 }
@@ -162,6 +179,26 @@ hipError_t launch_sparse_flash_mla(int is_fp16, const void* q, int64_t T, int64_
   void* mla_ws = static_cast<uint8_t*>(workspace) + v4_lists_bytes(T, cap);
   return launch_sparse_mla_rows(is_fp16, q, ori_kv, cmp_kv, a.rows, a.count, T, H, cap, sinks, sm_scale, out, lse,
                                 mla_ws, stream);
+}
+
+size_t sparse_attn_sink_workspace_bytes(int64_t T, int64_t H, int64_t K) { return v4_workspace_bytes(T, H, K); }
+
+// Caller validated: D = 512, H % 16 == 0, B * N < 2^30, T = B * M < 2^31 / (K + 1).
+hipError_t launch_sparse_attn_sink(int is_fp16, const void* q, const void* kv, const int32_t* idx, int64_t B,
+                                   int64_t M, int64_t H, int64_t N, int64_t K, const float* sinks, float sm_scale,
+                                   void* out, float* lse, void* workspace, hipStream_t stream) {
+  const int64_t T = B * M;
+  if (T == 0 || H == 0) return hipSuccess;
+  int32_t* count = static_cast<int32_t*>(workspace);
+  int32_t* rows = count + T;
+  const int per_block = 256 / kWave;
+  hipLaunchKernelGGL(index_row_lists_kernel, dim3((unsigned)((T + per_block - 1) / per_block)), dim3(256), 0, stream,
+                     idx, (int)T, (int)M, (int)N, (int)K, rows, count);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  void* mla_ws = static_cast<uint8_t*>(workspace) + v4_lists_bytes(T, K);
+  return launch_sparse_mla_rows(is_fp16, q, kv, nullptr, rows, count, T, H, K, sinks, sm_scale, out, lse, mla_ws,
+                                stream);
 }
 
 }  // namespace dsa

@@ -172,3 +172,58 @@ def sparse_flash_mla(
     if return_softmax_lse:
         return out, lse
     return out
+
+
+def sparse_attn(query_states: torch.Tensor, kv_states: torch.Tensor, attn_sink: torch.Tensor,
+                topk_idxs: torch.Tensor, softmax_scale: float) -> torch.Tensor:
+    """V4 gathered-index attention with sinks (examples/deepseek_v4/sparse_attention.py:171-198):
+    q [b, m, h, 512], kv [b, n, 512], attn_sink [h] fp32, topk_idxs [b, m, topk] int32 (-1 =
+    empty slot; duplicates count twice) -> fp32 [b, m, h, 512], as the reference kernel writes it."""
+    if query_states.dtype not in _KINDS or kv_states.dtype != query_states.dtype:
+        raise ValueError("query_states / kv_states must share a bfloat16 or float16 dtype")
+    dev = _lib.require_device(query_states)
+    if query_states.dim() != 4 or query_states.shape[-1] != D:
+        raise ValueError(f"query_states must be [b, m, h, {D}], got {tuple(query_states.shape)}")
+    b, m, h, _ = query_states.shape
+    if kv_states.dim() != 3 or kv_states.shape[0] != b or kv_states.shape[2] != D:
+        raise ValueError(f"kv_states must be [b, n, {D}], got {tuple(kv_states.shape)}")
+    if h % 16 != 0 or h > 1024:
+        raise ValueError(f"heads must be a multiple of 16 (<= 1024), got {h}")
+    n = kv_states.shape[1]
+    idx = topk_idxs.to(device=dev, dtype=torch.int32).contiguous()
+    if idx.dim() != 3 or tuple(idx.shape[:2]) != (b, m):
+        raise ValueError(f"topk_idxs must be [b, m, topk], got {tuple(topk_idxs.shape)}")
+    topk = idx.shape[2]
+    for name, t in (("query_states", query_states), ("kv_states", kv_states)):
+        _lib.require_contiguous(name, t)
+    kv = kv_states.to(dev)
+    sk = None if attn_sink is None else attn_sink.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+    if sk is not None and sk.numel() != h:
+        raise ValueError(f"attn_sink must hold one value per head ({h}), got {sk.numel()}")
+    out = torch.empty((b, m, h, D), dtype=query_states.dtype, device=dev)
+    lse = torch.empty((b, m, h), dtype=torch.float32, device=dev)
+    if b * m > 0:
+        lib = _lib.load_library()
+        ws_bytes = lib.dsa_sparse_attn_sink_workspace_size(b, m, h, topk)
+        ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+        rc = lib.dsa_sparse_attn_sink(_KINDS[query_states.dtype], _lib.ptr(query_states), _lib.ptr(kv),
+                                      _lib.ptr(idx), b, m, h, n, D, topk, _lib.ptr(sk), float(softmax_scale),
+                                      _lib.ptr(out), _lib.ptr(lse), _lib.ptr(ws), ws_bytes, _lib.stream_handle(dev))
+        _lib.check(rc, "dsa_sparse_attn_sink")
+    return out.float()
+
+
+def sparse_attn_kernel(h: int, d: int, scale: Optional[float] = None):
+    """Builder with the signature of sparse_attention.py:28 (``sparse_attn_kernel(h, d, scale)``):
+    returns ``kernel(q, kv, attn_sink, topk_idxs) -> fp32 [b, m, h, d]``; scale defaults to
+    1/sqrt(d) as there."""
+    if d != D:
+        raise ValueError(f"d must be {D}, got {d}")
+    sc = (1.0 / d) ** 0.5 if scale is None else scale
+
+    def kernel(q: torch.Tensor, kv: torch.Tensor, attn_sink: torch.Tensor, topk_idxs: torch.Tensor) -> torch.Tensor:
+        if q.shape[2] != h:
+            raise ValueError(f"q must have {h} heads, got {q.shape[2]}")
+        return sparse_attn(q, kv, attn_sink, topk_idxs, sc)
+
+    return kernel

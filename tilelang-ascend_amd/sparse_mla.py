@@ -137,3 +137,27 @@ def sparse_attention_fwd(heads: int, dim: int, tail_dim: int, topk: int, kv_stri
         return out
 
     return kernel
+
+
+def sparse_attn_tilelang(query, key, value, sparse_indices, scale_value, sparse_block_size,
+                         actual_seq_lengths_query, actual_seq_lengths_kv, query_rope=None, key_rope=None,
+                         layout_query="BSND", layout_kv="BSND", sparse_mode=3, block_table=None,
+                         attention_mode=None):
+    """The reference's torch_npu-style decode entry
+    (examples/sparse_flash_attention/bench_sfa/sparse_flash_attn_pa_no_cv_pipeline.py:384-419):
+    query [T, N, 512] with query_rope [T, N, 64]; key [blocks, block_size, 1, 512] with key_rope
+    [blocks, block_size, 1, 64] (value is the key, as there); sparse_indices [T, 1, topk]; a paged
+    cache through block_table.  Like the reference it joins each query / key with its rope part and
+    runs the 576-wide kernel (causal when sparse_mode is 3); returns out [T, N, 512]."""
+    del value, sparse_block_size, layout_query, layout_kv, attention_mode
+    if query_rope is None or key_rope is None:
+        raise ValueError("query_rope and key_rope are required (D = 512 + 64)")
+    q = torch.cat((query.unsqueeze(0), query_rope.unsqueeze(0)), dim=-1).contiguous()
+    kv = torch.cat((key, key_rope), dim=-1).contiguous()
+    T = q.shape[1]
+    idx = sparse_indices.to(torch.int32).reshape(1, T, 1, -1).contiguous()
+    out, _ = sparse_mla_fwd(q, kv, idx, float(scale_value), block_table=block_table,
+                            actual_seq_lengths_query=actual_seq_lengths_query,
+                            actual_seq_lengths_kv=actual_seq_lengths_kv, is_causal=sparse_mode == 3)
+    return out.squeeze(0)
+
