@@ -244,13 +244,29 @@ def run_c5(torch, pkg, dev, args, flush, ctx=131072, chunk=4096, H=128, topk=204
                                        chunk, H, 576, 512, ctx, 0, 0, topk, sm, 1, out.data_ptr(), lse.data_ptr(),
                                        ws.data_ptr(), ws_b, stream), "c5 mla")
 
-    for f in (run_idx, run_topk, run_mla):
+    fidx = torch.empty(1, chunk, 1, topk, dtype=torch.int32, device=dev)
+    fws_b = lib.dsa_lightning_indexer_fused_workspace_size(1, chunk, ctx, topk)
+    fws = torch.empty(fws_b, dtype=torch.uint8, device=dev)
+    fcnt = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def run_fused():
+        L.check(lib.dsa_lightning_indexer_fused(L.KIND_FP8_E4M3, qi.data_ptr(), ki.data_ptr(), ks.data_ptr(),
+                                                wi.data_ptr(), 1, chunk, ctx, Hi, D, None, None, None, 0, 0, 3, topk,
+                                                fidx.data_ptr(), None, fws.data_ptr(), fws_b, stream), "c5 fused")
+
+    for f in (run_idx, run_topk, run_mla, run_fused):
         f()
+    L.check(lib.dsa_lightning_indexer_fused_fallback_rows(fws.data_ptr(), 1, chunk, ctx, topk, fcnt.data_ptr(),
+                                                          stream), "c5 fallback rows")
     torch.cuda.synchronize()
+    fused_same = bool(torch.equal(fidx, idx))
+    fused_fallback = int(fcnt.item())
     reps = max(3, args.reps // 2)
     t_idx = _median(_timed(torch, run_idx, reps, flush))
     t_topk = _median(_timed(torch, run_topk, reps, flush))
     t_mla = _median(_timed(torch, run_mla, reps, flush))
+    t_fused = _median(_timed(torch, run_fused, reps, flush))
+    del fws
     pairs = sum(min(ctx, ctx - chunk + t + 1) for t in range(chunk))
     idx_flops = 2.0 * Hi * D * chunk * ctx
     mla_flops = 2.0 * H * topk * (576 + 512) * chunk
@@ -298,7 +314,8 @@ def run_c5(torch, pkg, dev, args, flush, ctx=131072, chunk=4096, H=128, topk=204
     torch.cuda.synchronize()
     t_dec = _median(_timed(torch, run_decode, reps, flush))
     dec_bytes = dec_b * (ctx * (D + 4) + topk * 576 * 2 + H * 576 * 2 + H * 512 * 2) + dec_b * ctx * 4 * 2
-    _log(f"C5: indexer {t_idx * 1e3:.1f} us, topk {t_topk * 1e3:.1f} us, mla {t_mla * 1e3:.1f} us, "
+    _log(f"C5: indexer {t_idx * 1e3:.1f} us, topk {t_topk * 1e3:.1f} us, fused {t_fused * 1e3:.1f} us "
+         f"(same: {fused_same}, fallback rows {fused_fallback}), mla {t_mla * 1e3:.1f} us, "
          f"decode chain {t_dec * 1e3:.1f} us")
     del qd, kd, kds, wd, table, dlog, didx, qm, pool, dout, dlse, dws, dtws
     return {
@@ -306,11 +323,16 @@ def run_c5(torch, pkg, dev, args, flush, ctx=131072, chunk=4096, H=128, topk=204
                     "MLA H=128 on that selection), plus a decode step of 32 sequences x 128K keys",
         "indexer_us": round(t_idx * 1e3, 1),
         "topk_us": round(t_topk * 1e3, 1),
-        "indexer_topk_us": round((t_idx + t_topk) * 1e3, 1),
+        "dense_indexer_topk_us": round((t_idx + t_topk) * 1e3, 1),
+        "indexer_topk_us": round(t_fused * 1e3, 1),
+        "indexer_topk_path": "fused (lightning_indexer streams the top-k for rows over 32768 keys)",
         "indexer_topk_roofline_us": round(roof_us, 1),
-        "indexer_topk_frac_roofline": round(roof_us / ((t_idx + t_topk) * 1e3), 4),
+        "indexer_topk_frac_roofline": round(roof_us / (t_fused * 1e3), 4),
+        "dense_frac_roofline": round(roof_us / ((t_idx + t_topk) * 1e3), 4),
         "indexer_tflops_dense": round(idx_flops / (t_idx * 1e-3) / 1e12, 1),
         "indexer_causal_pair_frac": round(pairs / (chunk * ctx), 4),
+        "fused_equals_dense": fused_same,
+        "fused_fallback_rows": fused_fallback,
         "mla_us": round(t_mla * 1e3, 1),
         "mla_tflops": round(mla_flops / (t_mla * 1e-3) / 1e12, 1),
         "decode_chain_us": round(t_dec * 1e3, 1),
@@ -612,12 +634,28 @@ def main():
             run_logits()
             run_topk()
 
-        for f in (run_logits, run_topk, run_both):
+        fidx = torch.empty(S1, K, dtype=torch.int32, device=dev)
+        fws_b = lib.dsa_lightning_indexer_fused_workspace_size(1, S1, S2, K)
+        fws = torch.empty(fws_b, dtype=torch.uint8, device=dev)
+        fcnt = torch.zeros(1, dtype=torch.int32, device=dev)
+
+        def run_fused():
+            rc = lib.dsa_lightning_indexer_fused(L.KIND_FP8_E4M3, qi.data_ptr(), ki.data_ptr(), ksi.data_ptr(),
+                                                 wi.data_ptr(), 1, S1, S2, Hi, 128, None, None, None, 0, 0, 3, K,
+                                                 fidx.data_ptr(), None, fws.data_ptr(), fws_b, stream)
+            L.check(rc, "fused indexer")
+
+        for f in (run_logits, run_topk, run_both, run_fused):
             f()
+        L.check(lib.dsa_lightning_indexer_fused_fallback_rows(fws.data_ptr(), 1, S1, S2, K, fcnt.data_ptr(), stream),
+                "fallback rows")
         torch.cuda.synchronize()
+        fused_same = bool(torch.equal(fidx, out_idx))
+        fused_fallback = int(fcnt.item())
         t_log = _median(_timed(torch, run_logits, args.reps, flush))
         t_topk = _median(_timed(torch, run_topk, args.reps, flush))
         t_both = _median(_timed(torch, run_both, args.reps, flush))
+        t_fused = _median(_timed(torch, run_fused, args.reps, flush))
         causal_pairs = sum(min(S2, S2 - S1 + t + 1) for t in range(S1))
         idx_flops = 2.0 * Hi * 128 * S1 * S2
         idx_tflops = idx_flops / (t_log * 1e-3) / 1e12
@@ -634,9 +672,13 @@ def main():
             "topk_gbs": round(topk_gbs, 1),
             "topk_frac_hbm": round(topk_gbs / PEAK_HBM_GBS, 4),
             "roofline_us": round((idx_flops / (PEAK_FP8_TFLOPS * 1e12) + topk_bytes / (PEAK_HBM_GBS * 1e9)) * 1e6, 1),
+            "fused_us": round(t_fused * 1e3, 1),
+            "fused_equals_dense": fused_same,
+            "fused_fallback_rows": fused_fallback,
         }
-        _log(f"C2: indexer {t_log * 1e3:.1f} us, topk {t_topk * 1e3:.1f} us, both {t_both * 1e3:.1f} us")
-        del qi, ki, wi, ksi, logits, out_idx
+        _log(f"C2: indexer {t_log * 1e3:.1f} us, topk {t_topk * 1e3:.1f} us, both {t_both * 1e3:.1f} us, "
+             f"fused {t_fused * 1e3:.1f} us (same: {fused_same}, fallback rows {fused_fallback})")
+        del qi, ki, wi, ksi, logits, out_idx, fidx, fws
 
     # ---------------- decode (C3) ----------------
     if "decode" not in skip:

@@ -112,6 +112,40 @@ int dsa_lightning_indexer(int kind, const void* q, const void* k, const float* k
                           int64_t max_blocks, int sparse_mode, int64_t sparse_count, int32_t* out_idx,
                           float* out_val, void* workspace, size_t workspace_bytes, void* stream);
 
+/* 1 when dsa_lightning_indexer_fused streams the top-k for this shape (else it
+ * runs dsa_lightning_indexer). */
+int dsa_lightning_indexer_fused_applies(int64_t B, int64_t S1, int64_t S2, int64_t sparse_count);
+
+/* Workspace bytes dsa_lightning_indexer_fused needs (at least those of
+ * dsa_lightning_indexer). */
+size_t dsa_lightning_indexer_fused_workspace_size(int64_t B, int64_t S1, int64_t S2, int64_t sparse_count);
+
+/*
+ * dsa_lightning_indexer with the top-k streamed out of the indexer: same
+ * arguments and the same output bit for bit, without writing the logits of
+ * every row.  Replaces the same wrapper call as dsa_lightning_indexer; the
+ * fused sort + merge design of the reference's kernel
+ * (examples/deepseek_v4/lightning_indexer.py:945-1033) is what it stands for.
+ * A sample of each row's logits sets a threshold, the indexer keeps only the
+ * keys that reach it, and the top-k runs over those; rows whose threshold turns
+ * out too high take the dense path.  Applies when S2 >= max(16384, 8 *
+ * sparse_count) and sparse_count <= 4096; otherwise this call runs
+ * dsa_lightning_indexer.
+ */
+int dsa_lightning_indexer_fused(int kind, const void* q, const void* k, const float* k_scale, const float* weights,
+                                int64_t B, int64_t S1, int64_t S2, int64_t H, int64_t D, const int32_t* actual_q_len,
+                                const int32_t* actual_k_len, const int32_t* block_table, int64_t block_size,
+                                int64_t max_blocks, int sparse_mode, int64_t sparse_count, int32_t* out_idx,
+                                float* out_val, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Diagnostic for the fused path: after a dsa_lightning_indexer_fused call on
+ * `workspace` (same shape), writes to device int *count the number of rows that
+ * went back to dense logits because their sampled threshold was too high or a key
+ * chunk overflowed its candidate slot (rows the register top-k handed to the
+ * exact kernel are not counted).  No counterpart in the reference. */
+int dsa_lightning_indexer_fused_fallback_rows(const void* workspace, int64_t B, int64_t S1, int64_t S2,
+                                              int64_t sparse_count, int32_t* count, void* stream);
+
 /*
  * Packed (TND) query rows.  The reference converts TND to padded BSND on the
  * host and back (examples/deepseek_v4/lightning_indexer.py:48-190 helpers,

@@ -1,0 +1,227 @@
+"""GPU parity of the fused (streaming) indexer -> top-k against the dense path and the oracle.
+
+The fused entry (``dsa_lightning_indexer_fused``) must give the dense path's
+output bit for bit: the same indices (sorted by score desc, index asc, -1
+padded) and the same values, on every path it can take -- the streamed top-k,
+rows with at most k valid keys (no threshold), and rows sent back to the dense
+logits because the sampled threshold was too high, a key chunk overflowed its
+candidate slot, or ties defeated the register top-k.  Inputs that force each
+fallback are built from the data (key scales), not from switches in the code.
+"""
+import pytest
+import torch
+
+from oracle import dsa_oracle as ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(B, S1, S2, H, D, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    qf = torch.randn(B, S1, H, D, generator=g)
+    kf = torch.randn(B, S2, D, generator=g)
+    w = torch.randn(B, S1, H, generator=g) / 8
+    if dtype == torch.float8_e4m3fn:
+        q = qf.to(torch.float8_e4m3fn)
+        k, ks = ref.fp8_quantize_per_token(kf)
+    else:
+        q, k, ks = qf.to(dtype), kf.to(dtype), torch.ones(B, S2)
+    return q, k, w, ks
+
+
+def _both(dsa, dev, q, k, w, ks, K, **kw):
+    args = (q.to(dev), k.to(dev), w.to(dev))
+    kw = dict(kw, key_scale=ks.to(dev), sparse_count=K)
+    a = dsa.lightning_indexer(*args, fuse_topk=True, **kw)
+    b = dsa.lightning_indexer(*args, fuse_topk=False, **kw)
+    torch.cuda.synchronize()
+    return a, b
+
+
+def _fused_c(dsa, dev, q, k, w, ks, K):
+    """The fused entry through the C ABI (contiguous BSND keys): (indices, values, rows sent
+    back to dense logits by a too-high threshold or a chunk overflow)."""
+    lib = dsa.load_library()
+    B, S1, H, D = q.shape
+    S2 = k.shape[1]
+    qd, kd, wd, ksd = q.to(dev), k.contiguous().to(dev), w.float().to(dev), ks.float().to(dev)
+    idx = torch.empty((B, S1, K), dtype=torch.int32, device=dev)
+    val = torch.empty((B, S1, K), dtype=torch.float32, device=dev)
+    nb = lib.dsa_lightning_indexer_fused_workspace_size(B, S1, S2, K)
+    ws = torch.empty((nb,), dtype=torch.uint8, device=dev)
+    cnt = torch.full((1,), -1, dtype=torch.int32, device=dev)
+    kind = 0 if q.dtype == torch.float8_e4m3fn else 1
+    st = torch.cuda.current_stream(dev).cuda_stream
+    rc = lib.dsa_lightning_indexer_fused(kind, qd.data_ptr(), kd.data_ptr(), ksd.data_ptr(), wd.data_ptr(), B, S1,
+                                         S2, H, D, None, None, None, 0, 0, 3, K, idx.data_ptr(), val.data_ptr(),
+                                         ws.data_ptr(), nb, st)
+    assert rc == 0
+    assert lib.dsa_lightning_indexer_fused_fallback_rows(ws.data_ptr(), B, S1, S2, K, cnt.data_ptr(), st) == 0
+    torch.cuda.synchronize()
+    return idx.view(B, S1, 1, K), val.view(B, S1, 1, K), int(cnt.item())
+
+
+def _applies(dsa, B, S1, S2, K):
+    return dsa.load_library().dsa_lightning_indexer_fused_applies(B, S1, S2, K) == 1
+
+
+@pytest.mark.parametrize("sparse_mode", [3, 0])
+def test_fused_equals_dense_c2_shape(dsa, dev, sparse_mode):
+    """C2's row length (32768 keys, 64 fp8 heads, top-2048) on 256 query rows at the tail."""
+    B, S1, S2, H, D, K = 1, 256, 32768, 64, 128, 2048
+    print(f"fused indexer C2 shape mode={sparse_mode}", flush=True)
+    assert _applies(dsa, B, S1, S2, K)
+    q, k, w, ks = _inputs(B, S1, S2, H, D, torch.float8_e4m3fn, 31)
+    (fi, fv), (di, dv) = _both(dsa, dev, q, k.unsqueeze(2), w, ks, K, sparse_mode=sparse_mode, return_value=True)
+    assert torch.equal(fi, di) and torch.equal(fv, dv)
+    if sparse_mode == 3:  # the streamed path did the work: no row went back to dense logits
+        ci, cv, nfb = _fused_c(dsa, dev, q, k, w, ks, K)
+        assert nfb == 0 and torch.equal(ci, di) and torch.equal(cv, dv)
+    # Anchored on the oracle too: its top-k of the GPU logits, for a few rows.
+    logits = dsa.indexer_logits(q.to(dev), k.unsqueeze(2).to(dev), w.to(dev), ks.to(dev),
+                                sparse_mode=sparse_mode).cpu().view(S1, S2)
+    rows = [0, 1, 100, 255]
+    ri, rv = ref.topk_stable(logits[rows], K)
+    assert torch.equal(fi.cpu().view(S1, K)[rows], ri) and torch.equal(fv.cpu().view(S1, K)[rows], rv)
+
+
+def test_fused_ragged_bf16_short_rows(dsa, dev):
+    """bf16, D 64, 32 heads, two batches with actual lengths: rows with fewer valid keys than k
+    (no threshold), rows just above k, padded query rows; S2 not a multiple of 64."""
+    B, S1, S2, H, D, K = 2, 96, 20000, 32, 64, 1024
+    print("fused indexer ragged bf16", flush=True)
+    assert _applies(dsa, B, S1, S2, K)
+    q, k, w, ks = _inputs(B, S1, S2, H, D, torch.bfloat16, 32)
+    aq = torch.tensor([96, 40], dtype=torch.int32)
+    ak = torch.tensor([20000, 1100], dtype=torch.int32)
+    (fi, fv), (di, dv) = _both(dsa, dev, q, k.unsqueeze(2), w, ks, K, sparse_mode=3, return_value=True,
+                               actual_seq_lengths_query=aq.to(dev), actual_seq_lengths_key=ak.to(dev))
+    assert torch.equal(fi, di) and torch.equal(fv.float(), dv.float())
+    assert (fi[1, :40] >= 0).sum(-1).max().item() <= 1100 and (fi[1, 40:] == -1).all()
+
+
+def test_fused_paged_keys(dsa, dev):
+    B, S1, S2, H, D, K, bs = 2, 48, 16384, 64, 128, 2048, 64
+    print("fused indexer paged", flush=True)
+    q, k, w, ks = _inputs(B, S1, S2, H, D, torch.float8_e4m3fn, 33)
+    nblk = S2 // bs
+    perm = torch.randperm(B * nblk, generator=torch.Generator().manual_seed(4))
+    table = perm.view(B, nblk).to(torch.int32)
+    pool = torch.empty(B * nblk, bs, 1, D, dtype=torch.float8_e4m3fn)
+    pscale = torch.empty(B * nblk, bs)
+    for b in range(B):
+        pool[table[b].long()] = k[b].view(nblk, bs, 1, D)
+        pscale[table[b].long()] = ks[b].view(nblk, bs)
+    ak = torch.tensor([16384, 9000], dtype=torch.int32)
+    (fi, _), (di, _) = _both(dsa, dev, q, pool, w, pscale, K, block_table=table.to(dev), layout_key="PA_BSND",
+                             actual_seq_lengths_key=ak.to(dev))
+    assert torch.equal(fi, di)
+    # The paged call equals the contiguous one.
+    ci, _ = dsa.lightning_indexer(q.to(dev), k.unsqueeze(2).to(dev), w.to(dev), key_scale=ks.to(dev),
+                                  sparse_count=K, actual_seq_lengths_key=ak.to(dev), fuse_topk=True)
+    assert torch.equal(fi, ci)
+
+
+def test_fused_threshold_too_high_falls_back(dsa, dev):
+    """Sampled keys (the first 64 of every 1024 at S2 = 32768) scaled up 50x: the sampled
+    threshold sits above every other key, fewer than k keys reach it, every row is recomputed
+    densely."""
+    B, S1, S2, H, D, K = 1, 64, 32768, 64, 128, 2048
+    print("fused indexer forced fallback (threshold)", flush=True)
+    q, k, w, ks = _inputs(B, S1, S2, H, D, torch.float8_e4m3fn, 34)
+    pos = torch.arange(S2)
+    ks = torch.where((pos % 1024) < 64, ks * 50, ks)
+    (fi, fv), (di, dv) = _both(dsa, dev, q, k.unsqueeze(2), w, ks, K, return_value=True)
+    assert torch.equal(fi, di) and torch.equal(fv, dv)
+    ci, cv, nfb = _fused_c(dsa, dev, q, k, w, ks, K)
+    assert nfb == S1 and torch.equal(ci, di) and torch.equal(cv, dv)
+
+
+def test_fused_chunk_overflow_falls_back(dsa, dev):
+    """k = 256: each key chunk keeps at most 1024 keys; the first chunk's unsampled keys scaled
+    up 50x overflow it."""
+    B, S1, S2, H, D, K = 1, 64, 32768, 64, 128, 256
+    print("fused indexer forced fallback (overflow)", flush=True)
+    q, k, w, ks = _inputs(B, S1, S2, H, D, torch.float8_e4m3fn, 35)
+    pos = torch.arange(S2)
+    ks = torch.where((pos < 4096) & ((pos % 1024) >= 64), ks * 50, ks)
+    (fi, fv), (di, dv) = _both(dsa, dev, q, k.unsqueeze(2), w, ks, K, return_value=True)
+    assert torch.equal(fi, di) and torch.equal(fv, dv)
+    ci, cv, nfb = _fused_c(dsa, dev, q, k, w, ks, K)
+    assert nfb > 0 and torch.equal(ci, di) and torch.equal(cv, dv)
+
+
+def test_fused_heavy_ties(dsa, dev):
+    """Most key scales zero: most logits are exactly 0, ties everywhere (lower index wins)."""
+    B, S1, S2, H, D, K = 1, 64, 32768, 64, 128, 2048
+    print("fused indexer ties", flush=True)
+    q, k, w, ks = _inputs(B, S1, S2, H, D, torch.float8_e4m3fn, 36)
+    ks = torch.where(torch.arange(S2) % 7 == 0, ks, torch.zeros_like(ks))
+    (fi, fv), (di, dv) = _both(dsa, dev, q, k.unsqueeze(2), w, ks, K, return_value=True)
+    assert torch.equal(fi, di) and torch.equal(fv, dv)
+
+
+def test_fused_long_rows_two_stage_shape(dsa, dev):
+    """S2 = 65536 (the dense path takes the two-stage top-k there), 32 rows at the tail."""
+    B, S1, S2, H, D, K = 1, 32, 65536, 64, 128, 2048
+    print("fused indexer long rows", flush=True)
+    q, k, w, ks = _inputs(B, S1, S2, H, D, torch.float8_e4m3fn, 37)
+    (fi, fv), (di, dv) = _both(dsa, dev, q, k.unsqueeze(2), w, ks, K, return_value=True)
+    assert torch.equal(fi, di) and torch.equal(fv, dv)
+
+
+def test_fused_entry_on_a_short_shape_runs_dense(dsa, dev):
+    B, S1, S2, H, D, K = 1, 16, 4096, 64, 128, 2048
+    assert not _applies(dsa, B, S1, S2, K)
+    q, k, w, ks = _inputs(B, S1, S2, H, D, torch.float8_e4m3fn, 38)
+    (fi, _), (di, _) = _both(dsa, dev, q, k.unsqueeze(2), w, ks, K)
+    assert torch.equal(fi, di)
+
+
+def test_fused_tied_candidates_resolved_on_packed_rows(dsa, dev):
+    """700 copies of one key (same row, same scale, x3) at unsampled positions: where their logit
+    is large they all become candidates with one value -- a bin the register top-k will not rank,
+    resolved by the exact kernel on the packed candidates (no dense recompute)."""
+    B, S1, S2, H, D, K = 1, 64, 32768, 64, 128, 2048
+    print("fused indexer tied candidates", flush=True)
+    q, k, w, ks = _inputs(B, S1, S2, H, D, torch.float8_e4m3fn, 39)
+    pos = torch.arange(S2)
+    clones = pos[(pos % 1024) >= 64][::40][:700]
+    k = k.clone()
+    k[0, clones] = k[0, 5].clone()
+    ks = ks.clone()
+    ks[0, clones] = ks[0, 5] * 3
+    (fi, fv), (di, dv) = _both(dsa, dev, q, k.unsqueeze(2), w, ks, K, return_value=True)
+    assert torch.equal(fi, di) and torch.equal(fv, dv)
+    ci, cv, nfb = _fused_c(dsa, dev, q, k, w, ks, K)
+    assert nfb == 0 and torch.equal(ci, di) and torch.equal(cv, dv)
+
+
+def test_fused_default_torch_op_and_graph_capture(dsa, dev):
+    """Rows over 32768 keys take the fused path by default, in the wrapper and in
+    torch.ops.dsa.lightning_indexer; the op captured in a HIP graph replays to the same output."""
+    B, S1, S2, H, D, K = 1, 32, 65536, 64, 128, 2048
+    print("fused indexer default path + graph", flush=True)
+    q, k, w, ks = _inputs(B, S1, S2, H, D, torch.float8_e4m3fn, 40)
+    qd, kd, wd, ksd = q.to(dev), k.unsqueeze(2).to(dev), w.to(dev), ks.to(dev)
+    di, dv = dsa.lightning_indexer(qd, kd, wd, key_scale=ksd, sparse_count=K, return_value=True, fuse_topk=False)
+    ai, av = dsa.lightning_indexer(qd, kd, wd, key_scale=ksd, sparse_count=K, return_value=True)
+    ops = dsa.load_torch_ops()
+    oi, ov = ops.lightning_indexer(qd, kd, wd, ksd, sparse_count=K, sparse_mode=3, return_value=True)
+    torch.cuda.synchronize()
+    assert torch.equal(ai, di) and torch.equal(av, dv) and torch.equal(oi, di) and torch.equal(ov, dv)
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        ops.lightning_indexer(qd, kd, wd, ksd, sparse_count=K, sparse_mode=3, return_value=True)
+    torch.cuda.current_stream(dev).wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gi, gv = ops.lightning_indexer(qd, kd, wd, ksd, sparse_count=K, sparse_mode=3, return_value=True)
+    for _ in range(3):
+        gi.fill_(7)
+        gv.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gi, di) and torch.equal(gv, dv)

@@ -41,6 +41,12 @@ SIGNATURES = {
     "dsa_lightning_indexer": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                        _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_i64, _c_vp, _c_vp, _c_vp,
                                        _c_size, _c_vp]),
+    "dsa_lightning_indexer_fused_applies": (_c_int, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "dsa_lightning_indexer_fused_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "dsa_lightning_indexer_fused": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64,
+                                             _c_i64, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_i64, _c_vp,
+                                             _c_vp, _c_vp, _c_size, _c_vp]),
+    "dsa_lightning_indexer_fused_fallback_rows": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp]),
     "dsa_indexer_logits_tnd": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                         _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_vp, _c_i64,
                                         _c_vp]),

@@ -26,6 +26,12 @@ __device__ __forceinline__ uint32_t float_key(float v) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// Inverse of float_key for keys of non-NaN values.
+__device__ __forceinline__ float key_to_float(uint32_t k) {
+  uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __uint_as_float(u);
+}
+
 __host__ __device__ constexpr uint32_t float_key_host(uint32_t u) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
@@ -33,6 +39,9 @@ __host__ __device__ constexpr uint32_t float_key_host(uint32_t u) {
 // Key of -1e30f: keys at or below it are "absent" (reported as index -1).
 // -1e30f = 0xF149F2CA.
 constexpr uint32_t kKeyInvalidMax = float_key_host(0xF149F2CAu);
+
+// out_idx[row][0] marker of the top-k paths: the row needs the exact radix path.
+constexpr int32_t kFallbackFlag = (int32_t)0x80000000;
 
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll

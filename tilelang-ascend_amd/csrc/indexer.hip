@@ -160,13 +160,71 @@ struct IdxArgs {
   int block_size, max_blocks;
   int sparse_mode;
   int key_chunk;
+  // Fused top-k (indexer_topk_fused): the sample and filter passes, and the
+  // dense pass restricted to flagged rows.  Rows are global query rows (q_base + t).
+  int tile_stride;          // keys between consecutive tiles: 64, or 64 * F in the sample pass
+  float* sample;            // [rows, sample_ld]: logits of the first 64 keys of every 64 * F
+  int64_t sample_ld;
+  float* thr;               // [rows]: written by the sample pass; the filter pass keeps keys with logit >= thr
+  int topk;
+  float* cand_val;          // [rows, nseg, cand_cap]: kept logits per (row, key chunk), in key order
+  int32_t* cand_idx;        // [rows, nseg, cand_cap]: their key positions
+  int32_t* cand_cnt;        // [rows, nseg]: keys kept (may exceed cand_cap: overflow)
+  int cand_cap;
+  const int32_t* flag_idx;  // dense pass: only workgroups with a row whose flag_idx[row * flag_ld] is kFallbackFlag
+  int64_t flag_ld;
 };
+
+enum IdxMode : int { kModeDense = 0, kModeSample = 1, kModeFilter = 2 };
 
 // kNhb = H / 16 head blocks, a compile-time count: no branch between the MFMAs.
 // kPaged: keys (and their scales) through the block table; otherwise one
 // contiguous [B, S2] run, addressed from per-thread bases and tile offsets.
-template <int kKind, int kD, int kTokPW, int kNhb, bool kPaged>
-__global__ __launch_bounds__(kIdxThreads) void indexer_logits_kernel(IdxArgs a) {
+// Filter threshold of one row, by one wave: the r-th largest valid sampled logit
+// rounded down to 16 key bits (sign, exponent, 7 mantissa bits: any threshold
+// keeps the result exact, this one only decides how many keys are kept),
+// r = mu + 4 sqrt(mu) + 2 with mu = k * sampled / valid the expected number of
+// sampled keys in the row's top k; -inf (keep every valid key) when the row has
+// at most k valid keys.  Absent samples hold key 0, below every candidate, and
+// counts over the wave come from ballots (scalar popcounts).
+template <int kPer>
+__device__ __forceinline__ float row_threshold(const float* __restrict__ sr, int m, int nv, int k, int lane) {
+  uint32_t key[kPer];
+  float x[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) x[i] = sr[min(lane + i * kWave, m - 1)];  // no branch: the loads overlap
+  int present = 0;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const uint32_t kk = float_key(x[i]);
+    const bool ok = lane + i * kWave < m && kk > kKeyInvalidMax;  // absent: past m, NaN, <= -1e30
+    key[i] = ok ? kk : 0u;
+    present += (int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(ok));
+  }
+  if (nv <= k || present == 0) return -__builtin_huge_valf();
+  const float mu = (float)k * (float)present / (float)nv;
+  const int r = min((int)ceilf(mu + 4.f * sqrtf(mu) + 2.f), present);
+  // The largest x (16 high bits) with #(key >= x) >= r, bit by bit.
+  uint32_t res = 0u;
+  for (int bit = 31; bit >= 16; --bit) {
+    const uint32_t cand = res | (1u << bit);
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) c += (int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(key[i] >= cand));
+    if (c >= r) res = cand;
+  }
+  return key_to_float(res);
+}
+
+//
+// Modes.  Dense: every logit of the chunk to `logits`.  Sample: only the first
+// tile of every tile_stride keys, to consecutive slots of `sample` (masked keys
+// as -inf), then each row's filter threshold.  Filter: no logits; each wave keeps,
+// per token, the valid keys whose logit is >= thr[row] (and > -1e30), appending
+// (logit, position) in key order to the row's slot of this key chunk -- a ballot
+// prefix gives each lane its slot, so no atomics -- and finally the kept count.
+template <int kKind, int kD, int kTokPW, int kNhb, bool kPaged, int kMode>
+__device__ __forceinline__ void indexer_body(const IdxArgs& a) {
   constexpr int kRB = IdxTraits<kKind, kD>::kRowBytes;
   constexpr int kLB = IdxTraits<kKind, kD>::kLaneBytes;
   constexpr int kPitch = lds_pitch<kKind, kD>();
@@ -195,6 +253,16 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_logits_kernel(IdxArgs a) 
                         : (a.ak_len ? min(max(a.ak_len[b], 0), a.S2) : a.S2);
   const int t_rows = a.cu_q ? aq : a.S1;  // rows of this batch that exist in the output
   constexpr int nhb = kNhb;
+  if (kMode == kModeDense && a.flag_idx) {  // block-uniform: every thread reads the same flags
+    bool any = false;
+#pragma unroll
+    for (int j = 0; j < kTok; ++j) {
+      const int t = t_base + j;
+      if (t < t_rows) any |= a.flag_idx[(q_base + t) * a.flag_ld] == kFallbackFlag;
+    }
+    if (!any) return;
+  }
+  const int tstride = kMode == kModeSample ? a.tile_stride : kIdxKeyTile;
 
   // Valid key count per token of this wave (0 for padded rows).
   int nvalid[kTokPW];
@@ -286,7 +354,20 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_logits_kernel(IdxArgs a) 
   }
 
   const int tile_end = min(key1, max_valid);  // keys at or past this are -inf for every token
-  const int ntiles = tile_end > key0 ? (tile_end - key0 + kIdxKeyTile - 1) / kIdxKeyTile : 0;
+  const int ntiles = tile_end > key0 ? (tile_end - key0 + tstride - 1) / tstride : 0;
+
+  // Filter mode: this wave's tokens' thresholds and kept counts.
+  float thr[kTokPW];
+  int kept[kTokPW];
+#pragma unroll
+  for (int j = 0; j < kTokPW; ++j) {
+    const int t = t_base + wave * kTokPW + j;
+    kept[j] = 0;
+    // Raised to the float just above -1e30: v >= thr then also rejects masked keys
+    // (-inf), scores the top-k never selects (<= -1e30) and NaN.
+    thr[j] = (kMode == kModeFilter && t < t_rows) ? fmaxf(a.thr[q_base + t], __uint_as_float(0xF149F2C9u))
+                                                  : __builtin_huge_valf();
+  }
 
   // Global -> register staging, two tiles in flight: tile t lands in
   // stage[t & 1] two tiles ahead of its use and goes to LDS one tile ahead.
@@ -298,19 +379,19 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_logits_kernel(IdxArgs a) 
   const uint8_t* kthread = a.k + (k_base + key0 + kr0) * kRB + (tid % (kRB / 16)) * 16;
   auto fetch = [&](auto slot_c, int tile) {
     constexpr int slot = decltype(slot_c)::value;
-    const int rows_left = tile_end - key0 - tile * kIdxKeyTile;  // block-uniform
+    const int rows_left = tile_end - key0 - tile * tstride;  // block-uniform
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
       const int kr = kr0 + i * kRowsPerLoad;    // key row in tile
       u32x4 v = {0, 0, 0, 0};
       if (kr < rows_left) {
         if constexpr (kPaged) {
-          const int s = key0 + tile * kIdxKeyTile + kr;
+          const int s = key0 + tile * tstride + kr;
           const int blk = a.block_table[(int64_t)b * a.max_blocks + s / a.block_size];
           const int64_t rowi = (int64_t)blk * a.block_size + s % a.block_size;
           v = *reinterpret_cast<const u32x4*>(a.k + rowi * kRB + (tid % (kRB / 16)) * 16);
         } else {
-          v = *reinterpret_cast<const u32x4*>(kthread + ((int64_t)tile * kIdxKeyTile + i * kRowsPerLoad) * kRB);
+          v = *reinterpret_cast<const u32x4*>(kthread + ((int64_t)tile * tstride + i * kRowsPerLoad) * kRB);
         }
       }
       stage[slot][i] = v;
@@ -386,8 +467,8 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_logits_kernel(IdxArgs a) 
         }
       }
     }
-    // Lane l now holds key (tile*64 + l) for each token.
-    const int s = key0 + tile * kIdxKeyTile + lane;
+    // Lane l now holds key (tile * tstride + l) of the chunk for each token.
+    const int s = key0 + tile * tstride + lane;
     float sc = 1.f;
     if (a.k_scale && s < tile_end) {
       if constexpr (kPaged) {
@@ -400,9 +481,27 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_logits_kernel(IdxArgs a) 
 #pragma unroll
     for (int j = 0; j < kTokPW; ++j) {
       const int t = t_base + wave * kTokPW + j;
-      if (t < t_rows && s < key1) {
-        const float v = (s < nvalid[j]) ? res[j] * (sc * post[j]) : -__builtin_huge_valf();
-        __builtin_nontemporal_store(v, &a.logits[(q_base + t) * a.ld + s]);
+      const float v = (s < nvalid[j]) ? res[j] * (sc * post[j]) : -__builtin_huge_valf();
+      if constexpr (kMode == kModeDense) {
+        if (t < t_rows && s < key1) __builtin_nontemporal_store(v, &a.logits[(q_base + t) * a.ld + s]);
+      } else if constexpr (kMode == kModeSample) {
+        if (t < t_rows && s < key1)
+          a.sample[(q_base + t) * a.sample_ld + (int64_t)(key0 / tstride + tile) * kIdxKeyTile + lane] = v;
+      } else {
+        // Masked keys (s >= nvalid, which covers keys past the chunk: chunks are
+        // whole tiles) hold -inf and fail v >= thr; thr is +inf on padded rows.
+        const bool keep = v >= thr[j];
+        const uint64_t bal = __builtin_amdgcn_ballot_w64(keep);
+        if (bal) {  // wave-uniform
+          const int pos = kept[j] + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+          if (keep && pos < a.cand_cap) {
+            const int64_t o = ((q_base + t) * gridDim.x + blockIdx.x) * a.cand_cap + pos;
+            a.cand_val[o] = v;
+            a.cand_idx[o] = s;
+          }
+          kept[j] += (int)__builtin_popcountll(bal);
+        }
       }
     }
     // Buffer (tile + 1) % 3 was last read two tiles ago, before the previous barrier.
@@ -414,24 +513,77 @@ __global__ __launch_bounds__(kIdxThreads) void indexer_logits_kernel(IdxArgs a) 
     if (tile + 1 < ntiles) step(Slot1{}, tile + 1);
   }
 
-  // Keys of this chunk past every token's bound: -inf.
-  const int masked0 = key0 + ntiles * kIdxKeyTile;
+  if constexpr (kMode == kModeDense) {
+    // Keys of this chunk past every token's bound: -inf.
+    const int masked0 = key0 + ntiles * kIdxKeyTile;
 #pragma unroll
-  for (int j = 0; j < kTokPW; ++j) {
-    const int t = t_base + wave * kTokPW + j;
-    if (t < t_rows) {
-      float* row = a.logits + (q_base + t) * a.ld;
-      for (int s = masked0 + lane; s < key1; s += kWave) __builtin_nontemporal_store(-__builtin_huge_valf(), &row[s]);
+    for (int j = 0; j < kTokPW; ++j) {
+      const int t = t_base + wave * kTokPW + j;
+      if (t < t_rows) {
+        float* row = a.logits + (q_base + t) * a.ld;
+        for (int s = masked0 + lane; s < key1; s += kWave) __builtin_nontemporal_store(-__builtin_huge_valf(), &row[s]);
+      }
+    }
+  } else if constexpr (kMode == kModeSample) {
+    // Sample slots of this chunk's tiles past every token's bound: -inf.
+    const int slot0 = key0 / tstride * kIdxKeyTile;
+    const int slot1 = (key1 + tstride - 1) / tstride * kIdxKeyTile;
+#pragma unroll
+    for (int j = 0; j < kTokPW; ++j) {
+      const int t = t_base + wave * kTokPW + j;
+      if (t < t_rows) {
+        float* row = a.sample + (q_base + t) * a.sample_ld;
+        for (int c = slot0 + ntiles * kIdxKeyTile + lane; c < slot1; c += kWave) row[c] = -__builtin_huge_valf();
+      }
+    }
+    // With one key chunk this workgroup wrote its rows' whole sample: each wave
+    // turns its own rows into thresholds (the barrier makes the stores visible).
+    if (gridDim.x == 1) {
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < kTokPW; ++j) {
+        const int t = t_base + wave * kTokPW + j;
+        if (t < t_rows) {
+          const float* row = a.sample + (q_base + t) * a.sample_ld;
+          const float th = a.sample_ld <= 32 * kWave
+                               ? row_threshold<32>(row, (int)a.sample_ld, nvalid[j], a.topk, lane)
+                               : row_threshold<64>(row, (int)a.sample_ld, nvalid[j], a.topk, lane);
+          if (lane == 0) a.thr[q_base + t] = th;
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kTokPW; ++j) {
+      const int t = t_base + wave * kTokPW + j;
+      if (t < t_rows && lane == 0) a.cand_cnt[(q_base + t) * gridDim.x + blockIdx.x] = kept[j];
     }
   }
 }
 
-template <int kKind, int kD>
+template <int kKind, int kD, int kTokPW, int kNhb, bool kPaged, int kMode>
+__global__ __launch_bounds__(kIdxThreads) void indexer_logits_kernel(IdxArgs a) {
+  indexer_body<kKind, kD, kTokPW, kNhb, kPaged, kMode>(a);
+}
+
+// The fp8 filter pass, held to the dense pass's three waves per SIMD (its few
+// extra registers would otherwise cost a wave).
+template <int kD, int kTokPW, int kNhb, bool kPaged>
+__global__ __launch_bounds__(kIdxThreads) __attribute__((amdgpu_waves_per_eu(3, 3)))
+void indexer_filter_fp8_kernel(IdxArgs a) {
+  indexer_body<kFp8, kD, kTokPW, kNhb, kPaged, kModeFilter>(a);
+}
+
+template <int kKind, int kD, int kMode = kModeDense>
 static hipError_t launch_indexer_kind(const IdxArgs& a, int B, hipStream_t stream) {
   constexpr int kTokPW = 2;
   constexpr int kTok = kTokPW * kIdxWaves;
   const dim3 grid((unsigned)((a.S2 + a.key_chunk - 1) / a.key_chunk), (unsigned)((a.S1 + kTok - 1) / kTok), (unsigned)B);
-#define DSA_IDX(N, P) hipLaunchKernelGGL((indexer_logits_kernel<kKind, kD, kTokPW, N, P>), grid, dim3(kIdxThreads), 0, stream, a)
+#define DSA_IDX(N, P)                                                                                           \
+  if constexpr (kKind == kFp8 && kMode == kModeFilter)                                                          \
+    hipLaunchKernelGGL((indexer_filter_fp8_kernel<kD, kTokPW, N, P>), grid, dim3(kIdxThreads), 0, stream, a);   \
+  else                                                                                                          \
+    hipLaunchKernelGGL((indexer_logits_kernel<kKind, kD, kTokPW, N, P, kMode>), grid, dim3(kIdxThreads), 0, stream, a)
 #define DSA_IDX2(N) \
   if (a.block_table) DSA_IDX(N, true); else DSA_IDX(N, false)
   switch ((a.H + 15) >> 4) {
@@ -445,14 +597,11 @@ static hipError_t launch_indexer_kind(const IdxArgs& a, int B, hipStream_t strea
   return hipGetLastError();
 }
 
-// kind: 0 fp8 e4m3fn, 1 bf16, 2 fp16.  Caller validated: D in {64, 128}, H % 16 == 0, H <= 64.
-hipError_t launch_indexer_logits(int kind, const void* q, const void* k, const float* k_scale, const float* w,
-                                 int64_t B, int64_t S1, int64_t S2, int64_t H, int64_t D,
-                                 const int32_t* aq_len, const int32_t* ak_len, const int32_t* cu_q,
-                                 const int32_t* cu_k, const int32_t* block_table, int64_t block_size,
-                                 int64_t max_blocks, int sparse_mode, float* logits, int64_t ld, hipStream_t stream) {
-  if (B == 0 || S1 == 0 || S2 == 0) return hipSuccess;
-  IdxArgs a;
+static IdxArgs make_idx_args(const void* q, const void* k, const float* k_scale, const float* w, int64_t S1,
+                             int64_t S2, int64_t H, const int32_t* aq_len, const int32_t* ak_len, const int32_t* cu_q,
+                             const int32_t* cu_k, const int32_t* block_table, int64_t block_size, int64_t max_blocks,
+                             int sparse_mode) {
+  IdxArgs a = {};
   a.q = static_cast<const uint8_t*>(q);
   a.k = static_cast<const uint8_t*>(k);
   a.k_scale = k_scale;
@@ -462,28 +611,250 @@ hipError_t launch_indexer_logits(int kind, const void* q, const void* k, const f
   a.cu_q = cu_q;
   a.cu_k = cu_k;
   a.block_table = block_table;
-  a.logits = logits;
-  a.ld = ld;
   a.S1 = (int)S1;
   a.S2 = (int)S2;
   a.H = (int)H;
   a.block_size = (int)block_size;
   a.max_blocks = (int)max_blocks;
   a.sparse_mode = sparse_mode;
-  // Enough workgroups to fill 256 CUs several times over.
+  a.tile_stride = kIdxKeyTile;
+  return a;
+}
+
+// Keys per workgroup: enough workgroups to fill 256 CUs several times over.
+static int64_t indexer_key_chunk(int64_t B, int64_t S1, int64_t S2) {
   const int64_t tok_groups = B * ((S1 + 7) / 8);
-  int64_t chunks = (2048 + tok_groups - 1) / tok_groups;
+  const int64_t chunks = (2048 + tok_groups - 1) / tok_groups;
   int64_t chunk = (S2 + chunks - 1) / chunks;
   chunk = ((chunk + kIdxKeyTile - 1) / kIdxKeyTile) * kIdxKeyTile;
-  if (chunk < 1024) chunk = 1024;
-  a.key_chunk = (int)chunk;
+  return chunk < 1024 ? 1024 : chunk;
+}
+
+template <int kMode>
+static hipError_t launch_indexer_mode(int kind, int64_t D, const IdxArgs& a, int64_t B, hipStream_t stream) {
   const bool d128 = (D == 128);
   switch (kind) {
-    case kFp8: return d128 ? launch_indexer_kind<kFp8, 128>(a, (int)B, stream) : launch_indexer_kind<kFp8, 64>(a, (int)B, stream);
-    case kBf16: return d128 ? launch_indexer_kind<kBf16, 128>(a, (int)B, stream) : launch_indexer_kind<kBf16, 64>(a, (int)B, stream);
-    case kFp16: return d128 ? launch_indexer_kind<kFp16, 128>(a, (int)B, stream) : launch_indexer_kind<kFp16, 64>(a, (int)B, stream);
+    case kFp8: return d128 ? launch_indexer_kind<kFp8, 128, kMode>(a, (int)B, stream)
+                           : launch_indexer_kind<kFp8, 64, kMode>(a, (int)B, stream);
+    case kBf16: return d128 ? launch_indexer_kind<kBf16, 128, kMode>(a, (int)B, stream)
+                            : launch_indexer_kind<kBf16, 64, kMode>(a, (int)B, stream);
+    case kFp16: return d128 ? launch_indexer_kind<kFp16, 128, kMode>(a, (int)B, stream)
+                            : launch_indexer_kind<kFp16, 64, kMode>(a, (int)B, stream);
     default: return hipErrorInvalidValue;
   }
+}
+
+// kind: 0 fp8 e4m3fn, 1 bf16, 2 fp16.  Caller validated: D in {64, 128}, 1 <= H <= 64.
+hipError_t launch_indexer_logits(int kind, const void* q, const void* k, const float* k_scale, const float* w,
+                                 int64_t B, int64_t S1, int64_t S2, int64_t H, int64_t D,
+                                 const int32_t* aq_len, const int32_t* ak_len, const int32_t* cu_q,
+                                 const int32_t* cu_k, const int32_t* block_table, int64_t block_size,
+                                 int64_t max_blocks, int sparse_mode, float* logits, int64_t ld, hipStream_t stream) {
+  if (B == 0 || S1 == 0 || S2 == 0) return hipSuccess;
+  IdxArgs a = make_idx_args(q, k, k_scale, w, S1, S2, H, aq_len, ak_len, cu_q, cu_k, block_table, block_size,
+                            max_blocks, sparse_mode);
+  a.logits = logits;
+  a.ld = ld;
+  a.key_chunk = (int)indexer_key_chunk(B, S1, S2);
+  return launch_indexer_mode<kModeDense>(kind, D, a, B, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Fused indexer -> top-k.  The logits of a row are never written whole:
+//   1. sample pass: the logits of the first 64 keys of every 64 F (about 2048
+//      keys per row);
+//   2. per row, at the end of the sample pass: thr = the r-th largest valid
+//      sampled logit, r = mu + 4 sqrt(mu) + 2 with mu = k * sampled / valid the
+//      expected number of sampled keys in the row's top k (thr = -inf when the
+//      row has at most k valid keys);
+//   3. filter pass: the indexer again, keeping (logit, key) for logit >= thr,
+//      per (row, key chunk) in key order;
+//   4. per row, the kept keys of all chunks packed in key order; the row is
+//      flagged when a chunk overflowed or when thr is finite and fewer than k
+//      keys reached it -- otherwise every key outside the kept set is below thr,
+//      which is at most the k-th largest logit, so the top k (ties to the lower
+//      index included) lie in the kept set;
+//   5. the register top-k over the packed rows (positions map back to keys), and
+//      the exact radix top-k over the packed rows it could not bound (ties);
+//   6. rows flagged in step 4 only: their dense logits and the exact radix top-k.
+// Steps 5-6 give the same output as the dense path bit for bit; step 6 costs an
+// early exit per workgroup when nothing is flagged.
+hipError_t launch_topk_candidates(const float* cval, const int32_t* cidx, const int32_t* row_len, int64_t rows,
+                                  int64_t ldc, int64_t k, int32_t* out_idx, float* out_val, hipStream_t stream);
+hipError_t launch_topk_flagged(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k, int32_t* out_idx,
+                               float* out_val, hipStream_t stream);
+
+constexpr int kFusedSampleTiles = 32;  // ~2048 sampled keys per row
+constexpr int kFusedMaxSeg = 8;
+
+struct FusedPlan {
+  bool fused;
+  int64_t rows, ld, sample_ld, ldc;
+  int64_t key_chunk, tile_stride;
+  int nseg, cap;
+  size_t dense, sample, thr, cval, cidx, ccnt, pval, pidx, plen, total;
+};
+
+static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+static FusedPlan fused_plan(int64_t B, int64_t S1, int64_t S2, int64_t k) {
+  FusedPlan p = {};
+  p.rows = B * S1;
+  p.ld = (S2 + 3) & ~int64_t(3);
+  // At most kFusedMaxSeg key chunks (candidate slots) per row.
+  const int64_t min_chunk = ((S2 + kFusedMaxSeg - 1) / kFusedMaxSeg + kIdxKeyTile - 1) / kIdxKeyTile * kIdxKeyTile;
+  p.key_chunk = indexer_key_chunk(B, S1, S2);
+  if (p.key_chunk < min_chunk) p.key_chunk = min_chunk;
+  p.nseg = (int)((S2 + p.key_chunk - 1) / p.key_chunk);
+  const int64_t tiles = (S2 + kIdxKeyTile - 1) / kIdxKeyTile;
+  const int64_t F = tiles / kFusedSampleTiles > 1 ? tiles / kFusedSampleTiles : 1;
+  p.tile_stride = F * kIdxKeyTile;
+  p.sample_ld = (S2 + p.tile_stride - 1) / p.tile_stride * kIdxKeyTile;  // <= 4096: F >= tiles / 64
+  const int64_t cap4k = (4 * k + 63) & ~int64_t(63);
+  p.cap = (int)(p.key_chunk < cap4k ? p.key_chunk : cap4k);
+  p.ldc = ((4 * k + 4095) / 4096) * 4096;
+  p.fused = k <= 4096 && S2 >= 16384 && S2 >= 8 * k &&
+            p.nseg <= kFusedMaxSeg && p.ldc <= 32768 && p.sample_ld <= 4096 && p.rows > 0;
+  size_t off = align256((size_t)p.rows * p.ld * sizeof(float));
+  p.dense = 0;
+  if (p.fused) {
+    const size_t R = (size_t)p.rows;
+    p.sample = off; off = align256(off + R * p.sample_ld * 4);
+    p.thr = off; off = align256(off + R * 4);
+    p.cval = off; off = align256(off + R * p.nseg * p.cap * 4);
+    p.cidx = off; off = align256(off + R * p.nseg * p.cap * 4);
+    p.ccnt = off; off = align256(off + R * p.nseg * 4);
+    p.pval = off; off = align256(off + R * p.ldc * 4);
+    p.pidx = off; off = align256(off + R * p.ldc * 4);
+    p.plen = off; off = align256(off + R * 4);
+  }
+  p.total = off;
+  return p;
+}
+
+// 0 when the fused path does not apply to this shape (the caller runs the dense path).
+size_t indexer_topk_fused_bytes(int64_t B, int64_t S1, int64_t S2, int64_t k) {
+  const FusedPlan p = fused_plan(B, S1, S2, k);
+  return p.fused ? p.total : 0;
+}
+
+__global__ __launch_bounds__(256) void fused_pack_kernel(const float* __restrict__ cval, const int32_t* __restrict__ cidx,
+                                                         const int32_t* __restrict__ ccnt, int nseg, int cap,
+                                                         const float* __restrict__ thr, int k, int ldc,
+                                                         float* __restrict__ pval, int32_t* __restrict__ pidx,
+                                                         int32_t* __restrict__ plen) {
+  __shared__ int offs[kFusedMaxSeg + 2];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  if (tid == 0) {
+    int tot = 0;
+    bool bad = false;
+    for (int s = 0; s < nseg; ++s) {
+      const int c = ccnt[row * nseg + s];
+      bad |= c > cap;
+      offs[s] = tot;
+      tot += min(c, cap);
+    }
+    bad |= tot > ldc || (tot < k && thr[row] != -__builtin_huge_valf());
+    offs[nseg] = tot;
+    offs[kFusedMaxSeg + 1] = bad;
+  }
+  __syncthreads();
+  const int tot = offs[nseg];
+  int32_t* pi = pidx + row * ldc;
+  if (offs[kFusedMaxSeg + 1]) {  // block-uniform
+    if (tid == 0) {
+      pi[0] = kFallbackFlag;  // the register top-k passes the flag on to the row's output
+      plen[row] = -1;         // and the exact kernel leaves it there
+    }
+    return;
+  }
+  float* pv = pval + row * ldc;
+  for (int s = 0; s < nseg; ++s) {
+    const int64_t src = (row * nseg + s) * cap;
+    const int n = offs[s + 1] - offs[s];
+    for (int i = tid; i < n; i += 256) {
+      pv[offs[s] + i] = cval[src + i];
+      pi[offs[s] + i] = cidx[src + i];
+    }
+  }
+  // The register top-k reads pidx[j * k] as segment flags: no stale flag past the row.
+  for (int j = tid; (int64_t)j * k < ldc; j += 256)
+    if (j * k >= tot) pi[j * k] = -1;
+  if (tid == 0) plen[row] = tot;
+}
+
+__global__ __launch_bounds__(256) void fused_count_flagged_kernel(const int32_t* __restrict__ pidx, int64_t rows,
+                                                                  int64_t ldc, int32_t* __restrict__ count) {
+  __shared__ int part[256 / kWave];
+  int c = 0;
+  for (int64_t r = threadIdx.x; r < rows; r += 256) c += pidx[r * ldc] == kFallbackFlag;
+  c = wave_sum_i(c);
+  if ((threadIdx.x & (kWave - 1)) == 0) part[threadIdx.x / kWave] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) count[0] = part[0] + part[1] + part[2] + part[3];
+}
+
+// Rows of the last fused call on `workspace` that went back to the dense logits because
+// the sampled threshold was too high or a key chunk overflowed (one int, written on `stream`).
+hipError_t launch_fused_fallback_rows(const void* workspace, int64_t B, int64_t S1, int64_t S2, int64_t k,
+                                      int32_t* count, hipStream_t stream) {
+  const FusedPlan p = fused_plan(B, S1, S2, k);
+  if (!p.fused) return hipErrorInvalidValue;
+  const int32_t* pidx = reinterpret_cast<const int32_t*>(static_cast<const uint8_t*>(workspace) + p.pidx);
+  hipLaunchKernelGGL(fused_count_flagged_kernel, dim3(1), dim3(256), 0, stream, pidx, p.rows, p.ldc, count);
+  return hipGetLastError();
+}
+
+// Caller validated as for launch_indexer_logits (BSND rows, optional paging), plus 1 <= k <= 8192
+// and a workspace of dsa_lightning_indexer_workspace_size + indexer_topk_fused_bytes bytes.
+hipError_t launch_indexer_topk_fused(int kind, const void* q, const void* k, const float* k_scale, const float* w,
+                                     int64_t B, int64_t S1, int64_t S2, int64_t H, int64_t D,
+                                     const int32_t* aq_len, const int32_t* ak_len, const int32_t* block_table,
+                                     int64_t block_size, int64_t max_blocks, int sparse_mode, int64_t topk,
+                                     int32_t* out_idx, float* out_val, void* workspace, hipStream_t stream) {
+  const FusedPlan p = fused_plan(B, S1, S2, topk);
+  if (!p.fused || B == 0 || S1 == 0) return hipErrorInvalidValue;
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  IdxArgs a = make_idx_args(q, k, k_scale, w, S1, S2, H, aq_len, ak_len, nullptr, nullptr, block_table, block_size,
+                            max_blocks, sparse_mode);
+  a.sample = reinterpret_cast<float*>(ws + p.sample);
+  a.sample_ld = p.sample_ld;
+  a.thr = reinterpret_cast<float*>(ws + p.thr);
+  a.topk = (int)topk;
+  a.cand_val = reinterpret_cast<float*>(ws + p.cval);
+  a.cand_idx = reinterpret_cast<int32_t*>(ws + p.cidx);
+  a.cand_cnt = reinterpret_cast<int32_t*>(ws + p.ccnt);
+  a.cand_cap = p.cap;
+  // 1-2. Sample pass and thresholds: one key chunk per row group (so each
+  // workgroup holds its rows' whole sample), tiles tile_stride apart.
+  a.tile_stride = (int)p.tile_stride;
+  a.key_chunk = (int)((S2 + p.tile_stride - 1) / p.tile_stride * p.tile_stride);
+  hipError_t e = launch_indexer_mode<kModeSample>(kind, D, a, B, stream);
+  if (e != hipSuccess) return e;
+  // 3. Filter pass over the usual key chunks (one candidate slot per chunk).
+  a.tile_stride = kIdxKeyTile;
+  a.key_chunk = (int)p.key_chunk;
+  if ((e = launch_indexer_mode<kModeFilter>(kind, D, a, B, stream)) != hipSuccess) return e;
+  // 4. Pack.
+  float* pval = reinterpret_cast<float*>(ws + p.pval);
+  int32_t* pidx = reinterpret_cast<int32_t*>(ws + p.pidx);
+  int32_t* plen = reinterpret_cast<int32_t*>(ws + p.plen);
+  hipLaunchKernelGGL(fused_pack_kernel, dim3((unsigned)p.rows), dim3(256), 0, stream, a.cand_val, a.cand_idx,
+                     a.cand_cnt, p.nseg, p.cap, a.thr, (int)topk, (int)p.ldc, pval, pidx, plen);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  // 5. Top-k over the packed rows.
+  if ((e = launch_topk_candidates(pval, pidx, plen, p.rows, p.ldc, topk, out_idx, out_val, stream)) != hipSuccess)
+    return e;
+  // 6. Rows still flagged: dense logits, then the exact radix top-k.
+  float* dense = reinterpret_cast<float*>(ws);
+  a.logits = dense;
+  a.ld = p.ld;
+  a.flag_idx = out_idx;
+  a.flag_ld = topk;
+  a.key_chunk = (int)p.key_chunk;
+  if ((e = launch_indexer_mode<kModeDense>(kind, D, a, B, stream)) != hipSuccess) return e;
+  return launch_topk_flagged(dense, p.ld, p.rows, S2, topk, out_idx, out_val, stream);
 }
 
 }  // namespace dsa

@@ -27,7 +27,6 @@ constexpr int kTopkWaves = kTopkThreads / kWave;
 constexpr int kHistBins = 2048;
 constexpr int kRedWords = 64;
 constexpr int kLdsBytes = 160 * 1024;
-constexpr int32_t kFallbackFlag = (int32_t)0x80000000;  // out_idx[row][0] marker: row needs the exact radix path
 
 // Inclusive wave scan and wave reductions on DPP (row shifts, then the row
 // broadcasts 15 and 31).
@@ -65,11 +64,6 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* red, u
   return before + incl - v;
 }
 
-__device__ __forceinline__ float key_to_float(uint32_t k) {
-  uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
-  return __uint_as_float(u);
-}
-
 template <bool kCached>
 __device__ __forceinline__ uint32_t load_key(const float* __restrict__ xr, const uint32_t* keys, int i) {
   if constexpr (kCached) return keys[i];
@@ -79,7 +73,8 @@ __device__ __forceinline__ uint32_t load_key(const float* __restrict__ xr, const
 template <bool kCached>
 __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(
     const float* __restrict__ x, int64_t ld, int n, int k, const int32_t* __restrict__ row_len,
-    int sorted, int kpad, int32_t* __restrict__ out_idx, float* __restrict__ out_val, int only_flagged) {
+    int sorted, int kpad, int32_t* __restrict__ out_idx, float* __restrict__ out_val, int only_flagged,
+    const int32_t* __restrict__ idx_map) {
   extern __shared__ __align__(16) uint32_t lds[];
   uint32_t* hist = lds;                                     // kHistBins
   uint32_t* red = hist + kHistBins;                         // kRedWords
@@ -91,11 +86,15 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(
   const float* __restrict__ xr = x + (int64_t)row * ld;
   int32_t* __restrict__ oi = out_idx + (int64_t)row * k;
   float* __restrict__ ov = out_val ? out_val + (int64_t)row * k : nullptr;
-  // Second pass behind topk_reg_kernel: only the rows it handed over.
+  // Second pass behind topk_reg_kernel: only the rows it handed over.  Over
+  // packed candidate rows (idx_map), a negative row length keeps the flag: the
+  // row's candidates are incomplete and it needs its dense logits.
   if (only_flagged && oi[0] != kFallbackFlag) return;
+  if (idx_map && row_len[row] < 0) return;
   __syncthreads();  // every thread has read the flag before any overwrites it
   int nv = n;
   if (row_len) nv = min(max(row_len[row], 0), n);
+  const int32_t* __restrict__ imap = idx_map ? idx_map + (int64_t)row * ld : nullptr;
 
   for (int b = tid; b < kHistBins; b += kTopkThreads) hist[b] = 0;
   __syncthreads();
@@ -195,7 +194,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(
         if (sorted) {
           sbuf[pos] = ((uint64_t)key[j] << 32) | (uint32_t)(~(uint32_t)idx);
         } else {
-          oi[pos] = idx;
+          oi[pos] = imap ? imap[idx] : idx;
           if (ov) ov[pos] = key_to_float(key[j]);
         }
       }
@@ -224,7 +223,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(
     }
     for (int i = tid; i < kk; i += kTopkThreads) {
       const uint64_t c = sbuf[i];
-      oi[i] = (int32_t)(~(uint32_t)c);
+      const int32_t p = (int32_t)(~(uint32_t)c);
+      oi[i] = imap ? imap[p] : p;
       if (ov) ov[i] = key_to_float((uint32_t)(c >> 32));
     }
   }
@@ -748,6 +748,10 @@ size_t topk_workspace_bytes(int64_t rows, int64_t n, int64_t k) {
 // Launch on `stream`.  Caller has validated shapes (rows, n >= 0; 1 <= k <= 8192) and, when
 // topk_workspace_bytes() is non-zero, passes a workspace of at least that size (else: nullptr,
 // and long rows take the radix kernel alone).
+static hipError_t launch_rows(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k,
+                              const int32_t* row_len, int sorted, int32_t* out_idx, float* out_val,
+                              int only_flagged, const int32_t* idx_map, hipStream_t stream);
+
 hipError_t launch_topk(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k,
                        const int32_t* row_len, int sorted, int32_t* out_idx, float* out_val,
                        void* workspace, hipStream_t stream) {
@@ -773,6 +777,32 @@ hipError_t launch_topk(const float* x, int64_t ld, int64_t rows, int64_t n, int6
     only_flagged = 1;
     sorted = 1;
   }
+  return launch_rows(x, ld, rows, n, k, row_len, sorted, out_idx, out_val, only_flagged, nullptr, stream);
+}
+
+// Top-k over packed candidate rows (the fused indexer): values cval [rows, ldc], the first
+// row_len[row] present, positions mapped to key indices through cidx (whose entries at
+// multiples of k must not be stale flags).  The register path, then the exact radix
+// kernel on the rows it could not bound.  Rows marked with row_len -1 and cidx[row][0] =
+// kFallbackFlag come out flagged in out_idx[row][0].
+hipError_t launch_topk_candidates(const float* cval, const int32_t* cidx, const int32_t* row_len, int64_t rows,
+                                  int64_t ldc, int64_t k, int32_t* out_idx, float* out_val, hipStream_t stream) {
+  if (rows == 0) return hipSuccess;
+  hipError_t e = launch_reg(cval, ldc, rows, ldc, k, row_len, out_idx, out_val, 1, ldc, cidx, stream);
+  if (e != hipSuccess) return e;
+  return launch_rows(cval, ldc, rows, ldc, k, row_len, 1, out_idx, out_val, 1, cidx, stream);
+}
+
+// The exact radix kernel for the rows whose out_idx[row][0] is kFallbackFlag (sorted output).
+hipError_t launch_topk_flagged(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k, int32_t* out_idx,
+                               float* out_val, hipStream_t stream) {
+  if (rows == 0) return hipSuccess;
+  return launch_rows(x, ld, rows, n, k, nullptr, 1, out_idx, out_val, 1, nullptr, stream);
+}
+
+static hipError_t launch_rows(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k,
+                              const int32_t* row_len, int sorted, int32_t* out_idx, float* out_val,
+                              int only_flagged, const int32_t* idx_map, hipStream_t stream) {
   const int kpad = sorted ? next_pow2((int)(k < 2 ? 2 : k)) : 0;
   const size_t base = (size_t)(kHistBins + kRedWords) * 4 + (size_t)kpad * 8;
   const size_t cached = base + (size_t)n * 4;
@@ -786,7 +816,7 @@ hipError_t launch_topk(const float* x, int64_t ld, int64_t rows, int64_t n, int6
       attr = true;
     }
     hipLaunchKernelGGL(topk_rows_kernel<true>, grid, block, lds, stream, x, ld, (int)n, (int)k, row_len,
-                       sorted, kpad, out_idx, out_val, only_flagged);
+                       sorted, kpad, out_idx, out_val, only_flagged, idx_map);
   } else {
     static bool attr = false;
     if (!attr) {
@@ -794,7 +824,7 @@ hipError_t launch_topk(const float* x, int64_t ld, int64_t rows, int64_t n, int6
       attr = true;
     }
     hipLaunchKernelGGL(topk_rows_kernel<false>, grid, block, lds, stream, x, ld, (int)n, (int)k, row_len,
-                       sorted, kpad, out_idx, out_val, only_flagged);
+                       sorted, kpad, out_idx, out_val, only_flagged, idx_map);
   }
   return hipGetLastError();
 }

@@ -100,9 +100,12 @@ std::tuple<at::Tensor, at::Tensor> lightning_indexer(const at::Tensor& query, co
   auto val = return_value ? at::empty({B, S1, 1, sparse_count}, query.options().dtype(at::kFloat))
                           : at::empty({0}, query.options().dtype(at::kFloat));
   if (B * S1 == 0) return {idx, val};
-  const size_t ws_bytes = dsa_lightning_indexer_workspace_size(B, S1, S2, sparse_count);
+  // Rows past 32768 keys stream the top-k out of the indexer (same output, no full logits).
+  const bool fused = S2 > 32768;
+  const size_t ws_bytes = fused ? dsa_lightning_indexer_fused_workspace_size(B, S1, S2, sparse_count)
+                                : dsa_lightning_indexer_workspace_size(B, S1, S2, sparse_count);
   auto ws = at::empty({(int64_t)(ws_bytes > 0 ? ws_bytes : 1)}, query.options().dtype(at::kByte));
-  check_rc(dsa_lightning_indexer(kind_of(query), ptr(query), ptr(key), ptr_or_null<float>(ks),
+  check_rc((fused ? dsa_lightning_indexer_fused : dsa_lightning_indexer)(kind_of(query), ptr(query), ptr(key), ptr_or_null<float>(ks),
                                  static_cast<float*>(ptr(w)), B, S1, S2, H, D, ptr_or_null<int32_t>(aq),
                                  ptr_or_null<int32_t>(ak), ptr_or_null<int32_t>(bt), paged ? key.size(1) : 0,
                                  paged ? bt->size(1) : 0, (int)sparse_mode, sparse_count,

@@ -231,7 +231,7 @@ def lightning_indexer(query: torch.Tensor, key: torch.Tensor, weights: torch.Ten
                       layout_key: str = "BSND", sparse_count: int = 2048, sparse_mode: int = 3,
                       pre_tokens: int = _INT64_MAX, next_tokens: int = _INT64_MAX, return_value: bool = False,
                       key_scale: Optional[torch.Tensor] = None, query_scale: Optional[torch.Tensor] = None,
-                      **tuning) -> Tuple[torch.Tensor, torch.Tensor]:
+                      fuse_topk: Optional[bool] = None, **tuning) -> Tuple[torch.Tensor, torch.Tensor]:
     """Top-``sparse_count`` key positions per query row: (indices [B, S1, 1, K] int32, values).
 
     Validation follows lightning_indexer.py:1229-1257.  ``layout_query="TND"``
@@ -242,7 +242,10 @@ def lightning_indexer(query: torch.Tensor, key: torch.Tensor, weights: torch.Ten
     (T on the empty early exit, lightning_indexer.py:1289-1296).  ``values`` is
     [B, S1, 1, K] (query dtype; fp32 for fp8 inputs) when ``return_value``, else
     an empty tensor.  Ascend tuning knobs (``block_n``, ``pp_slots``,
-    ``max_cores``) are accepted and ignored.
+    ``max_cores``) are accepted and ignored.  ``fuse_topk`` (BSND queries) streams
+    the top-k out of the indexer without writing every row's logits, where the
+    shape allows (``dsa_lightning_indexer_fused``); the output is the same bit for
+    bit.  The default (None) streams rows longer than 32768 keys, where it is faster.
     """
     unknown = set(tuning) - {"block_n", "pp_slots", "max_cores"}
     if unknown:
@@ -271,13 +274,16 @@ def lightning_indexer(query: torch.Tensor, key: torch.Tensor, weights: torch.Ten
         return idx, vals
     val = torch.empty((B, S1, 1, sparse_count), dtype=torch.float32, device=dev) if return_value else None
     lib = _lib.load_library()
-    ws_bytes = lib.dsa_lightning_indexer_workspace_size(B, S1, S2, sparse_count)
+    if fuse_topk is None:
+        fuse_topk = S2 > 32768
+    name = "dsa_lightning_indexer_fused" if fuse_topk else "dsa_lightning_indexer"
+    ws_bytes = getattr(lib, name + "_workspace_size")(B, S1, S2, sparse_count)
     ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
-    rc = lib.dsa_lightning_indexer(_KINDS[query.dtype], _lib.ptr(query), _lib.ptr(key), _lib.ptr(ks), _lib.ptr(w),
-                                   B, S1, S2, N1, D, _lib.ptr(aq), _lib.ptr(ak), _lib.ptr(bt), bs, mb, sparse_mode,
-                                   sparse_count, _lib.ptr(idx), _lib.ptr(val), _lib.ptr(ws), ws_bytes,
-                                   _lib.stream_handle(dev))
-    _lib.check(rc, "dsa_lightning_indexer")
+    rc = getattr(lib, name)(_KINDS[query.dtype], _lib.ptr(query), _lib.ptr(key), _lib.ptr(ks), _lib.ptr(w),
+                            B, S1, S2, N1, D, _lib.ptr(aq), _lib.ptr(ak), _lib.ptr(bt), bs, mb, sparse_mode,
+                            sparse_count, _lib.ptr(idx), _lib.ptr(val), _lib.ptr(ws), ws_bytes,
+                            _lib.stream_handle(dev))
+    _lib.check(rc, name)
     if return_value:
         return idx, val.to(vdt)
     return idx, torch.empty((0,), dtype=vdt, device=dev)
