@@ -187,6 +187,26 @@ int dsa_lightning_indexer_tnd(int kind, const void* q, const void* k, const floa
                               int64_t sparse_count, int32_t* out_idx, float* out_val, void* workspace,
                               size_t workspace_bytes, void* stream);
 
+/* Workspace bytes dsa_lightning_indexer_tnd_fused needs (at least those of
+ * dsa_lightning_indexer_tnd). */
+size_t dsa_lightning_indexer_tnd_fused_workspace_size(int64_t B, int64_t T, int64_t S1_max, int64_t S2_max,
+                                                      int64_t sparse_count);
+
+/*
+ * dsa_lightning_indexer_tnd with the top-k streamed out of the indexer, as
+ * dsa_lightning_indexer_fused does for padded rows: same arguments, same output
+ * bit for bit.  Replaces the same wrapper call (TND queries,
+ * examples/deepseek_v4/lightning_indexer.py:1202-1370).  Applies under the
+ * conditions of dsa_lightning_indexer_fused (S2_max in place of S2); otherwise
+ * runs dsa_lightning_indexer_tnd.
+ */
+int dsa_lightning_indexer_tnd_fused(int kind, const void* q, const void* k, const float* k_scale,
+                                    const float* weights, int64_t B, int64_t T, int64_t S1_max, int64_t S2_max,
+                                    int64_t H, int64_t D, const int32_t* cu_q, const int32_t* cu_k,
+                                    const int32_t* actual_k_len, const int32_t* block_table, int64_t block_size,
+                                    int64_t max_blocks, int sparse_mode, int64_t sparse_count, int32_t* out_idx,
+                                    float* out_val, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Workspace bytes dsa_sparse_mla_fwd needs (0 when no split of the index list is used). */
 size_t dsa_sparse_mla_workspace_size(int64_t B, int64_t S, int64_t H, int64_t topk);
 

@@ -209,3 +209,27 @@ def test_reference_example_tnd_paged(dsa, dev):
                                           sparse_mode=0)
     assert idx.shape == (sum(act_q), 1, K)
     assert _three_step(gi.view(-1, K), gl, idx.cpu().view(-1, K)) == 0
+
+
+def test_tnd_fused_topk_equals_dense(dsa, dev):
+    """Packed queries with the top-k streamed out of the indexer (dsa_lightning_indexer_tnd_fused):
+    bit-equal to the dense TND path, for packed and for paged keys, with an empty batch."""
+    q_lens, k_lens, H, D, K, bs = [33, 64, 0, 20], [20000, 40000, 9, 17000], 64, 128, 2048, 64
+    print("tnd fused top-k", flush=True)
+    q, k, w, ks, cu_q, cu_k = _packed(q_lens, k_lens, H, D, torch.float8_e4m3fn, seed=23)
+    qd, kd, wd, ksd = q.to(dev), k.unsqueeze(1).to(dev), w.to(dev), ks.to(dev)
+    cqd, ckd = cu_q.to(dev), cu_k.to(dev)
+    kw = dict(actual_seq_lengths_query=cqd, layout_query="TND", sparse_mode=3, sparse_count=K)
+    di, dv = dsa.lightning_indexer(qd, kd, wd, key_scale=ksd, actual_seq_lengths_key=ckd, layout_key="TND",
+                                   return_value=True, fuse_topk=False, **kw)
+    fi, fv = dsa.lightning_indexer(qd, kd, wd, key_scale=ksd, actual_seq_lengths_key=ckd, layout_key="TND",
+                                   return_value=True, **kw)  # default: fused for rows over 32768 keys
+    torch.cuda.synchronize()
+    assert torch.equal(fi, di) and torch.equal(fv, dv)
+    kp, _ = ref.tnd_to_padded(k.view(torch.uint8), cu_k.tolist())
+    sp, _ = ref.tnd_to_padded(ks, cu_k.tolist())
+    pool, pscale, table = _paged(kp.view(torch.float8_e4m3fn), sp, k_lens, bs, seed=5)
+    akd = torch.tensor(k_lens, dtype=torch.int32).to(dev)
+    pi, _ = dsa.lightning_indexer(qd, pool.to(dev), wd, key_scale=pscale.to(dev), actual_seq_lengths_key=akd,
+                                  block_table=table.to(dev), layout_key="PA_BSND", fuse_topk=True, **kw)
+    assert torch.equal(pi.cpu(), di.cpu())

@@ -54,6 +54,10 @@ SIGNATURES = {
     "dsa_lightning_indexer_tnd": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                            _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_i64, _c_vp,
                                            _c_vp, _c_vp, _c_size, _c_vp]),
+    "dsa_lightning_indexer_tnd_fused_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
+    "dsa_lightning_indexer_tnd_fused": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64,
+                                                 _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_int,
+                                                 _c_i64, _c_vp, _c_vp, _c_vp, _c_size, _c_vp]),
     "dsa_sparse_flash_mla_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64]),
     "dsa_sparse_flash_mla": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_vp,
                                       _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp,

@@ -9,14 +9,15 @@ namespace dsa {
 hipError_t launch_topk(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k, const int32_t* row_len,
                        int sorted, int32_t* out_idx, float* out_val, void* workspace, hipStream_t stream);
 size_t topk_workspace_bytes(int64_t rows, int64_t n, int64_t k);
-size_t indexer_topk_fused_bytes(int64_t B, int64_t S1, int64_t S2, int64_t k);
-hipError_t launch_fused_fallback_rows(const void* workspace, int64_t B, int64_t S1, int64_t S2, int64_t k,
-                                      int32_t* count, hipStream_t stream);
+size_t indexer_topk_fused_bytes(int64_t rows, int64_t B, int64_t S1, int64_t S2, int64_t k);
+hipError_t launch_fused_fallback_rows(const void* workspace, int64_t rows, int64_t B, int64_t S1, int64_t S2,
+                                      int64_t k, int32_t* count, hipStream_t stream);
 hipError_t launch_indexer_topk_fused(int kind, const void* q, const void* k, const float* k_scale, const float* w,
-                                     int64_t B, int64_t S1, int64_t S2, int64_t H, int64_t D,
-                                     const int32_t* aq_len, const int32_t* ak_len, const int32_t* block_table,
-                                     int64_t block_size, int64_t max_blocks, int sparse_mode, int64_t topk,
-                                     int32_t* out_idx, float* out_val, void* workspace, hipStream_t stream);
+                                     int64_t rows, int64_t B, int64_t S1, int64_t S2, int64_t H, int64_t D,
+                                     const int32_t* aq_len, const int32_t* ak_len, const int32_t* cu_q,
+                                     const int32_t* cu_k, const int32_t* block_table, int64_t block_size,
+                                     int64_t max_blocks, int sparse_mode, int64_t topk, int32_t* out_idx,
+                                     float* out_val, void* workspace, hipStream_t stream);
 hipError_t launch_indexer_logits(int kind, const void* q, const void* k, const float* k_scale, const float* w,
                                  int64_t B, int64_t S1, int64_t S2, int64_t H, int64_t D, const int32_t* aq_len,
                                  const int32_t* ak_len, const int32_t* cu_q, const int32_t* cu_k,
@@ -166,13 +167,13 @@ int dsa_lightning_indexer(int kind, const void* q, const void* k, const float* k
 
 int dsa_lightning_indexer_fused_applies(int64_t B, int64_t S1, int64_t S2, int64_t sparse_count) {
   if (B <= 0 || S1 <= 0 || S2 <= 0 || sparse_count < 1) return 0;
-  return dsa::indexer_topk_fused_bytes(B, S1, S2, sparse_count) > 0;
+  return dsa::indexer_topk_fused_bytes(B * S1, B, S1, S2, sparse_count) > 0;
 }
 
 size_t dsa_lightning_indexer_fused_workspace_size(int64_t B, int64_t S1, int64_t S2, int64_t sparse_count) {
   if (B <= 0 || S1 <= 0 || S2 <= 0) return 0;
   const int64_t k = sparse_count < 1 ? 1 : sparse_count;
-  const size_t fused = dsa::indexer_topk_fused_bytes(B, S1, S2, k);
+  const size_t fused = dsa::indexer_topk_fused_bytes(B * S1, B, S1, S2, k);
   return fused ? fused : dsa_lightning_indexer_workspace_size(B, S1, S2, sparse_count);
 }
 
@@ -188,13 +189,14 @@ int dsa_lightning_indexer_fused(int kind, const void* q, const void* k, const fl
     return reject("indexer: workspace too small");
   if (B * S1 > 0 && !out_idx) return reject("indexer: null out_idx");
   if (B * S1 == 0) return 0;
-  if (dsa::indexer_topk_fused_bytes(B, S1, S2, sparse_count) == 0)
+  if (dsa::indexer_topk_fused_bytes(B * S1, B, S1, S2, sparse_count) == 0)
     return dsa_lightning_indexer(kind, q, k, k_scale, weights, B, S1, S2, H, D, actual_q_len, actual_k_len,
                                  block_table, block_size, max_blocks, sparse_mode, sparse_count, out_idx, out_val,
                                  workspace, workspace_bytes, stream);
-  return ok(dsa::launch_indexer_topk_fused(kind, q, k, k_scale, weights, B, S1, S2, H, D, actual_q_len, actual_k_len,
-                                           block_table, block_size, max_blocks, sparse_mode, sparse_count, out_idx,
-                                           out_val, workspace, static_cast<hipStream_t>(stream)));
+  return ok(dsa::launch_indexer_topk_fused(kind, q, k, k_scale, weights, B * S1, B, S1, S2, H, D, actual_q_len,
+                                           actual_k_len, nullptr, nullptr, block_table, block_size, max_blocks,
+                                           sparse_mode, sparse_count, out_idx, out_val, workspace,
+                                           static_cast<hipStream_t>(stream)));
 }
 
 int dsa_lightning_indexer_fused_fallback_rows(const void* workspace, int64_t B, int64_t S1, int64_t S2,
@@ -202,7 +204,7 @@ int dsa_lightning_indexer_fused_fallback_rows(const void* workspace, int64_t B, 
   if (!dsa_lightning_indexer_fused_applies(B, S1, S2, sparse_count))
     return reject("indexer: the fused path does not apply to this shape");
   if (!workspace || !count) return reject("indexer: null pointer");
-  return ok(dsa::launch_fused_fallback_rows(workspace, B, S1, S2, sparse_count, count,
+  return ok(dsa::launch_fused_fallback_rows(workspace, B * S1, B, S1, S2, sparse_count, count,
                                             static_cast<hipStream_t>(stream)));
 }
 
@@ -266,6 +268,38 @@ int dsa_lightning_indexer_tnd(int kind, const void* q, const void* k, const floa
                    ? static_cast<void*>(static_cast<uint8_t*>(workspace) + indexer_logits_bytes(1, T, S2_max))
                    : nullptr;
   return ok(dsa::launch_topk(logits, ld, T, S2_max, sparse_count, nullptr, 1, out_idx, out_val, cand, st));
+}
+
+size_t dsa_lightning_indexer_tnd_fused_workspace_size(int64_t B, int64_t T, int64_t S1_max, int64_t S2_max,
+                                                      int64_t sparse_count) {
+  if (B <= 0 || T <= 0 || S1_max <= 0 || S2_max <= 0) return 0;
+  const int64_t k = sparse_count < 1 ? 1 : sparse_count;
+  const size_t fused = dsa::indexer_topk_fused_bytes(T, B, S1_max, S2_max, k);
+  return fused ? fused : dsa_lightning_indexer_tnd_workspace_size(T, S2_max, sparse_count);
+}
+
+int dsa_lightning_indexer_tnd_fused(int kind, const void* q, const void* k, const float* k_scale,
+                                    const float* weights, int64_t B, int64_t T, int64_t S1_max, int64_t S2_max,
+                                    int64_t H, int64_t D, const int32_t* cu_q, const int32_t* cu_k,
+                                    const int32_t* actual_k_len, const int32_t* block_table, int64_t block_size,
+                                    int64_t max_blocks, int sparse_mode, int64_t sparse_count, int32_t* out_idx,
+                                    float* out_val, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_indexer_tnd(kind, q, k, weights, B, T, S1_max, S2_max, H, D, cu_q, cu_k, actual_k_len, block_table,
+                             block_size, max_blocks, sparse_mode);
+  if (rc) return rc;
+  if (sparse_count < 1 || sparse_count > 8192) return reject("indexer: sparse_count must be in [1, 8192]");
+  if (workspace_bytes < dsa_lightning_indexer_tnd_fused_workspace_size(B, T, S1_max, S2_max, sparse_count))
+    return reject("indexer: workspace too small");
+  if (T > 0 && !out_idx) return reject("indexer: null out_idx");
+  if (T == 0 || S2_max == 0 || B == 0) return 0;
+  if (dsa::indexer_topk_fused_bytes(T, B, S1_max, S2_max, sparse_count) == 0)
+    return dsa_lightning_indexer_tnd(kind, q, k, k_scale, weights, B, T, S1_max, S2_max, H, D, cu_q, cu_k,
+                                     actual_k_len, block_table, block_size, max_blocks, sparse_mode, sparse_count,
+                                     out_idx, out_val, workspace, workspace_bytes, stream);
+  return ok(dsa::launch_indexer_topk_fused(kind, q, k, k_scale, weights, T, B, S1_max, S2_max, H, D, nullptr,
+                                           actual_k_len, cu_q, cu_k, block_table, block_size, max_blocks,
+                                           sparse_mode, sparse_count, out_idx, out_val, workspace,
+                                           static_cast<hipStream_t>(stream)));
 }
 
 size_t dsa_sparse_mla_workspace_size(int64_t B, int64_t S, int64_t H, int64_t topk) {

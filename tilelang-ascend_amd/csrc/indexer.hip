@@ -697,9 +697,10 @@ struct FusedPlan {
 
 static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
-static FusedPlan fused_plan(int64_t B, int64_t S1, int64_t S2, int64_t k) {
+// rows: B * S1 (padded queries) or T (packed queries, S1 = the longest batch).
+static FusedPlan fused_plan(int64_t rows, int64_t B, int64_t S1, int64_t S2, int64_t k) {
   FusedPlan p = {};
-  p.rows = B * S1;
+  p.rows = rows;
   p.ld = (S2 + 3) & ~int64_t(3);
   // At most kFusedMaxSeg key chunks (candidate slots) per row.
   const int64_t min_chunk = ((S2 + kFusedMaxSeg - 1) / kFusedMaxSeg + kIdxKeyTile - 1) / kIdxKeyTile * kIdxKeyTile;
@@ -733,8 +734,8 @@ static FusedPlan fused_plan(int64_t B, int64_t S1, int64_t S2, int64_t k) {
 }
 
 // 0 when the fused path does not apply to this shape (the caller runs the dense path).
-size_t indexer_topk_fused_bytes(int64_t B, int64_t S1, int64_t S2, int64_t k) {
-  const FusedPlan p = fused_plan(B, S1, S2, k);
+size_t indexer_topk_fused_bytes(int64_t rows, int64_t B, int64_t S1, int64_t S2, int64_t k) {
+  const FusedPlan p = fused_plan(rows, B, S1, S2, k);
   return p.fused ? p.total : 0;
 }
 
@@ -797,26 +798,27 @@ __global__ __launch_bounds__(256) void fused_count_flagged_kernel(const int32_t*
 
 // Rows of the last fused call on `workspace` that went back to the dense logits because
 // the sampled threshold was too high or a key chunk overflowed (one int, written on `stream`).
-hipError_t launch_fused_fallback_rows(const void* workspace, int64_t B, int64_t S1, int64_t S2, int64_t k,
-                                      int32_t* count, hipStream_t stream) {
-  const FusedPlan p = fused_plan(B, S1, S2, k);
+hipError_t launch_fused_fallback_rows(const void* workspace, int64_t rows, int64_t B, int64_t S1, int64_t S2,
+                                      int64_t k, int32_t* count, hipStream_t stream) {
+  const FusedPlan p = fused_plan(rows, B, S1, S2, k);
   if (!p.fused) return hipErrorInvalidValue;
   const int32_t* pidx = reinterpret_cast<const int32_t*>(static_cast<const uint8_t*>(workspace) + p.pidx);
   hipLaunchKernelGGL(fused_count_flagged_kernel, dim3(1), dim3(256), 0, stream, pidx, p.rows, p.ldc, count);
   return hipGetLastError();
 }
 
-// Caller validated as for launch_indexer_logits (BSND rows, optional paging), plus 1 <= k <= 8192
-// and a workspace of dsa_lightning_indexer_workspace_size + indexer_topk_fused_bytes bytes.
+// Caller validated as for launch_indexer_logits (padded or packed rows, optional paging), plus
+// 1 <= k <= 8192 and a workspace of indexer_topk_fused_bytes bytes.  rows: B * S1, or T with cu_q.
 hipError_t launch_indexer_topk_fused(int kind, const void* q, const void* k, const float* k_scale, const float* w,
-                                     int64_t B, int64_t S1, int64_t S2, int64_t H, int64_t D,
-                                     const int32_t* aq_len, const int32_t* ak_len, const int32_t* block_table,
-                                     int64_t block_size, int64_t max_blocks, int sparse_mode, int64_t topk,
-                                     int32_t* out_idx, float* out_val, void* workspace, hipStream_t stream) {
-  const FusedPlan p = fused_plan(B, S1, S2, topk);
+                                     int64_t rows, int64_t B, int64_t S1, int64_t S2, int64_t H, int64_t D,
+                                     const int32_t* aq_len, const int32_t* ak_len, const int32_t* cu_q,
+                                     const int32_t* cu_k, const int32_t* block_table, int64_t block_size,
+                                     int64_t max_blocks, int sparse_mode, int64_t topk, int32_t* out_idx,
+                                     float* out_val, void* workspace, hipStream_t stream) {
+  const FusedPlan p = fused_plan(rows, B, S1, S2, topk);
   if (!p.fused || B == 0 || S1 == 0) return hipErrorInvalidValue;
   uint8_t* ws = static_cast<uint8_t*>(workspace);
-  IdxArgs a = make_idx_args(q, k, k_scale, w, S1, S2, H, aq_len, ak_len, nullptr, nullptr, block_table, block_size,
+  IdxArgs a = make_idx_args(q, k, k_scale, w, S1, S2, H, aq_len, ak_len, cu_q, cu_k, block_table, block_size,
                             max_blocks, sparse_mode);
   a.sample = reinterpret_cast<float*>(ws + p.sample);
   a.sample_ld = p.sample_ld;

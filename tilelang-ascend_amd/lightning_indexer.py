@@ -242,7 +242,7 @@ def lightning_indexer(query: torch.Tensor, key: torch.Tensor, weights: torch.Ten
     (T on the empty early exit, lightning_indexer.py:1289-1296).  ``values`` is
     [B, S1, 1, K] (query dtype; fp32 for fp8 inputs) when ``return_value``, else
     an empty tensor.  Ascend tuning knobs (``block_n``, ``pp_slots``,
-    ``max_cores``) are accepted and ignored.  ``fuse_topk`` (BSND queries) streams
+    ``max_cores``) are accepted and ignored.  ``fuse_topk`` streams
     the top-k out of the indexer without writing every row's logits, where the
     shape allows (``dsa_lightning_indexer_fused``); the output is the same bit for
     bit.  The default (None) streams rows longer than 32768 keys, where it is faster.
@@ -261,7 +261,7 @@ def lightning_indexer(query: torch.Tensor, key: torch.Tensor, weights: torch.Ten
     if layout_query == "TND":
         return _lightning_indexer_tnd(query, key, weights, key_scale, actual_seq_lengths_query,
                                       actual_seq_lengths_key, block_table, layout_key, sparse_count, sparse_mode,
-                                      return_value, query_scale)
+                                      return_value, query_scale, fuse_topk)
     dev, B, S1, S2, N1, D, w, ks, aq, ak, bt, bs, mb = _prepare(
         query, key, weights, key_scale, actual_seq_lengths_query, actual_seq_lengths_key, block_table,
         layout_query, layout_key, sparse_mode, query_scale)
@@ -290,7 +290,8 @@ def lightning_indexer(query: torch.Tensor, key: torch.Tensor, weights: torch.Ten
 
 
 def _lightning_indexer_tnd(query, key, weights, key_scale, actual_seq_lengths_query, actual_seq_lengths_key,
-                           block_table, layout_key, sparse_count, sparse_mode, return_value, query_scale=None):
+                           block_table, layout_key, sparse_count, sparse_mode, return_value, query_scale=None,
+                           fuse_topk=None):
     _check_common(query, key, weights, "TND", layout_key, sparse_mode)
     (dev, B, T, T_rows, S1, S2, N1, D, w, ks, cu_q, cu_k, ak, bt, bs,
      mb) = _prepare_tnd(query, key, weights, key_scale, actual_seq_lengths_query, actual_seq_lengths_key,
@@ -304,13 +305,20 @@ def _lightning_indexer_tnd(query, key, weights, key_scale, actual_seq_lengths_qu
     idx = torch.empty((T_rows, 1, sparse_count), dtype=torch.int32, device=dev)
     val = torch.empty((T_rows, 1, sparse_count), dtype=torch.float32, device=dev) if return_value else None
     lib = _lib.load_library()
-    ws_bytes = lib.dsa_lightning_indexer_tnd_workspace_size(T_rows, S2, sparse_count)
+    if fuse_topk is None:
+        fuse_topk = S2 > 32768
+    if fuse_topk:
+        name = "dsa_lightning_indexer_tnd_fused"
+        ws_bytes = lib.dsa_lightning_indexer_tnd_fused_workspace_size(B, T_rows, S1, S2, sparse_count)
+    else:
+        name = "dsa_lightning_indexer_tnd"
+        ws_bytes = lib.dsa_lightning_indexer_tnd_workspace_size(T_rows, S2, sparse_count)
     ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
-    rc = lib.dsa_lightning_indexer_tnd(_KINDS[query.dtype], _lib.ptr(query), _lib.ptr(key), _lib.ptr(ks),
-                                       _lib.ptr(w), B, T_rows, S1, S2, N1, D, _lib.ptr(cu_q), _lib.ptr(cu_k),
-                                       _lib.ptr(ak), _lib.ptr(bt), bs, mb, sparse_mode, sparse_count, _lib.ptr(idx),
-                                       _lib.ptr(val), _lib.ptr(ws), ws_bytes, _lib.stream_handle(dev))
-    _lib.check(rc, "dsa_lightning_indexer_tnd")
+    rc = getattr(lib, name)(_KINDS[query.dtype], _lib.ptr(query), _lib.ptr(key), _lib.ptr(ks),
+                            _lib.ptr(w), B, T_rows, S1, S2, N1, D, _lib.ptr(cu_q), _lib.ptr(cu_k),
+                            _lib.ptr(ak), _lib.ptr(bt), bs, mb, sparse_mode, sparse_count, _lib.ptr(idx),
+                            _lib.ptr(val), _lib.ptr(ws), ws_bytes, _lib.stream_handle(dev))
+    _lib.check(rc, name)
     if return_value:
         return idx, val.to(vdt)
     return idx, torch.empty((0,), dtype=vdt, device=dev)
