@@ -152,3 +152,14 @@ def test_sparse_attn_tilelang_bench_sfa(dsa, dev, KV_S, T, sparse_mode):
     want, _ = ref.sparse_mla_fwd(q, kv, ind.view(1, T, 1, -1), 0.5, block_table=bt, actual_seq_lengths_query=[T],
                                  actual_seq_lengths_kv=[act_kv_s], is_causal=sparse_mode == 3)
     torch.testing.assert_close(out.cpu().float(), want[0], rtol=2e-2, atol=2e-2)
+
+
+def test_torch_op_equals_wrapper(dsa, dev):
+    """torch.ops.dsa.sparse_attn gives the wrapper's output and the C entry's LSE."""
+    q, kv, sink, idx = _inputs(1, 32, 256, 64, 512, 128, torch.bfloat16, 48)
+    ops = dsa.load_torch_ops()
+    o, l = ops.sparse_attn(q.to(dev), kv.to(dev), sink.to(dev), idx.to(dev), 512 ** -0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(o.cpu(), _run(dsa, dev, q, kv, sink, idx, 512 ** -0.5))
+    assert torch.equal(l.cpu(), _lse(dsa, dev, q, kv, sink, idx, 512 ** -0.5))
+

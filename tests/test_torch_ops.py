@@ -5,7 +5,8 @@ import torch
 
 def test_schemas_registered(dsa):
     ops = dsa.load_torch_ops()
-    for name in ("topk_select", "lightning_indexer", "sparse_mla_fwd", "sparse_flash_mla", "act_quant"):
+    for name in ("topk_select", "lightning_indexer", "sparse_mla_fwd", "sparse_flash_mla", "act_quant",
+                 "sparse_attn"):
         assert getattr(ops, name).default._schema.name == f"dsa::{name}"
 
 
@@ -32,3 +33,7 @@ def test_meta_shapes(dsa):
     assert y.shape == (3, 5, 128) and y.dtype == torch.float8_e4m3fn and s.shape == (3, 5, 1)
     y, s = ops.act_quant(torch.empty(4, 64, **m))
     assert y.dtype == torch.int8 and s.shape == (4, 1)
+    o, l = ops.sparse_attn(torch.empty(1, 6, 16, 512, dtype=torch.bfloat16, **m),
+                           torch.empty(1, 9, 512, dtype=torch.bfloat16, **m), torch.empty(16, **m),
+                           torch.empty(1, 6, 4, dtype=torch.int32, **m), 0.04)
+    assert o.shape == (1, 6, 16, 512) and o.dtype == torch.float32 and l.shape == (1, 6, 16)

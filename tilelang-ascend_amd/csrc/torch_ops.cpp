@@ -236,6 +236,40 @@ std::tuple<at::Tensor, at::Tensor> act_quant_meta(const at::Tensor& x, bool, c10
   return {at::empty(x.sizes(), x.options().dtype(dtype)), at::empty(sizes, x.options().dtype(at::kFloat))};
 }
 
+// V4 gathered-index attention with sinks (examples/deepseek_v4/sparse_attention.py:171-198):
+// q [b, m, h, 512], kv [b, n, 512], attn_sink [h] fp32, topk_idxs [b, m, topk] -> (out fp32, lse fp32).
+std::tuple<at::Tensor, at::Tensor> sparse_attn(const at::Tensor& q, const at::Tensor& kv,
+                                               const c10::optional<at::Tensor>& attn_sink, const at::Tensor& topk_idxs,
+                                               double softmax_scale) {
+  require(q, "q");
+  require(kv, "kv");
+  TORCH_CHECK(q.dim() == 4 && kv.dim() == 3 && topk_idxs.dim() == 3, "dsa.sparse_attn: q [b,m,h,d], kv [b,n,d], "
+              "topk_idxs [b,m,topk]");
+  TORCH_CHECK(kv.scalar_type() == q.scalar_type(), "dsa.sparse_attn: kv dtype must equal q dtype");
+  c10::OptionalDeviceGuard guard(q.device());
+  const int64_t B = q.size(0), M = q.size(1), H = q.size(2), D = q.size(3), N = kv.size(1), K = topk_idxs.size(2);
+  auto idx = topk_idxs.to(at::kInt).contiguous();
+  c10::optional<at::Tensor> sk;
+  if (attn_sink.has_value()) sk = attn_sink->to(at::kFloat).contiguous();
+  auto out = at::empty({B, M, H, D}, q.options());
+  auto lse = at::empty({B, M, H}, q.options().dtype(at::kFloat));
+  if (B * M > 0) {
+    const size_t ws_bytes = dsa_sparse_attn_sink_workspace_size(B, M, H, K);
+    auto ws = at::empty({(int64_t)(ws_bytes > 0 ? ws_bytes : 1)}, q.options().dtype(at::kByte));
+    check_rc(dsa_sparse_attn_sink(kind_of(q), ptr(q), ptr(kv), static_cast<int32_t*>(ptr(idx)), B, M, H, N, D, K,
+                                  ptr_or_null<float>(sk), (float)softmax_scale, ptr(out),
+                                  static_cast<float*>(ptr(lse)), ptr(ws), ws_bytes, stream_of(q)),
+             "sparse_attn");
+  }
+  return {out.to(at::kFloat), lse};
+}
+
+std::tuple<at::Tensor, at::Tensor> sparse_attn_meta(const at::Tensor& q, const at::Tensor&,
+                                                    const c10::optional<at::Tensor>&, const at::Tensor&, double) {
+  return {at::empty(q.sizes(), q.options().dtype(at::kFloat)),
+          at::empty({q.size(0), q.size(1), q.size(2)}, q.options().dtype(at::kFloat))};
+}
+
 }  // namespace
 
 TORCH_LIBRARY(dsa, m) {
@@ -253,6 +287,7 @@ TORCH_LIBRARY(dsa, m) {
       "Tensor seqused_kv, Tensor? sinks, float softmax_scale, Tensor? cmp_kv=None, Tensor? cmp_block_table=None, "
       "Tensor? cmp_sparse_indices=None, int cmp_ratio=4, int ori_win_left=127, int max_cmp=0) -> (Tensor, Tensor)");
   m.def("act_quant(Tensor x, bool round_scale=False, ScalarType? dtype=None) -> (Tensor, Tensor)");
+  m.def("sparse_attn(Tensor q, Tensor kv, Tensor? attn_sink, Tensor topk_idxs, float softmax_scale) -> (Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(dsa, CUDA, m) {
@@ -261,6 +296,7 @@ TORCH_LIBRARY_IMPL(dsa, CUDA, m) {
   m.impl("sparse_mla_fwd", &sparse_mla_fwd);
   m.impl("sparse_flash_mla", &sparse_flash_mla);
   m.impl("act_quant", &act_quant);
+  m.impl("sparse_attn", &sparse_attn);
 }
 
 TORCH_LIBRARY_IMPL(dsa, Meta, m) {
@@ -269,4 +305,5 @@ TORCH_LIBRARY_IMPL(dsa, Meta, m) {
   m.impl("sparse_mla_fwd", &sparse_mla_fwd_meta);
   m.impl("sparse_flash_mla", &sparse_flash_mla_meta);
   m.impl("act_quant", &act_quant_meta);
+  m.impl("sparse_attn", &sparse_attn_meta);
 }
