@@ -165,7 +165,8 @@ struct IdxArgs {
   int tile_stride;          // keys between consecutive tiles: 64, or 64 * F in the sample pass
   float* sample;            // [rows, sample_ld]: logits of the first 64 keys of every 64 * F
   int64_t sample_ld;
-  float* thr;               // [rows]: written by the sample pass; the filter pass keeps keys with logit >= thr
+  int32_t* row_valid;       // [rows]: valid keys per row (the sample pass, when it has several key chunks)
+  float* thr;               // [rows]: filter thresholds; the filter pass keeps keys with logit >= thr
   int topk;
   float* cand_val;          // [rows, nseg, cand_cap]: kept logits per (row, key chunk), in key order
   int32_t* cand_idx;        // [rows, nseg, cand_cap]: their key positions
@@ -199,6 +200,9 @@ __device__ __forceinline__ float row_threshold(const float* __restrict__ sr, int
     const uint32_t kk = float_key(x[i]);
     const bool ok = lane + i * kWave < m && kk > kKeyInvalidMax;  // absent: past m, NaN, <= -1e30
     key[i] = ok ? kk : 0u;
+    // Opaque from here on: otherwise the select is folded into every comparison
+    // below (a mask AND, a v_cndmask and a re-compare per element and step).
+    __asm__ volatile("" : "+v"(key[i]));
     present += (int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(ok));
   }
   if (nv <= k || present == 0) return -__builtin_huge_valf();
@@ -534,10 +538,12 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
       if (t < t_rows) {
         float* row = a.sample + (q_base + t) * a.sample_ld;
         for (int c = slot0 + ntiles * kIdxKeyTile + lane; c < slot1; c += kWave) row[c] = -__builtin_huge_valf();
+        if (gridDim.x > 1 && blockIdx.x == 0 && lane == 0) a.row_valid[q_base + t] = nvalid[j];
       }
     }
     // With one key chunk this workgroup wrote its rows' whole sample: each wave
     // turns its own rows into thresholds (the barrier makes the stores visible).
+    // With several, fused_threshold_kernel does it afterwards.
     if (gridDim.x == 1) {
       __syncthreads();
 #pragma unroll
@@ -663,8 +669,8 @@ hipError_t launch_indexer_logits(int kind, const void* q, const void* k, const f
 // Fused indexer -> top-k.  The logits of a row are never written whole:
 //   1. sample pass: the logits of the first 64 keys of every 64 F (about 2048
 //      keys per row);
-//   2. per row, at the end of the sample pass: thr = the r-th largest valid
-//      sampled logit, r = mu + 4 sqrt(mu) + 2 with mu = k * sampled / valid the
+//   2. per row (at the end of the sample pass, or in a kernel of its own when
+//      the sample spans several key chunks): thr = the r-th largest valid sampled logit, r = mu + 4 sqrt(mu) + 2 with mu = k * sampled / valid the
 //      expected number of sampled keys in the row's top k (thr = -inf when the
 //      row has at most k valid keys);
 //   3. filter pass: the indexer again, keeping (logit, key) for logit >= thr,
@@ -686,13 +692,14 @@ hipError_t launch_topk_flagged(const float* x, int64_t ld, int64_t rows, int64_t
 
 constexpr int kFusedSampleTiles = 32;  // ~2048 sampled keys per row
 constexpr int kFusedMaxSeg = 8;
+constexpr int kFusedSampleChunkTiles = 8;  // sampled tiles per workgroup of the sample pass
 
 struct FusedPlan {
   bool fused;
   int64_t rows, ld, sample_ld, ldc;
   int64_t key_chunk, tile_stride;
   int nseg, cap;
-  size_t dense, sample, thr, cval, cidx, ccnt, pval, pidx, plen, total;
+  size_t dense, sample, thr, valid, cval, cidx, ccnt, pval, pidx, plen, total;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
@@ -722,6 +729,7 @@ static FusedPlan fused_plan(int64_t rows, int64_t B, int64_t S1, int64_t S2, int
     const size_t R = (size_t)p.rows;
     p.sample = off; off = align256(off + R * p.sample_ld * 4);
     p.thr = off; off = align256(off + R * 4);
+    p.valid = off; off = align256(off + R * 4);
     p.cval = off; off = align256(off + R * p.nseg * p.cap * 4);
     p.cidx = off; off = align256(off + R * p.nseg * p.cap * 4);
     p.ccnt = off; off = align256(off + R * p.nseg * 4);
@@ -737,6 +745,19 @@ static FusedPlan fused_plan(int64_t rows, int64_t B, int64_t S1, int64_t S2, int
 size_t indexer_topk_fused_bytes(int64_t rows, int64_t B, int64_t S1, int64_t S2, int64_t k) {
   const FusedPlan p = fused_plan(rows, B, S1, S2, k);
   return p.fused ? p.total : 0;
+}
+
+// Thresholds after a sample pass of several key chunks: one wave per row.
+__global__ __launch_bounds__(256) void fused_threshold_kernel(const float* __restrict__ sample, int64_t sld,
+                                                              const int32_t* __restrict__ row_valid, int64_t rows,
+                                                              int k, float* __restrict__ thr) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = (int64_t)blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
+  if (row >= rows) return;
+  const float* sr = sample + row * sld;
+  const float t = sld <= 32 * kWave ? row_threshold<32>(sr, (int)sld, row_valid[row], k, lane)
+                                    : row_threshold<64>(sr, (int)sld, row_valid[row], k, lane);
+  if (lane == 0) thr[row] = t;
 }
 
 __global__ __launch_bounds__(256) void fused_pack_kernel(const float* __restrict__ cval, const int32_t* __restrict__ cidx,
@@ -828,12 +849,18 @@ hipError_t launch_indexer_topk_fused(int kind, const void* q, const void* k, con
   a.cand_idx = reinterpret_cast<int32_t*>(ws + p.cidx);
   a.cand_cnt = reinterpret_cast<int32_t*>(ws + p.ccnt);
   a.cand_cap = p.cap;
-  // 1-2. Sample pass and thresholds: one key chunk per row group (so each
-  // workgroup holds its rows' whole sample), tiles tile_stride apart.
+  // 1-2. Sample pass (tiles tile_stride apart, kFusedSampleChunkTiles per workgroup) and
+  // thresholds: in the sample pass itself when one key chunk holds the whole sample.
   a.tile_stride = (int)p.tile_stride;
-  a.key_chunk = (int)((S2 + p.tile_stride - 1) / p.tile_stride * p.tile_stride);
+  a.row_valid = reinterpret_cast<int32_t*>(ws + p.valid);
+  a.key_chunk = (int)(p.tile_stride * kFusedSampleChunkTiles);
   hipError_t e = launch_indexer_mode<kModeSample>(kind, D, a, B, stream);
   if (e != hipSuccess) return e;
+  if ((S2 + a.key_chunk - 1) / a.key_chunk > 1) {
+    hipLaunchKernelGGL(fused_threshold_kernel, dim3((unsigned)((p.rows + 3) / 4)), dim3(256), 0, stream, a.sample,
+                       p.sample_ld, a.row_valid, p.rows, (int)topk, a.thr);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
   // 3. Filter pass over the usual key chunks (one candidate slot per chunk).
   a.tile_stride = kIdxKeyTile;
   a.key_chunk = (int)p.key_chunk;
