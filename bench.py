@@ -547,6 +547,20 @@ def summarize_traffic(fetch_db, write_db, cal_fetch_db, cal_write_db):
         print(f"{key[0]:42s} {key[1]:9d} {fetch[key]:14.1f} {write[key]:14.1f}  {tb:.4e}")
 
 
+def summarize_mfma(util_db, mops_db):
+    """MFMA evidence per dsa kernel: rocprofv3's MfmaUtil (MFMA-busy cycles over all SIMDs' active
+    cycles, percent) and the FLOPs the hardware counted (SQ_INSTS_VALU_MFMA_MOPS_* x 512) per dispatch."""
+    util = _counter_means(util_db, "MfmaUtil")
+    mops = {cn: _counter_means(mops_db, cn) for cn in ("SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_INSTS_VALU_MFMA_MOPS_F8",
+                                                       "SQ_INSTS_VALU_MFMA_MOPS_F16")}
+    print(f"{'kernel':48s} {'grid':>9s} {'MfmaUtil_%':>10s} {'bf16_FLOP':>11s} {'fp8_FLOP':>11s} {'f16_FLOP':>11s}")
+    for key in sorted(util):
+        if not key[0].startswith("dsa::"):
+            continue
+        f = [mops[cn].get(key, 0.0) * 512.0 for cn in mops]
+        print(f"{key[0]:48s} {key[1]:9d} {util[key]:10.1f} {f[0]:11.4e} {f[1]:11.4e} {f[2]:11.4e}")
+
+
 def profiled_traffic(kernel, grid):
     """HBM bytes per launch of (kernel, grid) from the committed counter summary, or None if it has none."""
     path = PROFILES / "traffic_fetch_write_bench.txt"
@@ -560,10 +574,12 @@ def profiled_traffic(kernel, grid):
 
 
 def main():
-    if len(sys.argv) > 1 and sys.argv[1] in ("--rocprof-trace", "--rocprof-traffic"):
+    if len(sys.argv) > 1 and sys.argv[1] in ("--rocprof-trace", "--rocprof-traffic", "--rocprof-mfma"):
         # Summaries of rocprofv3 databases written by profiling this script (no GPU needed).
         if sys.argv[1] == "--rocprof-trace":
             summarize_trace(sys.argv[2])
+        elif sys.argv[1] == "--rocprof-mfma":
+            summarize_mfma(*sys.argv[2:4])
         else:
             summarize_traffic(*sys.argv[2:6])
         return
