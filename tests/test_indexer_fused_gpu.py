@@ -198,9 +198,9 @@ def test_fused_tied_candidates_resolved_on_packed_rows(dsa, dev):
 
 
 def test_fused_default_torch_op_and_graph_capture(dsa, dev):
-    """Rows over 32768 keys take the fused path by default, in the wrapper and in
+    """2048 rows over 32768 keys take the fused path by default, in the wrapper and in
     torch.ops.dsa.lightning_indexer; the op captured in a HIP graph replays to the same output."""
-    B, S1, S2, H, D, K = 1, 32, 65536, 64, 128, 2048
+    B, S1, S2, H, D, K = 1, 2048, 40960, 64, 128, 2048
     print("fused indexer default path + graph", flush=True)
     q, k, w, ks = _inputs(B, S1, S2, H, D, torch.float8_e4m3fn, 40)
     qd, kd, wd, ksd = q.to(dev), k.unsqueeze(2).to(dev), w.to(dev), ks.to(dev)

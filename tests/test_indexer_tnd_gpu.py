@@ -223,7 +223,7 @@ def test_tnd_fused_topk_equals_dense(dsa, dev):
     di, dv = dsa.lightning_indexer(qd, kd, wd, key_scale=ksd, actual_seq_lengths_key=ckd, layout_key="TND",
                                    return_value=True, fuse_topk=False, **kw)
     fi, fv = dsa.lightning_indexer(qd, kd, wd, key_scale=ksd, actual_seq_lengths_key=ckd, layout_key="TND",
-                                   return_value=True, **kw)  # default: fused for rows over 32768 keys
+                                   return_value=True, fuse_topk=True, **kw)
     torch.cuda.synchronize()
     assert torch.equal(fi, di) and torch.equal(fv, dv)
     kp, _ = ref.tnd_to_padded(k.view(torch.uint8), cu_k.tolist())

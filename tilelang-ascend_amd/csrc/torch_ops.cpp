@@ -100,8 +100,8 @@ std::tuple<at::Tensor, at::Tensor> lightning_indexer(const at::Tensor& query, co
   auto val = return_value ? at::empty({B, S1, 1, sparse_count}, query.options().dtype(at::kFloat))
                           : at::empty({0}, query.options().dtype(at::kFloat));
   if (B * S1 == 0) return {idx, val};
-  // Rows past 32768 keys stream the top-k out of the indexer (same output, no full logits).
-  const bool fused = S2 > 32768;
+  // At least 2048 rows past 32768 keys stream the top-k out of the indexer (same output, no full logits).
+  const bool fused = S2 > 32768 && B * S1 >= 2048;
   const size_t ws_bytes = fused ? dsa_lightning_indexer_fused_workspace_size(B, S1, S2, sparse_count)
                                 : dsa_lightning_indexer_workspace_size(B, S1, S2, sparse_count);
   auto ws = at::empty({(int64_t)(ws_bytes > 0 ? ws_bytes : 1)}, query.options().dtype(at::kByte));

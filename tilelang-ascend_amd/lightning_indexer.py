@@ -245,7 +245,8 @@ def lightning_indexer(query: torch.Tensor, key: torch.Tensor, weights: torch.Ten
     ``max_cores``) are accepted and ignored.  ``fuse_topk`` streams
     the top-k out of the indexer without writing every row's logits, where the
     shape allows (``dsa_lightning_indexer_fused``); the output is the same bit for
-    bit.  The default (None) streams rows longer than 32768 keys, where it is faster.
+    bit.  The default (None) streams calls of at least 2048 rows longer than 32768 keys, where it
+    is faster.
     """
     unknown = set(tuning) - {"block_n", "pp_slots", "max_cores"}
     if unknown:
@@ -275,7 +276,7 @@ def lightning_indexer(query: torch.Tensor, key: torch.Tensor, weights: torch.Ten
     val = torch.empty((B, S1, 1, sparse_count), dtype=torch.float32, device=dev) if return_value else None
     lib = _lib.load_library()
     if fuse_topk is None:
-        fuse_topk = S2 > 32768
+        fuse_topk = _fuse_by_default(B * S1, S2)
     name = "dsa_lightning_indexer_fused" if fuse_topk else "dsa_lightning_indexer"
     ws_bytes = getattr(lib, name + "_workspace_size")(B, S1, S2, sparse_count)
     ws = torch.empty((ws_bytes,), dtype=torch.uint8, device=dev)
@@ -287,6 +288,12 @@ def lightning_indexer(query: torch.Tensor, key: torch.Tensor, weights: torch.Ten
     if return_value:
         return idx, val.to(vdt)
     return idx, torch.empty((0,), dtype=vdt, device=dev)
+
+
+def _fuse_by_default(rows: int, S2: int) -> bool:
+    """The streamed top-k pays off for long rows (over 32768 keys, where the dense top-k takes two
+    stages) when there are enough of them (2048) for its launch to keep the dense pass's key chunks."""
+    return S2 > 32768 and rows >= 2048
 
 
 def _lightning_indexer_tnd(query, key, weights, key_scale, actual_seq_lengths_query, actual_seq_lengths_key,
@@ -306,7 +313,7 @@ def _lightning_indexer_tnd(query, key, weights, key_scale, actual_seq_lengths_qu
     val = torch.empty((T_rows, 1, sparse_count), dtype=torch.float32, device=dev) if return_value else None
     lib = _lib.load_library()
     if fuse_topk is None:
-        fuse_topk = S2 > 32768
+        fuse_topk = _fuse_by_default(T_rows, S2)
     if fuse_topk:
         name = "dsa_lightning_indexer_tnd_fused"
         ws_bytes = lib.dsa_lightning_indexer_tnd_fused_workspace_size(B, T_rows, S1, S2, sparse_count)
