@@ -225,3 +225,26 @@ def test_fused_default_torch_op_and_graph_capture(dsa, dev):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(gi, di) and torch.equal(gv, dv)
+
+
+@pytest.mark.parametrize("case", range(6))
+def test_fused_random_shapes(dsa, dev, case):
+    """Seeded random shapes: batch 1-3, 8-160 query rows, 16384-70000 keys, k in {1, 77, 1000, 2048,
+    4096}, ragged lengths, causal or full, fp8 / bf16 / fp16, 16-64 heads; bit-equal to the dense path."""
+    g = torch.Generator().manual_seed(1000 + case)
+    r = lambda lo, hi: int(torch.randint(lo, hi + 1, (1,), generator=g))
+    B, S1 = r(1, 3), r(8, 160)
+    K = [1, 77, 1000, 2048, 4096][r(0, 4)]
+    S2 = max(r(16384, 70000), 8 * K)
+    H = [16, 32, 64][r(0, 2)]
+    dtype = [torch.float8_e4m3fn, torch.bfloat16, torch.float16][case % 3]
+    D = 128 if dtype == torch.float8_e4m3fn else 64
+    mode = [3, 0][r(0, 1)]
+    print(f"fused random case {case}: B={B} S1={S1} S2={S2} K={K} H={H} D={D} {dtype} mode={mode}", flush=True)
+    assert _applies(dsa, B, S1, S2, K)
+    q, k, w, ks = _inputs(B, S1, S2, H, D, dtype, 2000 + case)
+    aq = torch.tensor([r(1, S1) for _ in range(B)], dtype=torch.int32)
+    ak = torch.tensor([r(1, S2) for _ in range(B)], dtype=torch.int32)
+    (fi, fv), (di, dv) = _both(dsa, dev, q, k.unsqueeze(2), w, ks, K, sparse_mode=mode, return_value=True,
+                               actual_seq_lengths_query=aq.to(dev), actual_seq_lengths_key=ak.to(dev))
+    assert torch.equal(fi, di) and torch.equal(fv.float(), dv.float())
