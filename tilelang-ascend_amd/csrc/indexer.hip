@@ -168,8 +168,7 @@ struct IdxArgs {
   int32_t* row_valid;       // [rows]: valid keys per row (the sample pass, when it has several key chunks)
   float* thr;               // [rows]: filter thresholds; the filter pass keeps keys with logit >= thr
   int topk;
-  float* cand_val;          // [rows, nseg, cand_cap]: kept logits per (row, key chunk), in key order
-  int32_t* cand_idx;        // [rows, nseg, cand_cap]: their key positions
+  u32x2* cand;              // [rows, nseg, cand_cap]: (logit bits, key position) kept per (row, key chunk), in key order
   int32_t* cand_cnt;        // [rows, nseg]: keys kept (may exceed cand_cap: overflow)
   int cand_cap;
   const int32_t* flag_idx;  // dense pass: only workgroups with a row whose flag_idx[row * flag_ld] is kFallbackFlag
@@ -360,13 +359,15 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
   const int tile_end = min(key1, max_valid);  // keys at or past this are -inf for every token
   const int ntiles = tile_end > key0 ? (tile_end - key0 + tstride - 1) / tstride : 0;
 
-  // Filter mode: this wave's tokens' thresholds and kept counts.
+  // Filter mode: this wave's tokens' thresholds, kept counts and candidate slots.
   float thr[kTokPW];
   int kept[kTokPW];
+  u32x2* crow[kTokPW];
 #pragma unroll
   for (int j = 0; j < kTokPW; ++j) {
     const int t = t_base + wave * kTokPW + j;
     kept[j] = 0;
+    crow[j] = kMode == kModeFilter ? a.cand + ((q_base + t) * gridDim.x + blockIdx.x) * a.cand_cap : nullptr;
     // Raised to the float just above -1e30: v >= thr then also rejects masked keys
     // (-inf), scores the top-k never selects (<= -1e30) and NaN.
     thr[j] = (kMode == kModeFilter && t < t_rows) ? fmaxf(a.thr[q_base + t], __uint_as_float(0xF149F2C9u))
@@ -499,11 +500,7 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
         if (bal) {  // wave-uniform
           const int pos = kept[j] + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
                                                                    __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-          if (keep && pos < a.cand_cap) {
-            const int64_t o = ((q_base + t) * gridDim.x + blockIdx.x) * a.cand_cap + pos;
-            a.cand_val[o] = v;
-            a.cand_idx[o] = s;
-          }
+          if (keep && pos < a.cand_cap) crow[j][pos] = u32x2{__float_as_uint(v), (uint32_t)s};
           kept[j] += (int)__builtin_popcountll(bal);
         }
       }
@@ -699,7 +696,7 @@ struct FusedPlan {
   int64_t rows, ld, sample_ld, ldc;
   int64_t key_chunk, tile_stride;
   int nseg, cap;
-  size_t dense, sample, thr, valid, cval, cidx, ccnt, pval, pidx, plen, total;
+  size_t dense, sample, thr, valid, cval, ccnt, pval, pidx, plen, total;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
@@ -730,8 +727,7 @@ static FusedPlan fused_plan(int64_t rows, int64_t B, int64_t S1, int64_t S2, int
     p.sample = off; off = align256(off + R * p.sample_ld * 4);
     p.thr = off; off = align256(off + R * 4);
     p.valid = off; off = align256(off + R * 4);
-    p.cval = off; off = align256(off + R * p.nseg * p.cap * 4);
-    p.cidx = off; off = align256(off + R * p.nseg * p.cap * 4);
+    p.cval = off; off = align256(off + R * p.nseg * p.cap * 8);
     p.ccnt = off; off = align256(off + R * p.nseg * 4);
     p.pval = off; off = align256(off + R * p.ldc * 4);
     p.pidx = off; off = align256(off + R * p.ldc * 4);
@@ -760,7 +756,7 @@ __global__ __launch_bounds__(256) void fused_threshold_kernel(const float* __res
   if (lane == 0) thr[row] = t;
 }
 
-__global__ __launch_bounds__(256) void fused_pack_kernel(const float* __restrict__ cval, const int32_t* __restrict__ cidx,
+__global__ __launch_bounds__(256) void fused_pack_kernel(const u32x2* __restrict__ cand,
                                                          const int32_t* __restrict__ ccnt, int nseg, int cap,
                                                          const float* __restrict__ thr, int k, int ldc,
                                                          float* __restrict__ pval, int32_t* __restrict__ pidx,
@@ -796,8 +792,9 @@ __global__ __launch_bounds__(256) void fused_pack_kernel(const float* __restrict
     const int64_t src = (row * nseg + s) * cap;
     const int n = offs[s + 1] - offs[s];
     for (int i = tid; i < n; i += 256) {
-      pv[offs[s] + i] = cval[src + i];
-      pi[offs[s] + i] = cidx[src + i];
+      const u32x2 c = cand[src + i];
+      pv[offs[s] + i] = __uint_as_float(c.x);
+      pi[offs[s] + i] = (int32_t)c.y;
     }
   }
   // The register top-k reads pidx[j * k] as segment flags: no stale flag past the row.
@@ -845,8 +842,7 @@ hipError_t launch_indexer_topk_fused(int kind, const void* q, const void* k, con
   a.sample_ld = p.sample_ld;
   a.thr = reinterpret_cast<float*>(ws + p.thr);
   a.topk = (int)topk;
-  a.cand_val = reinterpret_cast<float*>(ws + p.cval);
-  a.cand_idx = reinterpret_cast<int32_t*>(ws + p.cidx);
+  a.cand = reinterpret_cast<u32x2*>(ws + p.cval);
   a.cand_cnt = reinterpret_cast<int32_t*>(ws + p.ccnt);
   a.cand_cap = p.cap;
   // 1-2. Sample pass (tiles tile_stride apart, kFusedSampleChunkTiles per workgroup) and
@@ -869,7 +865,7 @@ hipError_t launch_indexer_topk_fused(int kind, const void* q, const void* k, con
   float* pval = reinterpret_cast<float*>(ws + p.pval);
   int32_t* pidx = reinterpret_cast<int32_t*>(ws + p.pidx);
   int32_t* plen = reinterpret_cast<int32_t*>(ws + p.plen);
-  hipLaunchKernelGGL(fused_pack_kernel, dim3((unsigned)p.rows), dim3(256), 0, stream, a.cand_val, a.cand_idx,
+  hipLaunchKernelGGL(fused_pack_kernel, dim3((unsigned)p.rows), dim3(256), 0, stream, a.cand,
                      a.cand_cnt, p.nseg, p.cap, a.thr, (int)topk, (int)p.ldc, pval, pidx, plen);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   // 5. Top-k over the packed rows.
