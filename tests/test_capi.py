@@ -81,3 +81,48 @@ def test_python_layer_validation_messages(dsa):
         dsa.lightning_indexer(q, q.to(torch.bfloat16), torch.zeros(1, 2, 16))
     with pytest.raises(ValueError, match="non-casual|non-causal"):
         dsa.sparse_attention_fwd(128, 512, 64, 2048, is_causal=False)
+
+
+def test_fused_indexer_host_logic(dsa):
+    """When the fused indexer applies, its workspace, and its argument checks (host only)."""
+    lib = dsa.load_library()
+    # C2 and C5 rows apply; short rows, k > 4096 and S2 < 8k do not.
+    assert lib.dsa_lightning_indexer_fused_applies(1, 4096, 32768, 2048) == 1
+    assert lib.dsa_lightning_indexer_fused_applies(1, 4096, 131072, 2048) == 1
+    assert lib.dsa_lightning_indexer_fused_applies(32, 1, 131072, 2048) == 1
+    assert lib.dsa_lightning_indexer_fused_applies(1, 4096, 8192, 2048) == 0
+    assert lib.dsa_lightning_indexer_fused_applies(1, 4096, 131072, 8192) == 0
+    assert lib.dsa_lightning_indexer_fused_applies(1, 64, 20000, 4096) == 0
+    # The fused workspace holds the dense logits too; where the fused path does not apply the
+    # entry runs the dense path and asks for exactly its workspace.
+    dense = lib.dsa_lightning_indexer_workspace_size(1, 4096, 131072, 2048)
+    fused = lib.dsa_lightning_indexer_fused_workspace_size(1, 4096, 131072, 2048)
+    assert fused >= 4096 * 131072 * 4 and fused > 0 and dense > 0
+    assert (lib.dsa_lightning_indexer_fused_workspace_size(1, 16, 4096, 2048)
+            == lib.dsa_lightning_indexer_workspace_size(1, 16, 4096, 2048))
+    assert (lib.dsa_lightning_indexer_tnd_fused_workspace_size(2, 100, 80, 40000, 2048)
+            >= lib.dsa_lightning_indexer_tnd_workspace_size(100, 40000, 2048))
+    # Argument checks, before any launch.
+    assert lib.dsa_lightning_indexer_fused(0, 8, 8, None, 8, 1, 16, 32768, 64, 128, None, None, None, 0, 0, 3,
+                                           0, 8, None, 8, 1 << 40, None) == 1
+    assert b"sparse_count" in lib.dsa_last_error_message()
+    assert lib.dsa_lightning_indexer_fused(0, 8, 8, None, 8, 1, 16, 32768, 64, 128, None, None, None, 0, 0, 3,
+                                           2048, 8, None, 8, 16, None) == 1
+    assert b"workspace" in lib.dsa_last_error_message()
+    assert lib.dsa_lightning_indexer_tnd_fused(0, 8, 8, None, 8, 1, 16, 16, 32768, 64, 128, None, 8, None, None,
+                                               0, 0, 3, 2048, 8, None, 8, 1 << 40, None) == 1
+    assert b"cu_q" in lib.dsa_last_error_message()
+    assert lib.dsa_lightning_indexer_fused_fallback_rows(8, 1, 16, 4096, 2048, 8, None) == 1
+    assert b"does not apply" in lib.dsa_last_error_message()
+
+
+def test_sparse_attn_sink_host_checks(dsa):
+    lib = dsa.load_library()
+    args = lambda kind, H, D: (kind, 8, 8, 8, 1, 4, H, 16, D, 8, None, 0.1, 8, 8, 8, 1 << 30, None)
+    assert lib.dsa_sparse_attn_sink(*args(0, 64, 512)) == 1
+    assert b"kind" in lib.dsa_last_error_message()
+    assert lib.dsa_sparse_attn_sink(*args(1, 64, 576)) == 1
+    assert b"D must be 512" in lib.dsa_last_error_message()
+    assert lib.dsa_sparse_attn_sink(*args(1, 40, 512)) == 1
+    assert b"multiple of 16" in lib.dsa_last_error_message()
+    assert lib.dsa_sparse_attn_sink_workspace_size(1, 4, 64, 8) > 0
