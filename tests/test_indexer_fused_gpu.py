@@ -248,3 +248,45 @@ def test_fused_random_shapes(dsa, dev, case):
     (fi, fv), (di, dv) = _both(dsa, dev, q, k.unsqueeze(2), w, ks, K, sparse_mode=mode, return_value=True,
                                actual_seq_lengths_query=aq.to(dev), actual_seq_lengths_key=ak.to(dev))
     assert torch.equal(fi, di) and torch.equal(fv.float(), dv.float())
+
+
+def test_fused_fallback_under_graph_replay(dsa, dev):
+    """The fused entry captured in a HIP graph on inputs that send every row back to the dense path
+    (sampled keys scaled up), replayed with the outputs clobbered in between: every replay equals the
+    dense path, and no flag or packed length from one replay leaks into the next."""
+    B, S1, S2, H, D, K = 1, 64, 32768, 64, 128, 2048
+    print("fused indexer fallback under graph replay", flush=True)
+    q, k, w, ks = _inputs(B, S1, S2, H, D, torch.float8_e4m3fn, 41)
+    pos = torch.arange(S2)
+    ks = torch.where((pos % 1024) < 64, ks * 50, ks)
+    di, dv = dsa.lightning_indexer(q.to(dev), k.unsqueeze(2).to(dev), w.to(dev), key_scale=ks.to(dev),
+                                   sparse_count=K, return_value=True, fuse_topk=False)
+    lib = dsa.load_library()
+    qd, kd, wd, ksd = q.to(dev), k.contiguous().to(dev), w.float().to(dev), ks.float().to(dev)
+    idx = torch.empty((B, S1, K), dtype=torch.int32, device=dev)
+    val = torch.empty((B, S1, K), dtype=torch.float32, device=dev)
+    nb = lib.dsa_lightning_indexer_fused_workspace_size(B, S1, S2, K)
+    ws = torch.empty((nb,), dtype=torch.uint8, device=dev)
+
+    def call():
+        rc = lib.dsa_lightning_indexer_fused(0, qd.data_ptr(), kd.data_ptr(), ksd.data_ptr(), wd.data_ptr(), B, S1,
+                                             S2, H, D, None, None, None, 0, 0, 3, K, idx.data_ptr(), val.data_ptr(),
+                                             ws.data_ptr(), nb, torch.cuda.current_stream(dev).cuda_stream)
+        assert rc == 0
+
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        call()
+    torch.cuda.current_stream(dev).wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    for rep in range(3):
+        idx.fill_(5)
+        val.zero_()
+        ws.fill_(rep)  # stale flags, counts and thresholds everywhere in the workspace
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(idx.view(B, S1, 1, K), di) and torch.equal(val.view(B, S1, 1, K), dv)
