@@ -200,6 +200,43 @@ def run_step(torch, pkg, dev, args, S, H, topk, sm_scale):
     return result, (q, kv, idx)
 
 
+C5_SEED = 20261205
+
+
+def gen_c5_prefill(torch, dev, g, ctx=131072, chunk=4096, H=128, Hi=64, D=128):
+    """C5 prefill chunk (the last `chunk` of `ctx` positions): fp8 indexer q [1, chunk, Hi, D], keys
+    [1, ctx, D] fp8 with per-token scale absmax/448, weights N(0,1)/8; MLA q [1, chunk, H, 576] and
+    kv [1, ctx, 1, 576] bf16 ~ N(0,1)*0.5.  Draws from generator `g` in that order."""
+    qi = torch.randn(1, chunk, Hi, D, generator=g, device=dev).to(torch.float8_e4m3fn)
+    kf = torch.randn(1, ctx, D, generator=g, device=dev)
+    ks = (kf.abs().amax(dim=-1) / 448.0).to(torch.float32)
+    ki = (kf / ks.unsqueeze(-1)).clamp(-448, 448).to(torch.float8_e4m3fn).contiguous()
+    del kf
+    wi = torch.randn(1, chunk, Hi, generator=g, device=dev) / 8
+    q = (torch.randn(1, chunk, H, 576, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    kv = (torch.randn(1, ctx, 1, 576, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    return qi, ki, ks, wi, q, kv
+
+
+def gen_c5_decode(torch, dev, g, ctx=131072, dec_b=32, H=128, Hi=64, D=128, bs=64):
+    """C5 decode step: `dec_b` sequences x 1 query over `ctx` keys each, paged in `bs`-token blocks
+    behind one seeded random block table shared by the fp8 index keys and the bf16 latent KV pool.
+    Draws from generator `g` (after gen_c5_prefill in the benchmark)."""
+    nblk = ctx // bs
+    qd = torch.randn(dec_b, 1, Hi, D, generator=g, device=dev).to(torch.float8_e4m3fn)
+    kdf = torch.randn(dec_b * nblk, bs, D, generator=g, device=dev)
+    kds = (kdf.abs().amax(dim=-1) / 448.0).to(torch.float32)
+    kd = (kdf / kds.unsqueeze(-1)).clamp(-448, 448).to(torch.float8_e4m3fn).contiguous()
+    del kdf
+    wd = torch.randn(dec_b, 1, Hi, generator=g, device=dev) / 8
+    table = torch.randperm(dec_b * nblk, generator=g, device=dev).view(dec_b, nblk).to(torch.int32)
+    lens_q = torch.ones(dec_b, dtype=torch.int32, device=dev)
+    lens_k = torch.full((dec_b,), ctx, dtype=torch.int32, device=dev)
+    qm = (torch.randn(dec_b, 1, H, 576, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    pool = (torch.randn(dec_b * nblk, bs, 1, 576, generator=g, device=dev) * 0.5).to(torch.bfloat16)
+    return qd, kd, kds, wd, table, lens_q, lens_k, qm, pool
+
+
 def run_c5(torch, pkg, dev, args, flush, ctx=131072, chunk=4096, H=128, topk=2048, dec_b=32):
     """C5: one sequence of 128K keys; a prefill chunk of 4096 queries at its tail runs indexer -> top-k ->
     sparse MLA on the indexer's own selection; then a decode step of 32 sequences (one query each, 128K keys
@@ -209,18 +246,11 @@ def run_c5(torch, pkg, dev, args, flush, ctx=131072, chunk=4096, H=128, topk=204
     lib = pkg.load_library()
     stream = L.stream_handle(dev)
     _log("C5 inputs")
-    g = torch.Generator(device=dev).manual_seed(20261205)
+    g = torch.Generator(device=dev).manual_seed(C5_SEED)
     Hi, D = 64, 128
-    qi = torch.randn(1, chunk, Hi, D, generator=g, device=dev).to(torch.float8_e4m3fn)
-    kf = torch.randn(1, ctx, D, generator=g, device=dev)
-    ks = (kf.abs().amax(dim=-1) / 448.0).to(torch.float32)
-    ki = (kf / ks.unsqueeze(-1)).clamp(-448, 448).to(torch.float8_e4m3fn).contiguous()
-    del kf
-    wi = torch.randn(1, chunk, Hi, generator=g, device=dev) / 8
+    qi, ki, ks, wi, q, kv = gen_c5_prefill(torch, dev, g, ctx=ctx, chunk=chunk, H=H, Hi=Hi, D=D)
     logits = torch.empty(chunk, ctx, dtype=torch.float32, device=dev)
     idx = torch.empty(1, chunk, 1, topk, dtype=torch.int32, device=dev)
-    q = (torch.randn(1, chunk, H, 576, generator=g, device=dev) * 0.5).to(torch.bfloat16)
-    kv = (torch.randn(1, ctx, 1, 576, generator=g, device=dev) * 0.5).to(torch.bfloat16)
     out = torch.empty(1, chunk, H, 512, dtype=torch.bfloat16, device=dev)
     lse = torch.empty(1, chunk, H, dtype=torch.float32, device=dev)
     ws_b = lib.dsa_sparse_mla_workspace_size(1, chunk, H, topk)
@@ -278,19 +308,10 @@ def run_c5(torch, pkg, dev, args, flush, ctx=131072, chunk=4096, H=128, topk=204
     _log("C5 decode inputs")
     bs = 64
     nblk = ctx // bs
-    qd = torch.randn(dec_b, 1, Hi, D, generator=g, device=dev).to(torch.float8_e4m3fn)
-    kdf = torch.randn(dec_b * nblk, bs, D, generator=g, device=dev)
-    kds = (kdf.abs().amax(dim=-1) / 448.0).to(torch.float32)
-    kd = (kdf / kds.unsqueeze(-1)).clamp(-448, 448).to(torch.float8_e4m3fn).contiguous()
-    del kdf
-    wd = torch.randn(dec_b, 1, Hi, generator=g, device=dev) / 8
-    table = torch.randperm(dec_b * nblk, generator=g, device=dev).view(dec_b, nblk).to(torch.int32)
-    lens_q = torch.ones(dec_b, dtype=torch.int32, device=dev)
-    lens_k = torch.full((dec_b,), ctx, dtype=torch.int32, device=dev)
+    qd, kd, kds, wd, table, lens_q, lens_k, qm, pool = gen_c5_decode(torch, dev, g, ctx=ctx, dec_b=dec_b, H=H, Hi=Hi,
+                                                                     D=D, bs=bs)
     dlog = torch.empty(dec_b, 1, ctx, dtype=torch.float32, device=dev)
     didx = torch.empty(dec_b, 1, 1, topk, dtype=torch.int32, device=dev)
-    qm = (torch.randn(dec_b, 1, H, 576, generator=g, device=dev) * 0.5).to(torch.bfloat16)
-    pool = (torch.randn(dec_b * nblk, bs, 1, 576, generator=g, device=dev) * 0.5).to(torch.bfloat16)
     dout = torch.empty(dec_b, 1, H, 512, dtype=torch.bfloat16, device=dev)
     dlse = torch.empty(dec_b, 1, H, dtype=torch.float32, device=dev)
     dws_b = lib.dsa_sparse_mla_workspace_size(dec_b, 1, H, topk)

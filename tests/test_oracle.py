@@ -167,6 +167,27 @@ def test_mla_gather_equals_dense_mask_restatement():
     torch.testing.assert_close(out, dense, rtol=1e-5, atol=1e-5)
 
 
+def test_mla_skv_padding_equals_dense_golden():
+    """The SFA example pads index lists with SKV, not -1 (example_sparse_flash_attn.py:303-308);
+    its golden scatters them into an extra mask column that is cut off (:277-278).  The gather
+    oracle drops indices >= kv_len the same way, with the golden's causal origin q_start."""
+    q, kv, _ = _mla_inputs(S=4, Skv=96, topk=24)
+    Skv, q_start = 96, 40
+    g = torch.Generator().manual_seed(8)
+    idx = torch.full((1, 4, 1, 24), Skv, dtype=torch.int32)
+    for t in range(4):
+        i_i = torch.randperm(t + q_start, generator=g)[:20]
+        idx[0, t, 0, :len(i_i)] = i_i.to(torch.int32)
+    dense = ref.sparse_mla_dense_ref(q, kv, idx, q_start_index_s=q_start)
+    # The gather form's causal rule is idx <= kv_len - q_len + t: rows t see q_start + t.
+    out, _ = ref.sparse_mla_fwd(q, kv[:, :q_start + 4], idx, actual_seq_lengths_kv=[q_start + 4])
+    torch.testing.assert_close(out, dense, rtol=1e-5, atol=1e-5)
+    # SKV slots are dropped: the same as -1 padding.
+    out_m1, _ = ref.sparse_mla_fwd(q, kv[:, :q_start + 4], torch.where(idx == Skv, -1, idx),
+                                   actual_seq_lengths_kv=[q_start + 4])
+    torch.testing.assert_close(out, out_m1, rtol=0, atol=0)
+
+
 def test_mla_single_index_closed_form():
     q, kv, _ = _mla_inputs(S=1)
     idx = torch.full((1, 1, 1, 8), -1, dtype=torch.int32)

@@ -78,3 +78,109 @@ def test_hip_graph_capture_and_replay(dsa, dev):
         assert junk.isfinite()
         for a, b in zip(got, want):
             assert torch.equal(a, b), f"replay {rep}"
+
+
+def _raises(fn, match):
+    with pytest.raises(RuntimeError, match=match):
+        fn()
+
+
+def test_ops_reject_host_and_misshaped_arguments(dsa, dev):
+    """Every tensor argument of every op is checked before a kernel is launched: a host tensor
+    (the torch_npu convention for sequence lengths) or a short buffer raises."""
+    ops = dsa.load_torch_ops()
+    g = torch.Generator().manual_seed(9)
+    B, S, Skv, H, Hi, D = 2, 4, 256, 16, 16, 128
+    qi = torch.randn(B, S, Hi, D, generator=g).to(torch.bfloat16).to(dev)
+    ki = torch.randn(B, Skv, 1, D, generator=g).to(torch.bfloat16).to(dev)
+    w = torch.randn(B, S, Hi, generator=g).to(dev)
+    lens = torch.tensor([S, S], dtype=torch.int32)
+    ops.lightning_indexer(qi, ki, w, sparse_count=16)                      # well-formed: runs
+    _raises(lambda: ops.lightning_indexer(qi, ki, w, actual_seq_lengths_query=lens), "must be on")
+    _raises(lambda: ops.lightning_indexer(qi, ki, w, actual_seq_lengths_key=lens[:1].to(dev)), "elements")
+    _raises(lambda: ops.lightning_indexer(qi, ki, w[:, :2]), "weights")
+    _raises(lambda: ops.lightning_indexer(qi, ki, w, torch.ones(B * Skv)), "key_scale")
+    _raises(lambda: ops.lightning_indexer(qi, ki, w, torch.ones(B, Skv - 1, device=dev)), "key_scale")
+    _raises(lambda: ops.lightning_indexer(qi, ki[:1], w), "batch")
+    _raises(lambda: ops.lightning_indexer(qi, ki, w, block_table=torch.zeros(B, 4, dtype=torch.int32)),
+            "must be on|s2")
+    q = torch.randn(B, S, H, 576, generator=g).to(torch.bfloat16).to(dev)
+    kv = torch.randn(B, Skv, 1, 576, generator=g).to(torch.bfloat16).to(dev)
+    idx = torch.randint(0, 64, (B, S, 1, 32), generator=g, dtype=torch.int32).to(dev)
+    sm = 576 ** -0.5
+    _raises(lambda: ops.sparse_mla_fwd(q, kv, idx, sm, actual_seq_lengths_kv=lens), "must be on")
+    _raises(lambda: ops.sparse_mla_fwd(q, kv, idx, sm, block_table=torch.zeros(B, 4, dtype=torch.int32)),
+            "must be on")
+    _raises(lambda: ops.sparse_mla_fwd(q, kv, idx, sm, block_table=torch.zeros(1, 4, dtype=torch.int32,
+                                                                                 device=dev)), "block_table")
+    _raises(lambda: ops.sparse_mla_fwd(q[..., :512].contiguous(), kv, idx, sm), "576")
+    _raises(lambda: ops.sparse_mla_fwd(q, kv[..., :512].contiguous(), idx, sm), "576")
+    _raises(lambda: ops.sparse_mla_fwd(q, kv, idx[:, :2].contiguous(), sm), "indices")
+    _raises(lambda: ops.sparse_mla_fwd(q, kv[:1], idx, sm), "batch")
+    qa = torch.randn(1, 3, 16, 512, generator=g).to(torch.bfloat16).to(dev)
+    kva = torch.randn(1, 40, 512, generator=g).to(torch.bfloat16).to(dev)
+    ia = torch.randint(0, 40, (1, 3, 8), generator=g, dtype=torch.int32).to(dev)
+    ops.sparse_attn(qa, kva, torch.zeros(16, device=dev), ia, 0.04)     # well-formed: runs
+    _raises(lambda: ops.sparse_attn(qa, kva, torch.zeros(16), ia, 0.04), "must be on")
+    _raises(lambda: ops.sparse_attn(qa, kva, torch.zeros(8, device=dev), ia, 0.04), "attn_sink")
+    _raises(lambda: ops.sparse_attn(qa, kva, None, ia.cpu(), 0.04), "must be on")
+    _raises(lambda: ops.sparse_attn(qa, kva, None, ia[:, :2].contiguous(), 0.04), "topk_idxs")
+    T, bs = 5, 128
+    qv = torch.randn(T, 16, 512, generator=g).to(torch.bfloat16).to(dev)
+    cache = torch.randn(4, bs, 1, 512, generator=g).to(torch.bfloat16).to(dev)
+    bt = torch.arange(4, dtype=torch.int32, device=dev).view(1, 4)
+    qs = torch.tensor([0], dtype=torch.int32, device=dev)
+    ql = torch.tensor([T], dtype=torch.int32, device=dev)
+    kl = torch.tensor([300], dtype=torch.int32, device=dev)
+    sinks = torch.zeros(16, device=dev)
+    ops.sparse_flash_mla(qv, cache, bt, qs, ql, kl, sinks, 0.04)         # well-formed: runs
+    _raises(lambda: ops.sparse_flash_mla(qv, cache, bt, qs.cpu(), ql, kl, sinks, 0.04), "must be on")
+    _raises(lambda: ops.sparse_flash_mla(qv, cache, bt, qs, ql, kl.cpu(), sinks, 0.04), "must be on")
+    _raises(lambda: ops.sparse_flash_mla(qv, cache, bt, qs, ql, kl, sinks.cpu(), 0.04), "must be on")
+    _raises(lambda: ops.sparse_flash_mla(qv, cache, bt, qs, ql, kl, sinks[:8], 0.04), "sinks")
+    _raises(lambda: ops.sparse_flash_mla(qv, cache, bt.cpu(), qs, ql, kl, sinks, 0.04), "must be on")
+    _raises(lambda: ops.sparse_flash_mla(qv, cache, bt, qs, ql, kl, sinks, 0.04, cache, bt), "max_cmp")
+    _raises(lambda: ops.sparse_flash_mla(qv, cache, bt, qs, ql, kl, sinks, 0.04, cache, None,
+                                         torch.zeros(T, 8, dtype=torch.int32, device=dev)), "cmp_block_table")
+    _raises(lambda: ops.sparse_flash_mla(qv, cache, bt, qs, ql, kl, sinks, 0.04, cache, bt,
+                                         torch.zeros(T - 1, 8, dtype=torch.int32, device=dev)), "cmp_sparse_indices")
+    torch.cuda.synchronize()
+
+
+def test_op_hca_matches_python_wrapper(dsa, dev):
+    """sparse_flash_mla in "hca" mode (compressed rows without selection lists) through the op,
+    with max_cmp = seqused_kv.max() // cmp_ratio as the reference API derives it, equals the
+    Python wrapper bit for bit."""
+    ops = dsa.load_torch_ops()
+    g = torch.Generator().manual_seed(12)
+    H, bs, ratio, win = 64, 128, 4, 127
+    kv_len = [700, 1500]
+    q_len = [3, 5]
+    T = sum(q_len)
+    ob = [(n + bs - 1) // bs for n in kv_len]
+    cb = [((n // ratio) + bs - 1) // bs for n in kv_len]
+    q = torch.randn(T, H, 512, generator=g).to(torch.bfloat16).to(dev)
+    ori = torch.randn(sum(ob), bs, 1, 512, generator=g).to(torch.bfloat16).to(dev)
+    cmp = torch.randn(sum(cb), bs, 1, 512, generator=g).to(torch.bfloat16).to(dev)
+    obt = torch.full((2, max(ob)), -1, dtype=torch.int32)
+    cbt = torch.full((2, max(cb)), -1, dtype=torch.int32)
+    obt[0, :ob[0]] = torch.arange(ob[0])
+    obt[1, :ob[1]] = torch.arange(ob[0], ob[0] + ob[1])
+    cbt[0, :cb[0]] = torch.arange(cb[0])
+    cbt[1, :cb[1]] = torch.arange(cb[0], cb[0] + cb[1])
+    obt, cbt = obt.to(dev), cbt.to(dev)
+    qs = torch.tensor([0, q_len[0]], dtype=torch.int32, device=dev)
+    ql = torch.tensor(q_len, dtype=torch.int32, device=dev)
+    kl = torch.tensor(kv_len, dtype=torch.int32, device=dev)
+    sinks = torch.randn(H, generator=g).to(dev)
+    scale = 512 ** -0.5
+    o1, l1 = ops.sparse_flash_mla(q, ori, obt, qs, ql, kl, sinks, scale, cmp, cbt, None, ratio, win,
+                                  max(kv_len) // ratio)
+    cu = torch.tensor([0] + list(torch.tensor(q_len).cumsum(0)), dtype=torch.int32, device=dev)
+    o2, l2 = dsa.sparse_flash_mla(q, ori_kv=ori, cmp_kv=cmp, ori_block_table=obt, cmp_block_table=cbt,
+                                  cu_seqlens_q=cu, seqused_kv=kl, sinks=sinks, softmax_scale=scale,
+                                  cmp_ratio=ratio, ori_mask_mode=4, cmp_mask_mode=3, ori_win_left=win,
+                                  ori_win_right=0, layout_q="TND", layout_kv="PA_ND",
+                                  return_softmax_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2.view_as(o1)) and torch.equal(l1, l2.view_as(l1))

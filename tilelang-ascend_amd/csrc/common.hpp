@@ -3,9 +3,33 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 namespace dsa {
 
 constexpr int kWave = 64;
+
+// Devices a process may drive (per-device launch state is kept per index).
+constexpr int kMaxDevices = 64;
+
+// Raises Kernel's dynamic-LDS limit to `bytes` on the current device, once per
+// device and thread-safely (std::call_once per device index); every later call
+// returns the first call's result, so a failure keeps being reported.  The
+// limit is a property of the kernel as loaded on one device.
+template <auto Kernel>
+hipError_t set_dynamic_lds_once(int bytes) {
+  static std::once_flag once[kMaxDevices];
+  static hipError_t result[kMaxDevices];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::call_once(once[dev], [&] {
+    result[dev] = hipFuncSetAttribute(reinterpret_cast<const void*>(Kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  });
+  return result[dev];
+}
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));

@@ -165,7 +165,7 @@ struct IdxArgs {
   int tile_stride;          // keys between consecutive tiles: 64, or 64 * F in the sample pass
   float* sample;            // [rows, sample_ld]: logits of the first 64 keys of every 64 * F
   int64_t sample_ld;
-  int32_t* row_valid;       // [rows]: valid keys per row (the sample pass, when it has several key chunks)
+  int32_t* row_valid;       // [rows]: valid keys per row (written by the sample pass)
   float* thr;               // [rows]: filter thresholds; the filter pass keeps keys with logit >= thr
   int topk;
   u32x2* cand;              // [rows, nseg, cand_cap]: (logit bits, key position) kept per (row, key chunk), in key order
@@ -535,26 +535,10 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
       if (t < t_rows) {
         float* row = a.sample + (q_base + t) * a.sample_ld;
         for (int c = slot0 + ntiles * kIdxKeyTile + lane; c < slot1; c += kWave) row[c] = -__builtin_huge_valf();
-        if (gridDim.x > 1 && blockIdx.x == 0 && lane == 0) a.row_valid[q_base + t] = nvalid[j];
+        if (blockIdx.x == 0 && lane == 0) a.row_valid[q_base + t] = nvalid[j];
       }
     }
-    // With one key chunk this workgroup wrote its rows' whole sample: each wave
-    // turns its own rows into thresholds (the barrier makes the stores visible).
-    // With several, fused_threshold_kernel does it afterwards.
-    if (gridDim.x == 1) {
-      __syncthreads();
-#pragma unroll
-      for (int j = 0; j < kTokPW; ++j) {
-        const int t = t_base + wave * kTokPW + j;
-        if (t < t_rows) {
-          const float* row = a.sample + (q_base + t) * a.sample_ld;
-          const float th = a.sample_ld <= 32 * kWave
-                               ? row_threshold<32>(row, (int)a.sample_ld, nvalid[j], a.topk, lane)
-                               : row_threshold<64>(row, (int)a.sample_ld, nvalid[j], a.topk, lane);
-          if (lane == 0) a.thr[q_base + t] = th;
-        }
-      }
-    }
+    // fused_threshold_kernel turns the rows' samples into thresholds afterwards.
   } else {
 #pragma unroll
     for (int j = 0; j < kTokPW; ++j) {
@@ -845,18 +829,16 @@ hipError_t launch_indexer_topk_fused(int kind, const void* q, const void* k, con
   a.cand = reinterpret_cast<u32x2*>(ws + p.cval);
   a.cand_cnt = reinterpret_cast<int32_t*>(ws + p.ccnt);
   a.cand_cap = p.cap;
-  // 1-2. Sample pass (tiles tile_stride apart, kFusedSampleChunkTiles per workgroup) and
-  // thresholds: in the sample pass itself when one key chunk holds the whole sample.
+  // 1-2. Sample pass (tiles tile_stride apart, kFusedSampleChunkTiles per workgroup), then
+  // the thresholds.
   a.tile_stride = (int)p.tile_stride;
   a.row_valid = reinterpret_cast<int32_t*>(ws + p.valid);
   a.key_chunk = (int)(p.tile_stride * kFusedSampleChunkTiles);
   hipError_t e = launch_indexer_mode<kModeSample>(kind, D, a, B, stream);
   if (e != hipSuccess) return e;
-  if ((S2 + a.key_chunk - 1) / a.key_chunk > 1) {
-    hipLaunchKernelGGL(fused_threshold_kernel, dim3((unsigned)((p.rows + 3) / 4)), dim3(256), 0, stream, a.sample,
-                       p.sample_ld, a.row_valid, p.rows, (int)topk, a.thr);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-  }
+  hipLaunchKernelGGL(fused_threshold_kernel, dim3((unsigned)((p.rows + 3) / 4)), dim3(256), 0, stream, a.sample,
+                     p.sample_ld, a.row_valid, p.rows, (int)topk, a.thr);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
   // 3. Filter pass over the usual key chunks (one candidate slot per chunk).
   a.tile_stride = kIdxKeyTile;
   a.key_chunk = (int)p.key_chunk;

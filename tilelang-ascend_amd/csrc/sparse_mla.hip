@@ -1004,12 +1004,8 @@ size_t mla_workspace_bytes(int64_t tokens, int64_t H, int64_t topk) {
 template <int kNW, bool kF16, int kD>
 static hipError_t launch_mla_nw(const MlaArgs& a, int head_groups, hipStream_t stream) {
   constexpr int kLds = MlaGeom<kD>::kLds;
-  static bool attr = false;
-  if (!attr) {
-    (void)hipFuncSetAttribute((const void*)sparse_mla_kernel<kNW, kF16, kD>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
-    attr = true;
-  }
+  const hipError_t ea = set_dynamic_lds_once<sparse_mla_kernel<kNW, kF16, kD>>(kLds);
+  if (ea != hipSuccess) return ea;
   const dim3 grid((unsigned)((int64_t)a.B * a.S * a.splits), (unsigned)head_groups);
   hipLaunchKernelGGL((sparse_mla_kernel<kNW, kF16, kD>), grid, dim3(kNW * kWave), kLds, stream, a);
   return hipGetLastError();

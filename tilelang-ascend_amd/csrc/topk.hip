@@ -810,19 +810,13 @@ static hipError_t launch_rows(const float* x, int64_t ld, int64_t rows, int64_t 
   const size_t lds = use_cache ? cached : base;
   const dim3 grid((unsigned)rows), block(kTopkThreads);
   if (use_cache) {
-    static bool attr = false;
-    if (!attr) {
-      (void)hipFuncSetAttribute((const void*)topk_rows_kernel<true>, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-      attr = true;
-    }
+    const hipError_t ea = set_dynamic_lds_once<topk_rows_kernel<true>>(kLdsBytes);
+    if (ea != hipSuccess) return ea;
     hipLaunchKernelGGL(topk_rows_kernel<true>, grid, block, lds, stream, x, ld, (int)n, (int)k, row_len,
                        sorted, kpad, out_idx, out_val, only_flagged, idx_map);
   } else {
-    static bool attr = false;
-    if (!attr) {
-      (void)hipFuncSetAttribute((const void*)topk_rows_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-      attr = true;
-    }
+    const hipError_t ea = set_dynamic_lds_once<topk_rows_kernel<false>>(kLdsBytes);
+    if (ea != hipSuccess) return ea;
     hipLaunchKernelGGL(topk_rows_kernel<false>, grid, block, lds, stream, x, ld, (int)n, (int)k, row_len,
                        sorted, kpad, out_idx, out_val, only_flagged, idx_map);
   }

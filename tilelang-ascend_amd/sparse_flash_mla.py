@@ -178,7 +178,9 @@ def sparse_attn(query_states: torch.Tensor, kv_states: torch.Tensor, attn_sink: 
                 topk_idxs: torch.Tensor, softmax_scale: float) -> torch.Tensor:
     """V4 gathered-index attention with sinks (examples/deepseek_v4/sparse_attention.py:171-198):
     q [b, m, h, 512], kv [b, n, 512], attn_sink [h] fp32, topk_idxs [b, m, topk] int32 (-1 =
-    empty slot; duplicates count twice) -> fp32 [b, m, h, 512], as the reference kernel writes it."""
+    empty slot; duplicates count twice) -> fp32 [b, m, h, 512].  The reference kernel writes its
+    fp32 accumulator; this kernel accumulates in fp32 and rounds the normalised output to q's dtype
+    (bf16 / fp16: a relative rounding of at most 2^-9 / 2^-12), then widens it to fp32."""
     if query_states.dtype not in _KINDS or kv_states.dtype != query_states.dtype:
         raise ValueError("query_states / kv_states must share a bfloat16 or float16 dtype")
     dev = _lib.require_device(query_states)
