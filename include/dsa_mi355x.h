@@ -15,7 +15,8 @@
  *    void (src/target/codegen_ascend.cc:1138-1225); errors are reported here
  *    instead of being dropped.
  *  - Kernels are stateless and reentrant; concurrent calls on different
- *    streams are safe.
+ *    streams are safe (except dsa_sparse_mla_fwd_noalloc, whose calls on one
+ *    GPU share a scratch array).
  */
 #ifndef DSA_MI355X_H_
 #define DSA_MI355X_H_
@@ -232,6 +233,27 @@ int dsa_sparse_mla_fwd(int kind, const void* q, const void* kv, const int32_t* i
                        int64_t H, int64_t d_qk, int64_t d_v, int64_t Skv, int64_t block_size, int64_t max_blocks,
                        int64_t topk, float sm_scale, int is_causal, void* out, float* lse, void* workspace,
                        size_t workspace_bytes, void* stream);
+
+/*
+ * dsa_sparse_mla_fwd without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * Same arguments (minus the workspace), kernels and results as
+ * dsa_sparse_mla_fwd; the split partials of decode-shaped calls go to a
+ * library-owned scratch array of dsa_sparse_mla_noalloc_max_workspace() bytes
+ * (64 MiB) per GPU, held from the library's first use on that GPU until the
+ * process ends.  A shape whose dsa_sparse_mla_workspace_size() exceeds it is
+ * rejected (hipErrorInvalidValue).  The call allocates nothing.  Calls that
+ * overlap on one GPU (concurrent streams, or host threads) share that array
+ * and race: serialise them.
+ */
+size_t dsa_sparse_mla_noalloc_max_workspace(void);
+
+int dsa_sparse_mla_fwd_noalloc(int kind, const void* q, const void* kv, const int32_t* indices,
+                               const int32_t* block_table, const int32_t* actual_q_len, const int32_t* actual_kv_len,
+                               int64_t B, int64_t S, int64_t H, int64_t d_qk, int64_t d_v, int64_t Skv,
+                               int64_t block_size, int64_t max_blocks, int64_t topk, float sm_scale, int is_causal,
+                               void* out, float* lse, void* stream);
 
 /*
  * DeepSeek V4 sparse flash MLA (D = 512, K = V, paged caches, attention sinks).

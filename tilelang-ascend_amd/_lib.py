@@ -71,6 +71,10 @@ SIGNATURES = {
     "dsa_sparse_mla_fwd": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64,
                                     _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_float, _c_int, _c_vp, _c_vp, _c_vp,
                                     _c_size, _c_vp]),
+    "dsa_sparse_mla_noalloc_max_workspace": (_c_size, []),
+    "dsa_sparse_mla_fwd_noalloc": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
+                                            _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_float, _c_int, _c_vp,
+                                            _c_vp, _c_vp]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

@@ -28,6 +28,8 @@ hipError_t launch_sparse_mla(int is_fp16, const void* q, const void* kv, const i
                              int64_t Skv, int64_t block_size, int64_t max_blocks, int64_t topk, float sm_scale,
                              int causal, void* out, float* lse, void* workspace, hipStream_t stream);
 size_t mla_workspace_bytes(int64_t tokens, int64_t H, int64_t topk);
+size_t mla_scratch_bytes();
+hipError_t mla_scratch_ptr(void** out);
 size_t v4_workspace_bytes(int64_t T, int64_t H, int64_t cap);
 size_t sparse_attn_sink_workspace_bytes(int64_t T, int64_t H, int64_t K);
 hipError_t launch_sparse_attn_sink(int is_fp16, const void* q, const void* kv, const int32_t* idx, int64_t B,
@@ -65,7 +67,7 @@ constexpr int64_t dsa_kSrc2Limit = 0x40000000;
 
 extern "C" {
 
-int dsa_abi_version(void) { return 103; }
+int dsa_abi_version(void) { return 104; }
 
 const char* dsa_last_error_message(void) { return g_msg; }
 
@@ -329,6 +331,26 @@ int dsa_sparse_mla_fwd(int kind, const void* q, const void* kv, const int32_t* i
   return ok(dsa::launch_sparse_mla(kind == DSA_KIND_FP16, q, kv, indices, block_table, actual_q_len, actual_kv_len, B, S, H, skv_eff,
                                    block_size, max_blocks, topk, sm_scale, is_causal ? 1 : 0, out, lse, workspace,
                                    static_cast<hipStream_t>(stream)));
+}
+
+size_t dsa_sparse_mla_noalloc_max_workspace(void) { return dsa::mla_scratch_bytes(); }
+
+int dsa_sparse_mla_fwd_noalloc(int kind, const void* q, const void* kv, const int32_t* indices,
+                               const int32_t* block_table, const int32_t* actual_q_len, const int32_t* actual_kv_len,
+                               int64_t B, int64_t S, int64_t H, int64_t d_qk, int64_t d_v, int64_t Skv,
+                               int64_t block_size, int64_t max_blocks, int64_t topk, float sm_scale, int is_causal,
+                               void* out, float* lse, void* stream) {
+  const size_t need = dsa_sparse_mla_workspace_size(B, S, H, topk);
+  if (need > dsa::mla_scratch_bytes())
+    return reject("sparse_mla_noalloc: the split partials of this shape exceed the 64 MiB scratch "
+                  "(dsa_sparse_mla_noalloc_max_workspace); use dsa_sparse_mla_fwd with a workspace");
+  void* ws = nullptr;
+  if (need > 0) {
+    const hipError_t e = dsa::mla_scratch_ptr(&ws);
+    if (e != hipSuccess) return ok(e);
+  }
+  return dsa_sparse_mla_fwd(kind, q, kv, indices, block_table, actual_q_len, actual_kv_len, B, S, H, d_qk, d_v, Skv,
+                            block_size, max_blocks, topk, sm_scale, is_causal, out, lse, ws, need, stream);
 }
 
 // Row-list capacity of a V4 call: the window plus the compressed slots.

@@ -1001,6 +1001,35 @@ size_t mla_workspace_bytes(int64_t tokens, int64_t H, int64_t topk) {
   return (size_t)splits * tokens * H * (kMlaDV * 2 + 4) + 256;
 }
 
+// Split partials of the allocation-free entry (dsa_sparse_mla_fwd_noalloc): one
+// array per GPU, resident from the library's load on that GPU until the process
+// ends.  64 MiB holds the split partials of decode batches up to 64 sequences x
+// 128 heads x topk 2048 (33.7 MB).  Every partial slot the kernels read is
+// written earlier in the same call (a split with no valid slot writes zeros and
+// an LSE of -inf), so nothing needs clearing between calls; calls that overlap
+// on one GPU share the array and race.
+constexpr size_t kMlaScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) uint8_t scratch[kMlaScratchBytes];
+
+size_t mla_scratch_bytes() { return kMlaScratchBytes; }
+
+// The device address of `scratch` on the current device.  In host code the
+// array's name only stands for the symbol; its address on a GPU comes from
+// hipGetSymbolAddress, looked up once per device (each GPU holds its own copy)
+// and kept.
+hipError_t mla_scratch_ptr(void** out) {
+  static std::once_flag once[kMaxDevices];
+  static void* addr[kMaxDevices];
+  static hipError_t result[kMaxDevices];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::call_once(once[dev], [&] { result[dev] = hipGetSymbolAddress(&addr[dev], HIP_SYMBOL(scratch)); });
+  *out = result[dev] == hipSuccess ? addr[dev] : nullptr;
+  return result[dev];
+}
+
 template <int kNW, bool kF16, int kD>
 static hipError_t launch_mla_nw(const MlaArgs& a, int head_groups, hipStream_t stream) {
   constexpr int kLds = MlaGeom<kD>::kLds;
