@@ -23,8 +23,8 @@
 // 4-stage ring, up to three tiles ahead of the MFMAs; each wave waits on its
 // own vmcnt, then a barrier publishes the tile.  A tile is 36 blocks of 1 KB,
 // each 8 slots x 8 chunks of 16 bytes, XOR-swizzled (lds_swizzle below): one
-// DMA instruction fetches 8 whole 128-byte lines, and both the 16-slot MFMA
-// operand reads and the transposed V reads are bank-conflict free.  Empty /
+// DMA instruction fetches 8 whole 128-byte lines, and the 16-slot MFMA
+// operand reads are bank-conflict free.  Empty /
 // masked slots re-load a valid row of the same workgroup and get probability 0;
 // leading tiles with no valid slot are skipped.
 //
@@ -64,7 +64,7 @@ struct MlaGeom {
   static constexpr int kStageBytes = kMlaTile * kRowBytes;      // 36864 / 32768
   static constexpr int kTileInstr = kStageBytes / 1024;         // wave-wide 16-byte DMA loads per tile
   static constexpr int kRowsOffset = kStages * kStageBytes;
-  static constexpr int kTileMaskOffset = kRowsOffset + kSlotsCap * 4 + 16;  // after rows, overflow flag, first valid slot
+  static constexpr int kTileMaskOffset = kRowsOffset + kSlotsCap * 4 + 16;  // after rows, overflow flag, first and last valid slot
   static constexpr int kLds = kTileMaskOffset + (kSlotsCap / 32) * 4;       // + one valid-slot bitmask per tile
   static constexpr int kSteps = kD / 32;                        // 32-dim steps of Q K^T
   static constexpr int kQkHalf = 2 * kSteps;                    // half-steps (one K operand read each)
@@ -155,11 +155,18 @@ struct MlaCfg {
 // 8b .. 8b+7, with (slot 8a+u, chunk 8b+w) at 16-byte position
 // 8u + (w ^ lds_swizzle(u, a)) of the block.  One DMA instruction fills one
 // block, so its 64 lanes fetch 8 whole 128-byte lines (8 lanes per slot) --
-// a gather of full cache lines -- and the swizzle keeps the Q K^T operand
-// reads (ds_read_b128) and the transposed V reads (ds_read_b64_tr_b16)
-// free of LDS bank conflicts.
+// a gather of full cache lines.  The swizzle is set by the LDS of gfx950:
+// 128 banks of 4 bytes, a ds_read_b128 served per 32-lane half-wave, which
+// is conflict-free when its 32 16-byte chunks fall on distinct positions
+// modulo 512 bytes.  A Q K^T operand read (half-wave: slots r = 0..15 of row
+// groups a, a+1, chunks 4 par + g for two g) lands on position
+// 8 (u & 3) + (w ^ lds_swizzle(u, a)) mod 32, so the swizzle maps
+// (u >> 2, a & 1) one-to-one onto bits 2 and 1, leaving bit 0 to g: all 32
+// distinct.  The transposed V reads (8 bytes a lane, one half of each chunk
+// per instruction) keep the 2-way sharing that such reads have in any
+// layout; the DMA writes are contiguous.
 __host__ __device__ constexpr int lds_swizzle(int u, int a) {
-  return ((u & 1) ? 2 : 0) ^ ((u & 2) ? 4 : 0) ^ ((u & 4) ? 1 : 0) ^ ((a & 1) ? 2 : 0);
+  return ((u & 2) ? 4 : 0) ^ ((u & 4) ? 4 : 0) ^ ((a & 1) ? 2 : 0);
 }
 
 // The DMA of tile `tile` (slots tile*32 .. +31 of this workgroup) into a
@@ -667,12 +674,17 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
 #pragma unroll
   for (int j = 0; j < kIdxPerLane; ++j) __asm__ __volatile__("" : "+v"(row_of[j]));
   int32_t* first_valid = rows + kSlotsCap + 1;
-  if (tid == 0) *first_valid = 0x7fffffff;
+  int32_t* last_valid = rows + kSlotsCap + 2;
+  if (tid == 0) {
+    *first_valid = 0x7fffffff;
+    *last_valid = -1;
+  }
   __syncthreads();
   // Each wave wrote 64 consecutive slots per pass; record, per tile of 32,
   // the bitmask of its valid slots.
   uint32_t* tile_mask = reinterpret_cast<uint32_t*>(lds + Geo::kTileMaskOffset);
   int wave_first = 0x7fffffff;  // lowest valid slot this wave saw (wave-uniform)
+  int wave_last = -1;           // highest
 #pragma unroll
   for (int j = 0; j < kIdxPerLane; ++j) {
     const int i0 = wave * kWave + j * Cfg::kThreads;
@@ -680,22 +692,31 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
     const int row = row_active ? row_of[j] : -1;
     if (i < ntiles * kMlaTile) rows[i] = row;
     const uint64_t vm = __ballot(row >= 0 && i < ntiles * kMlaTile);
-    if (vm != 0) wave_first = min(wave_first, i0 + (int)__builtin_ctzll(vm));
+    if (vm != 0) {
+      wave_first = min(wave_first, i0 + (int)__builtin_ctzll(vm));
+      wave_last = max(wave_last, i0 + 63 - (int)__builtin_clzll(vm));
+    }
     if (lane == 0 && i0 < ntiles * kMlaTile) {
       tile_mask[i0 / kMlaTile] = (uint32_t)vm;
       if (i0 / kMlaTile + 1 < ntiles) tile_mask[i0 / kMlaTile + 1] = (uint32_t)(vm >> 32);
     }
   }
   // One LDS atomic per wave (one per valid slot would serialise hundreds).
-  if (lane == 0 && wave_first != 0x7fffffff) atomicMin(first_valid, wave_first);
+  if (lane == 0 && wave_first != 0x7fffffff) {
+    atomicMin(first_valid, wave_first);
+    atomicMax(last_valid, wave_last);
+  }
   __syncthreads();
   const int fv = *first_valid;
   const int safe_row = fv < kSlotsCap ? rows[fv] : -1;
   const int nslots_all = ntiles * kMlaTile;  // the exact fallback walks every slot
   if (safe_row < 0) ntiles = 0;              // no valid slot: out = 0, lse = -inf
   // Tiles before the first valid slot contribute nothing: start at its tile,
-  // which then also fixes the softmax reference.
+  // which then also fixes the softmax reference.  Tiles after the last valid
+  // slot contribute nothing either (a causal row shorter than topk ends in
+  // empty slots): stop at its tile.
   const int t_first = safe_row < 0 ? 0 : fv / kMlaTile;
+  if (safe_row >= 0) ntiles = min(ntiles, *last_valid / kMlaTile + 1);
   ntiles -= t_first;
   const int32_t* trows = rows + t_first * kMlaTile;
   const uint32_t* tmask = tile_mask + t_first;
