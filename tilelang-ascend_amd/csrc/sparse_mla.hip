@@ -570,7 +570,8 @@ __device__ __attribute__((noinline)) void mla_exact_fallback(const uint16_t* q, 
   }
 }
 
-template <int kNW, bool kF16, int kD>
+// kPaged: the KV rows are addressed through a block table (a.block_table).
+template <int kNW, bool kF16, int kD, bool kPaged>
 __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   using Cfg = MlaCfg<kNW, kD>;
   using Geo = MlaGeom<kD>;
@@ -594,9 +595,12 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   hb_on[1] = head0 + 16 < a.H;
 
   // The prologue is a chain of global-memory latencies; it is ordered so
-  // they overlap: the lengths and this lane's slot indices go out first, the
-  // Q rows (the largest load) right behind them (a compiler barrier keeps
-  // that order), and the block-table lookups as soon as the indices are back.
+  // they overlap: the lengths and this lane's slot indices go out first, then
+  // the Q rows (the largest load; a compiler barrier keeps that order) -- for
+  // a paged cache only after the block-table lookups, which need the indices
+  // -- so that the slot table and the first tiles' DMA are issued while Q is
+  // still arriving: nothing waits for Q before the first tile (vector-memory
+  // loads complete in issue order, so the first tile's wait covers Q).
   const int32_t* irow = a.indices + (int64_t)token * a.topk;
   const int slot_begin = split * a.keys_per_split;
   // Row lists: a negative count marks a padded query row (out = 0, lse = 0).
@@ -622,14 +626,19 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   __asm__ __volatile__("" ::: "memory");
 
   // Q operands (B of S^T = K Q^T): head head0 + 16*hb + r, dims 32*st + 8*g .. +8.
+  // Heads past H (a wave's second head block when H is not a multiple of 32)
+  // repeat head H - 1; their results are not stored.
   u32x4 qb[2][kD / 32];
+  auto load_q = [&]() {
 #pragma unroll
-  for (int hb = 0; hb < 2; ++hb) {
-    const int h = min(head0 + 16 * hb + r, a.H - 1);
-    const uint16_t* qp = a.q + ((int64_t)token * a.H + h) * kD + 8 * g;
+    for (int hb = 0; hb < 2; ++hb) {
+      const int h = min(head0 + 16 * hb + r, a.H - 1);
+      const uint16_t* qp = a.q + ((int64_t)token * a.H + h) * kD + 8 * g;
 #pragma unroll
-    for (int st = 0; st < kD / 32; ++st) qb[hb][st] = *reinterpret_cast<const u32x4*>(qp + 32 * st);
-  }
+      for (int st = 0; st < kD / 32; ++st) qb[hb][st] = *reinterpret_cast<const u32x4*>(qp + 32 * st);
+    }
+  };
+  if constexpr (!kPaged) load_q();
   const int ql = min(max(ql_raw, 0), a.S);
   const int kl = Geo::kRowLists ? 0x7fffffff : min(max(kl_raw, 0), a.Skv);
   const bool row_active = Geo::kRowLists ? count_raw >= 0 : s < ql;
@@ -649,28 +658,20 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   if constexpr (Geo::kRowLists) {
 #pragma unroll
     for (int j = 0; j < kIdxPerLane; ++j) row_of[j] = ok[j] ? idx_raw[j] : -1;
-  } else if (a.block_table) {
-    // All lookups first (from a clamped valid entry), then the translation.
+  } else if constexpr (kPaged) {
+    // All lookups first (from a clamped valid entry), then Q, then the translation.
     int blk[kIdxPerLane];
     const int32_t* bt = a.block_table + (int64_t)b * a.max_blocks;
 #pragma unroll
     for (int j = 0; j < kIdxPerLane; ++j) blk[j] = bt[ok[j] ? idx_raw[j] / a.block_size : 0];
+    __asm__ __volatile__("" ::: "memory");
+    load_q();
 #pragma unroll
     for (int j = 0; j < kIdxPerLane; ++j) row_of[j] = ok[j] ? blk[j] * a.block_size + idx_raw[j] % a.block_size : -1;
   } else {
 #pragma unroll
     for (int j = 0; j < kIdxPerLane; ++j) row_of[j] = ok[j] ? b * a.Skv + idx_raw[j] : -1;
   }
-  // Q and the block-table lookups must be resident before the DMA ring
-  // starts: vmcnt then only counts DMA.
-  wait_vmcnt<0>();
-#pragma unroll
-  for (int hb = 0; hb < 2; ++hb)
-#pragma unroll
-    for (int st = 0; st < kD / 32; ++st) {
-      if (!hb_on[hb]) qb[hb][st] = u32x4{0, 0, 0, 0};  // heads past H (wave-uniform)
-      __asm__ __volatile__("" : "+v"(qb[hb][st]));
-    }
 #pragma unroll
   for (int j = 0; j < kIdxPerLane; ++j) __asm__ __volatile__("" : "+v"(row_of[j]));
   int32_t* first_valid = rows + kSlotsCap + 1;
@@ -1051,14 +1052,23 @@ hipError_t mla_scratch_ptr(void** out) {
   return result[dev];
 }
 
-template <int kNW, bool kF16, int kD>
-static hipError_t launch_mla_nw(const MlaArgs& a, int head_groups, hipStream_t stream) {
+template <int kNW, bool kF16, int kD, bool kPaged>
+static hipError_t launch_mla_kernel(const MlaArgs& a, int head_groups, hipStream_t stream) {
   constexpr int kLds = MlaGeom<kD>::kLds;
-  const hipError_t ea = set_dynamic_lds_once<sparse_mla_kernel<kNW, kF16, kD>>(kLds);
+  const hipError_t ea = set_dynamic_lds_once<sparse_mla_kernel<kNW, kF16, kD, kPaged>>(kLds);
   if (ea != hipSuccess) return ea;
   const dim3 grid((unsigned)((int64_t)a.B * a.S * a.splits), (unsigned)head_groups);
-  hipLaunchKernelGGL((sparse_mla_kernel<kNW, kF16, kD>), grid, dim3(kNW * kWave), kLds, stream, a);
+  hipLaunchKernelGGL((sparse_mla_kernel<kNW, kF16, kD, kPaged>), grid, dim3(kNW * kWave), kLds, stream, a);
   return hipGetLastError();
+}
+
+// Row lists (D = 512) never use a block table.
+template <int kNW, bool kF16, int kD>
+static hipError_t launch_mla_nw(const MlaArgs& a, int head_groups, hipStream_t stream) {
+  if constexpr (kD == 576) {
+    if (a.block_table) return launch_mla_kernel<kNW, kF16, kD, true>(a, head_groups, stream);
+  }
+  return launch_mla_kernel<kNW, kF16, kD, false>(a, head_groups, stream);
 }
 
 template <bool kF16, int kD>
