@@ -154,6 +154,82 @@ def cpu_baseline_prefill(torch, q, kv, idx, budget_s=12.0):
                       f"of the step workload, {el:.1f} s"}
 
 
+def _cpu_model():
+    """The host CPU's model name (first /proc/cpuinfo entry)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def cpu_baselines_other(torch):
+    """The oracle (fp32, all host threads) on the other configurations: C1 at full shape, C2 and C3 on
+    bounded samples scaled linearly to the full shape (labelled "extrapolated")."""
+    from oracle import dsa_oracle as ref
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    res = {}
+
+    # C1: B=1, Sq=128, Skv=4096, H=16, topk=512, the parity case's own inputs (seed 20261201).
+    g = torch.Generator().manual_seed(20261201)
+    q = (torch.randn(1, 128, 16, 576, generator=g) * 0.5).to(torch.bfloat16)
+    kv = (torch.randn(1, 4096, 1, 576, generator=g) * 0.5).to(torch.bfloat16)
+    idx = ref.causal_sparse_indices(1, 128, 4096, 512, seed=20261201)
+    ref.sparse_mla_fwd(q[:, :4], kv, idx[:, :4], 576 ** -0.5, compute_dtype=torch.float32)  # warm
+    t0 = time.perf_counter()
+    ref.sparse_mla_fwd(q, kv, idx, 576 ** -0.5, compute_dtype=torch.float32)
+    el = time.perf_counter() - t0
+    fl = 2.0 * 16 * 512 * 1088 * 128
+    res["C1_sparse_mla"] = {"value": round(fl / el / 1e12, 4), "unit": "TFLOP/s", "ms": round(el * 1e3, 1),
+                            "sample": "full shape (128 queries x 16 heads x topk 512 over 4096 keys)"}
+
+    # C2: indexer logits + top-2048 over the last 256 of 4096 query rows (32768 keys, 64 fp8 heads x 128), x16.
+    g = torch.Generator().manual_seed(20261202)
+    S1, S2, Hi, D, K, rows = 4096, 32768, 64, 128, 2048, 256
+    qi = torch.randn(1, rows, Hi, D, generator=g).to(torch.float8_e4m3fn)
+    kf = torch.randn(1, S2, D, generator=g)
+    ks = (kf.abs().amax(dim=-1) / 448.0).to(torch.float32)
+    ki = (kf / ks.unsqueeze(-1)).clamp(-448, 448).to(torch.float8_e4m3fn)
+    wi = torch.randn(1, rows, Hi, generator=g) / 8
+    del kf
+    t0 = time.perf_counter()
+    # The last 256 rows of the causal chunk see keys s <= S2 - S1 + t: as rows of a 256-row chunk at the tail.
+    lg = ref.indexer_logits(qi, ki, wi, ks, sparse_mode=3, row_chunk=16, compute_dtype=torch.float32)
+    t1 = time.perf_counter()
+    ref.topk_stable(lg.view(rows, S2), K)
+    t2 = time.perf_counter()
+    scale = S1 / rows
+    res["C2_indexer_topk"] = {"us": round((t2 - t0) * scale * 1e6, 0), "indexer_us": round((t1 - t0) * scale * 1e6, 0),
+                              "topk_us": round((t2 - t1) * scale * 1e6, 0), "unit": "us per call",
+                              "sample": f"last {rows} of {S1} query rows, x{scale:.0f} (extrapolated)"}
+    del qi, ki, wi, lg
+
+    # C3: paged decode, 8 of the 64 sequences (their 1024 blocks each, remapped), x8.
+    g = torch.Generator().manual_seed(20261203)
+    nseq, B, H, bs, nblk, topk = 8, 64, 128, 64, 1024, 2048
+    qd = (torch.randn(nseq, 1, H, 576, generator=g) * 0.5).to(torch.bfloat16)
+    pool = (torch.randn(nseq * nblk, bs, 1, 576, generator=g) * 0.5).to(torch.bfloat16)
+    table = torch.randperm(nseq * nblk, generator=g).view(nseq, nblk).to(torch.int32)
+    idd = torch.stack([torch.randperm(nblk * bs, generator=g)[:topk] for _ in range(nseq)]).to(torch.int32)
+    idd = idd.view(nseq, 1, 1, topk)
+    t0 = time.perf_counter()
+    ref.sparse_mla_fwd(qd, pool, idd, 576 ** -0.5, block_table=table, compute_dtype=torch.float32)
+    el = (time.perf_counter() - t0) * (B / nseq)
+    res["C3_decode"] = {"us": round(el * 1e6, 0), "unit": "us per call",
+                        "sample": f"{nseq} of {B} sequences (128 heads x topk 2048, 64-token blocks), x{B // nseq} "
+                                  "(extrapolated)"}
+    res["cores"] = threads
+    res["kind"] = "port"
+    return res
+
+
 def run_step(torch, pkg, dev, args, S, H, topk, sm_scale):
     """C4 sparse MLA prefill: the timed step.  Returns (result dict, inputs for the CPU baseline)."""
     _log("generating C4 prefill inputs")
@@ -191,7 +267,7 @@ def run_step(torch, pkg, dev, args, S, H, topk, sm_scale):
                      # HBM bytes per launch from the committed FETCH_SIZE/WRITE_SIZE summary; at H=128 the
                      # kernel runs one 256-thread workgroup per query token.
                      "traffic": profiled_traffic(STEP_KERNEL, S * 256),
-                     "traffic_source": "profiles/traffic_fetch_write_bench.txt",
+                     "traffic_source": "profiles/traffic_c4_prefill_step.txt",
                      "kernel": STEP_KERNEL, "flops_per_launch": flops},
         "wall_s_timed_region": round(wall, 4),
         "step_ms_p10_p90": [round(sorted(step_ms)[len(step_ms) // 10], 4),
@@ -362,7 +438,7 @@ def run_c5(torch, pkg, dev, args, flush, ctx=131072, chunk=4096, H=128, topk=204
 
 
 PROFILES = ROOT / "profiles"
-STEP_KERNEL = "dsa::sparse_mla_kernel<4, false, 576>"
+STEP_KERNEL = "dsa::sparse_mla_kernel<4, false, 576, false>"
 COPY_KERNEL = "__amd_rocclr_copyBuffer"
 
 
@@ -511,24 +587,27 @@ def _kname(name):
     return name[5:] if name.startswith("void ") else name
 
 
-def summarize_trace(db):
-    """Per-kernel dispatch statistics from a `rocprofv3 --kernel-trace` rocpd database (durations in us)."""
+def summarize_trace(db, drop=0, label=""):
+    """Per-kernel dispatch statistics from a `rocprofv3 --kernel-trace` rocpd database (durations in us).
+
+    The first `drop` dispatches of every (kernel, grid) row are left out (the warmup launches of a
+    bench part), so the averages cover the timed launches only; `label` names the workload."""
     con = _rocpd(db)
     rows = con.execute("select name, grid_x * grid_y * grid_z, workgroup_x, duration, lds_size, scratch_size, "
-                       "vgpr_count, accum_vgpr_count from kernels").fetchall()
+                       "vgpr_count, accum_vgpr_count, start from kernels order by start").fetchall()
     agg = {}
-    for name, grid, wg, dur, lds, scr, vg, ag in rows:
+    for name, grid, wg, dur, lds, scr, vg, ag, _start in rows:
         name = _kname(name)
         if not name.startswith("dsa::"):
             continue
         key = (name, grid, wg)
         agg.setdefault(key, {"d": [], "meta": (lds, scr, vg, ag)})["d"].append(dur / 1e3)
-    print(f"{'kernel':42s} {'grid':>9s} {'wg':>4s} {'calls':>5s} {'avg_us':>10s} {'min_us':>10s} {'max_us':>10s} "
-          f"lds/scratch/vgpr/agpr")
+    print(f"{'workload':10s} {'kernel':48s} {'grid':>9s} {'wg':>4s} {'calls':>5s} {'avg_us':>10s} {'min_us':>10s} "
+          f"{'max_us':>10s} lds/scratch/vgpr/agpr")
     for (name, grid, wg), v in sorted(agg.items(), key=lambda kv: -sum(kv[1]["d"])):
-        d = v["d"]
-        print(f"{name:42s} {grid:9d} {wg:4d} {len(d):5d} {sum(d) / len(d):10.1f} {min(d):10.1f} {max(d):10.1f} "
-              f"{'/'.join(str(x) for x in v['meta'])}")
+        d = v["d"][drop:] if len(v["d"]) > drop else v["d"]
+        print(f"{label:10s} {name:48s} {grid:9d} {wg:4d} {len(d):5d} {sum(d) / len(d):10.1f} {min(d):10.1f} "
+              f"{max(d):10.1f} {'/'.join(str(x) for x in v['meta'])}")
 
 
 def _counter_means(db, counter):
@@ -584,7 +663,7 @@ def summarize_mfma(util_db, mops_db):
 
 def profiled_traffic(kernel, grid):
     """HBM bytes per launch of (kernel, grid) from the committed counter summary, or None if it has none."""
-    path = PROFILES / "traffic_fetch_write_bench.txt"
+    path = PROFILES / "traffic_c4_prefill_step.txt"
     if not path.exists():
         return None
     for line in path.read_text().splitlines():
@@ -598,7 +677,9 @@ def main():
     if len(sys.argv) > 1 and sys.argv[1] in ("--rocprof-trace", "--rocprof-traffic", "--rocprof-mfma"):
         # Summaries of rocprofv3 databases written by profiling this script (no GPU needed).
         if sys.argv[1] == "--rocprof-trace":
-            summarize_trace(sys.argv[2])
+            # --rocprof-trace DB [DROP [LABEL]]
+            summarize_trace(sys.argv[2], int(sys.argv[3]) if len(sys.argv) > 3 else 0,
+                            sys.argv[4] if len(sys.argv) > 4 else "")
         elif sys.argv[1] == "--rocprof-mfma":
             summarize_mfma(*sys.argv[2:4])
         else:
@@ -610,6 +691,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--reps", type=int, default=20, help="repetitions of the secondary (flushed) benchmarks")
     ap.add_argument("--skip", default="", help="comma list of parts to skip: step,indexer,decode,c5,v4,sfa,cpu")
+    ap.add_argument("--only", default="", help="comma list of the only parts to run (the complement of --skip)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy (HBM byte-counter calibration for rocprof)")
     args = ap.parse_args()
@@ -618,6 +700,9 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     skip = set(filter(None, args.skip.split(",")))
+    parts = {"step", "indexer", "decode", "c5", "v4", "sfa", "cpu"}
+    if args.only:
+        skip |= parts - set(filter(None, args.only.split(",")))
 
     import torch
     import __graft_entry__
@@ -776,6 +861,9 @@ def main():
     if "cpu" not in skip and cpu_inputs is not None:
         _log("CPU baseline (oracle, bounded sample)")
         result["cpu_baseline"] = cpu_baseline_prefill(torch, *cpu_inputs)
+        del cpu_inputs
+        result["cpu_baselines_other"] = cpu_baselines_other(torch)
+        result["cpu_model"] = _cpu_model()
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)

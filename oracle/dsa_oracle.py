@@ -138,6 +138,7 @@ def indexer_logits(
     actual_k_len: Optional[Sequence[int]] = None,
     sparse_mode: int = 3,
     row_chunk: int = 256,
+    compute_dtype: torch.dtype = torch.float64,
 ) -> torch.Tensor:
     """logits[b, t, s] = k_scale[b, s] * sum_h w[b, t, h] * ReLU(q[b, t, h, :] . k[b, s, :]).
 
@@ -148,6 +149,8 @@ def indexer_logits(
     weighted head sum, causal mask) and example_lightning_indexer.py:137-142.
     Rows are processed in chunks so the [rows, H, S2] intermediate stays small
     (the reference materialises it whole, 34 GB at the largest config).
+    ``compute_dtype`` float32 follows the reference's own fp32 arithmetic (used
+    for the timed CPU baseline); the default float64 is the checker's.
     """
     if k.dim() == 4:
         k = k[:, :, 0, :]
@@ -164,15 +167,15 @@ def indexer_logits(
         aq, ak = aq_l[b], ak_l[b]
         if aq == 0 or ak == 0:
             continue
-        kb = kf[b, :ak].to(torch.float64)  # [ak, D]
+        kb = kf[b, :ak].to(compute_dtype)  # [ak, D]
         for r0 in range(0, aq, row_chunk):
             r1 = min(aq, r0 + row_chunk)
-            qb = qf[b, r0:r1].to(torch.float64)  # [r, H, D]
-            wb = wf[b, r0:r1].to(torch.float64)  # [r, H]
+            qb = qf[b, r0:r1].to(compute_dtype)  # [r, H, D]
+            wb = wf[b, r0:r1].to(compute_dtype)  # [r, H]
             qk = torch.relu(torch.einsum("rhd,sd->rhs", qb, kb))
             score = torch.einsum("rhs,rh->rs", qk, wb)
             if sc is not None:
-                score = score * sc[b, :ak].to(torch.float64)[None, :]
+                score = score * sc[b, :ak].to(compute_dtype)[None, :]
             score = score.to(torch.float32)
             for i in range(r1 - r0):
                 nv = causal_valid_len(aq, ak, r0 + i, sparse_mode)
