@@ -181,9 +181,7 @@ __host__ __device__ constexpr int lds_swizzle(int u, int a) {
 // (reading the slot -> row map from LDS; a row tagged kSrc2Bit is read from
 // the second source), issue<D>() sends instruction D.
 // Sent in one burst, the instructions of the four waves queue behind each
-// other in the memory pipeline and stall the issuing waves.  Past the last
-// tile (`live` false) every lane re-reads `safe_row` into the stage nobody
-// uses any more, which keeps the matrix loop free of branches.
+// other in the memory pipeline and stall the issuing waves.
 template <int kNW, int kD>
 struct TileDma {
   static constexpr int kRowChunks = MlaGeom<kD>::kRowChunks;
@@ -194,14 +192,14 @@ struct TileDma {
   int wave;
 
   __device__ __forceinline__ void prepare(const uint8_t* kv, const uint8_t* kv2, const int32_t* rows, int safe_row,
-                                          int tile, uint8_t* stage_base, int wave_, int lane, bool live) {
+                                          int tile, uint8_t* stage_base, int wave_, int lane) {
     wave = wave_;
     stage = stage_base;
     const int u = lane >> 3;
 #pragma unroll
     for (int ag = 0; ag < kGroups; ++ag) {
       const int a = wave + ag * kNW;
-      int row = live ? rows[tile * kMlaTile + 8 * a + u] : -1;
+      int row = rows[tile * kMlaTile + 8 * a + u];
       row = row >= 0 ? row : safe_row;
       const uint8_t* base = kv;
       if constexpr (MlaGeom<kD>::kRowLists) {
@@ -727,13 +725,13 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   constexpr int kStageBytes = Geo::kStageBytes;
   constexpr int kDepth = Cfg::kDepth;
   constexpr int kL = Cfg::kMaxPerWave;
-  // Every tile index below ntiles + kDepth gets a DMA (a dummy one past the
-  // end), so each iteration waits for a fixed number of outstanding tiles.
-  if (ntiles > 0) {
+  // The first min(kDepth, ntiles) tiles go out now; iteration t sends tile
+  // t + kDepth while it exists (no DMA past the last tile).
 #pragma unroll
-    for (int t = 0; t < kDepth; ++t) {
+  for (int t = 0; t < kDepth; ++t) {
+    if (t < ntiles) {
       TileDma<kNW, kD> dma;
-      dma.prepare(kvb, kvb2, trows, safe_row, t, lds + (t % kStages) * kStageBytes, wave, lane, t < ntiles);
+      dma.prepare(kvb, kvb2, trows, safe_row, t, lds + (t % kStages) * kStageBytes, wave, lane);
       il_dma_all(dma);
     }
   }
@@ -817,7 +815,7 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   if (ntiles > 0) {
     u32x4 pa[2];
     {
-      wait_tiles<kL>(kDepth - 1);
+      wait_tiles<kL>(min(kDepth, ntiles) - 1);
       raw_barrier();
       f32x4 c[2][2];
       uint32_t qa[2];
@@ -848,19 +846,19 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
       sm.template run<8>();
       sm.template run<9>();
     }
-    for (int tile = 0; tile + 1 < ntiles; ++tile) {
-      wait_tiles<kL>(kDepth - 2);
-      raw_barrier();
+    auto iteration = [&](auto dma_c, int tile) {
+      constexpr bool kDma = decltype(dma_c)::value;
       // The DMA of tile + kDepth (into the stage tile - 1 left) goes out
       // spread over phase A.
       TileDma<kNW, kD> dma;
-      dma.prepare(kvb, kvb2, trows, safe_row, tile + kDepth, lds + ((tile + kDepth) % kStages) * kStageBytes, wave,
-                  lane, tile + kDepth < ntiles);
+      if constexpr (kDma)
+        dma.prepare(kvb, kvb2, trows, safe_row, tile + kDepth, lds + ((tile + kDepth) % kStages) * kStageBytes, wave,
+                    lane);
       f32x4 c[2][2];
       uint32_t qa[2], va[2];
       stage_k(tile + 1, qa);
       stage_v(tile, va);
-      qk_phase<kF16, kNW, kD, true>(c, qb, qa, dma);
+      qk_phase<kF16, kNW, kD, kDma>(c, qb, qa, dma);
       mask_scores(c, __builtin_amdgcn_readfirstlane(tmask[tile + 1]));
       u32x4 pa_next[2];
       Softmax sm{c, pa_next, lsum, lsum_r, overflow, {-m_ref[0], -m_ref[1]}, scale_log2, {}};
@@ -870,13 +868,26 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
       pv_softmax_pipeline<kF16, 0, Geo::kRowLists>(o, pa, va, vg0, vg1, sm);
       pa[0] = pa_next[0];
       pa[1] = pa_next[1];
+    };
+    // Steady state: tiles t+2 .. t+kDepth-1 stay in flight past tile t+1.
+    int tile = 0;
+    for (; tile + kDepth < ntiles; ++tile) {
+      wait_tiles<kL>(kDepth - 2);
+      raw_barrier();
+      iteration(std::true_type{}, tile);
+    }
+    // The last kDepth - 1 iterations send nothing: fewer tiles remain behind t+1.
+    for (; tile + 1 < ntiles; ++tile) {
+      wait_tiles<kL>(ntiles - 2 - tile);
+      raw_barrier();
+      iteration(std::false_type{}, tile);
     }
     // The last tile is resident and published; no DMA targets its stage.
     uint32_t va[2];
     stage_v(ntiles - 1, va);
     pv_only<kF16>(o, pa, va);
   }
-  // All LDS reads and the trailing dummy DMAs retire before the ring is reused below.
+  // All LDS reads and DMAs retire before the ring is reused below.
   __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
   // Any wave whose scores outgrew the biased reference: recompute exactly.
   if (tid == 0) *overflow_flag = 0;
