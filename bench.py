@@ -378,6 +378,7 @@ def run_c5(torch, pkg, dev, args, flush, ctx=131072, chunk=4096, H=128, topk=204
     mla_flops = 2.0 * H * topk * (576 + 512) * chunk
     topk_bytes = chunk * ctx * 4 + chunk * topk * 4
     roof_us = (idx_flops / (PEAK_FP8_TFLOPS * 1e12) + topk_bytes / (PEAK_HBM_GBS * 1e9)) * 1e6
+    floor_us = idx_flops / (PEAK_FP8_TFLOPS * 1e12) * 1e6
     del qi, ki, wi, logits, q, kv, out, lse, ws, tws
 
     # Decode step: 32 sequences x 1 query, 128K keys each, paged KV (64-token blocks).
@@ -426,7 +427,11 @@ def run_c5(torch, pkg, dev, args, flush, ctx=131072, chunk=4096, H=128, topk=204
         "indexer_topk_roofline_us": round(roof_us, 1),
         "indexer_topk_frac_roofline": round(roof_us / (t_fused * 1e3), 4),
         "dense_frac_roofline": round(roof_us / ((t_idx + t_topk) * 1e3), 4),
+        # The fused path never writes the logits, so its floor is the fp8 MFMA work alone.
+        "fused_floor_us": round(floor_us, 1),
+        "fused_frac_fp8_floor": round(floor_us / (t_fused * 1e3), 4),
         "indexer_tflops_dense": round(idx_flops / (t_idx * 1e-3) / 1e12, 1),
+        "indexer_frac_fp8_peak": round(idx_flops / (t_idx * 1e-3) / 1e12 / PEAK_FP8_TFLOPS, 4),
         "indexer_causal_pair_frac": round(pairs / (chunk * ctx), 4),
         "fused_equals_dense": fused_same,
         "fused_fallback_rows": fused_fallback,
@@ -795,6 +800,7 @@ def main():
             "topk_frac_hbm": round(topk_gbs / PEAK_HBM_GBS, 4),
             "roofline_us": round((idx_flops / (PEAK_FP8_TFLOPS * 1e12) + topk_bytes / (PEAK_HBM_GBS * 1e9)) * 1e6, 1),
             "fused_us": round(t_fused * 1e3, 1),
+            "fused_frac_fp8_floor": round(idx_flops / (PEAK_FP8_TFLOPS * 1e12) * 1e6 / (t_fused * 1e3), 4),
             "fused_equals_dense": fused_same,
             "fused_fallback_rows": fused_fallback,
         }

@@ -56,6 +56,28 @@ def test_fewer_heads_and_d64(dsa, dev, H):
         _assert_logits(got, ref.indexer_logits(q, k, w, ks))
 
 
+def test_fp8_skewed_head_norms(dsa, dev):
+    # fp8 scores are scaled per head into [-1, 1] before the f16 head reduction.
+    # Head 0 is ~2^14 times larger than the others and negative against every
+    # (all-positive) key, so each logit comes from the small heads alone; with
+    # one scale for the whole token their scores would sink into f16 subnormals
+    # (a CPU model of that arithmetic is off by 7e-2 here; per head, by 9e-4).
+    # Held to 3e-3, a third of the parity bar.
+    B, S1, S2, H, D = 1, 24, 512, 64, 128
+    g = torch.Generator().manual_seed(77)
+    qf = torch.randn(B, S1, H, D, generator=g) * 2.0 ** -6
+    qf[:, :, 0, :] = -448.0
+    q = qf.to(torch.float8_e4m3fn)
+    k, ks = ref.fp8_quantize_per_token(torch.randn(B, S2, D, generator=g).abs())
+    w = torch.randn(B, S1, H, generator=g) / 8
+    got = dsa.indexer_logits(q.to(dev), k.unsqueeze(2).to(dev), w.to(dev), ks.to(dev), sparse_mode=0).cpu()
+    want = ref.indexer_logits(q, k, w, ks, sparse_mode=0)
+    assert torch.all(want.abs() < 10), "head 0 must contribute nothing"
+    rms = want.double().pow(2).mean().sqrt().item()
+    d = (got - want).abs()
+    assert torch.all(d <= 3e-3 * (want.abs() + rms)), f"max err {d.max().item()} (rms {rms})"
+
+
 def test_actual_lengths_and_paged_keys(dsa, dev):
     B, S1, S2, H, D, bs = 3, 40, 700, 64, 128, 64
     q, k, w, ks = _inputs(B, S1, S2, H, D, torch.float8_e4m3fn, seed=12)

@@ -20,12 +20,12 @@
 // one barrier per tile.
 //
 // Head reduction.  fp8: on the matrix cores.  The scores leave the QK MFMA
-// scaled by 2^-9 (its E8M0 A scale; fp8 scores are bounded, so they fit f16),
-// go to f16 and through ReLU in packed form (v_cvt_pk_f16_f32, v_pk_max_f16),
-// and form the B operand of a 16x16x32 f16 MFMA whose A operand holds the
-// token's 32 head weights (f16, times a per-token power of two) in every row:
-// every row of the result is sum_h w[h] ReLU(S[h][key]), accumulated in fp32,
-// two MFMAs per 64 heads.  bf16/fp16 inputs (unbounded scores): fp32 ReLU,
+// scaled per head into [-1, 1] (its E8M0 A scales; fp8 scores are bounded by
+// the row sums of |q|), go to f16 with ReLU as the conversion's clamp
+// (v_cvt_pk_f16_f32 ... clamp), and form the B operand of a 16x16x32 f16 MFMA
+// whose A operand holds the token's 32 head weights (f16, times the heads'
+// scales and a per-token power of two) in every row: every row of the result
+// is sum_h w[h] ReLU(S[h][key]), accumulated in fp32, two MFMAs per 64 heads.  bf16/fp16 inputs (unbounded scores): fp32 ReLU,
 // multiply by w[t, h], sum the lane's 4 head rows, then two cross-lane adds
 // over the 4 row groups.  After four 16-key slices lane l holds key l of the
 // 64-key tile, so each token's logits go out as one coalesced 256-byte store.
@@ -86,21 +86,25 @@ __device__ __forceinline__ void load_operand_lds(Operand<kKind, kD>& op, const u
   for (int c = 0; c < Operand<kKind, kD>::kPieces; ++c) set_piece(op, c, *reinterpret_cast<const u32x4*>(p + 16 * c));
 }
 
-// fp8 scores come out of the MFMA scaled by 2^-9 (the E8M0 block scale of A is
-// 127 - 9): |q . k| <= 128 * 448^2 < 2^25 for e4m3 inputs, so the scaled
-// score stays below 2^16 and fits f16 for the head-reduction MFMA.
-constexpr int kFp8ScoreShift = 9;
-
-template <int kKind, int kD>
-__device__ __forceinline__ f32x4 mfma_qk(const Operand<kKind, kD>& a, const Operand<kKind, kD>& b) {
+// fp8 scores come out of the MFMA scaled per head, by 2^-e_h (the E8M0 scale
+// of A's rows: lane (g, r) holds row r, one 32-element scale block), with e_h
+// chosen so that every score of head h is at most 1: |q . k| <= 448 *
+// sum_i |q[h][i]| for e4m3 keys.  ReLU is then the [0, 1] clamp of the
+// conversion to f16 (one v_cvt_pk_f16_f32 ... clamp per pair, no separate
+// max), the f16 operand of the head-reduction MFMA keeps full precision down to
+// 2^-14 of each head's bound, and the head weights carry the 2^e_h back.
+//
+// scale_a: E8M0 codes of A's scale, byte kOpsel used (fp8 only).
+template <int kKind, int kD, int kOpsel = 0>
+__device__ __forceinline__ f32x4 mfma_qk(const Operand<kKind, kD>& a, const Operand<kKind, kD>& b, int scale_a) {
   f32x4 c = {0.f, 0.f, 0.f, 0.f};
   if constexpr (Operand<kKind, kD>::kWhole) {
-    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a.v, b.v, c, 0, 0, 0, 127 - kFp8ScoreShift, 0, 127);
+    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a.v, b.v, c, 0, 0, kOpsel, scale_a, 0, 127);
   } else if constexpr (kKind == kFp8) {
     // One 16x16x128 fp8 MFMA; a D = 64 row leaves half of each lane's K-slice zero.
     const i32x8 av = {(int)a.p[0].x, (int)a.p[0].y, (int)a.p[0].z, (int)a.p[0].w, 0, 0, 0, 0};
     const i32x8 bv = {(int)b.p[0].x, (int)b.p[0].y, (int)b.p[0].z, (int)b.p[0].w, 0, 0, 0, 0};
-    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 0, 0, 0, 127 - kFp8ScoreShift, 0, 127);
+    c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 0, 0, kOpsel, scale_a, 0, 127);
   } else {
 #pragma unroll
     for (int s = 0; s < Operand<kKind, kD>::kPieces; ++s) {
@@ -127,11 +131,80 @@ __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, r);
 }
 
-// Two scaled scores to f16 (v_cvt_pk_f16_f32), then ReLU on the pair
-// (v_pk_max_f16).
+// Two scaled scores (at most 1) to f16 with ReLU: the min / max pair folds into
+// the clamp bit of v_cvt_pk_f16_f32, whose [0, 1] clamp is ReLU here.
 __device__ __forceinline__ uint32_t relu_f16x2(float a, float b) {
   const f16x2 r = {(_Float16)a, (_Float16)b};
-  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(r, f16x2{(_Float16)0.f, (_Float16)0.f}));
+  const f16x2 lo = {(_Float16)0.f, (_Float16)0.f}, hi = {(_Float16)1.f, (_Float16)1.f};
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_elementwise_max(r, lo), hi));
+}
+
+// The exponent e_h of head h's score scale: 448 * sum_i |q[h][i]| <= 2^e_h (0
+// for a zero row, 25 -- which bounds any e4m3 row, 128 * 448^2 < 2^25 -- for a
+// row holding a NaN).
+__device__ __forceinline__ int head_score_exponent(float l1) {
+  const float bound = 448.f * l1;
+  if (!(bound <= 3.0e38f)) return 25;
+  if (bound == 0.f) return 0;
+  return (int)((__float_as_uint(bound) >> 23) & 0xff) - 127 + 1;  // bound < 2^(E + 1)
+}
+
+// One token's fp8 score scales and reduction weights.  The row sums of |q|
+// come from one MFMA per head block (|q| against a B operand of ones), one
+// block at a time (few registers live).  In: `w` the fp32 weights of heads
+// 16 hb + 4g + i (lane (g, r)), scaled in place to W_h = w_h 2^e_h.  Out:
+// `codes` byte hb = the E8M0 code 127 - e_h of head 16 hb + r (lane (g, r)'s A
+// row); `wa` = W as the f16 A operands of the head-reduction MFMAs (block pairs
+// (0, 1) and (2, 3)), normalised by a power of two so that max |W| lies in
+// [2^14, 2^15); `post` undoes that power at the store.
+template <int kD>
+__device__ __forceinline__ void fp8_head_scales(const Operand<kFp8, kD> (&qa)[4], f32x4 (&w)[4], int nhb, int r,
+                                                uint32_t& codes, u32x4 (&wa)[2], float& post) {
+  Operand<kFp8, kD> ones;
+  if constexpr (Operand<kFp8, kD>::kWhole) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ones.v[i] = 0x38383838;  // e4m3 1.0
+  } else {
+    ones.p[0] = u32x4{0x38383838u, 0x38383838u, 0x38383838u, 0x38383838u};
+  }
+  float m = 0.f;
+  codes = 0;
+#pragma unroll
+  for (int hb = 0; hb < 4; ++hb) {
+    f32x4 l1 = {0.f, 0.f, 0.f, 0.f};
+    if (hb < nhb) {
+      Operand<kFp8, kD> aq;
+      if constexpr (Operand<kFp8, kD>::kWhole) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) aq.v[i] = qa[hb].v[i] & 0x7f7f7f7f;
+      } else {
+        aq.p[0] = qa[hb].p[0] & 0x7f7f7f7fu;
+      }
+      l1 = mfma_qk<kFp8, kD>(aq, ones, 127);  // lane (g, r): rows 4g + i = heads 16 hb + 4g + i
+    }
+    // Lane (g, r) scales A row r: head 16 hb + r, component r % 4 of lane group r / 4.
+    int v = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = head_score_exponent(l1[i]);
+      w[hb][i] *= __uint_as_float((uint32_t)(127 + e) << 23);
+      m = fmaxf(m, fabsf(w[hb][i]));
+      const int x = __shfl(e, 16 * (r >> 2), kWave);
+      v = (r & 3) == i ? x : v;
+    }
+    codes |= (uint32_t)(127 - v) << (8 * hb);
+  }
+  m = fmaxf(m, __shfl_xor(m, 16, kWave));
+  m = fmaxf(m, __shfl_xor(m, 32, kWave));
+  // m = 2^e * f with f in [1, 2): weights x 2^(14 - e), results x 2^(e - 14).
+  const int e = m > 0.f ? (int)((__float_as_uint(m) >> 23) & 0xff) - 127 : 0;
+  const float up = __uint_as_float((uint32_t)(127 + 14 - e) << 23);
+  post = __uint_as_float((uint32_t)(127 + e - 14) << 23);
+#pragma unroll
+  for (int pr = 0; pr < 2; ++pr)
+    wa[pr] = u32x4{pack_f16x2(w[2 * pr].x * up, w[2 * pr].y * up), pack_f16x2(w[2 * pr].z * up, w[2 * pr].w * up),
+                   pack_f16x2(w[2 * pr + 1].x * up, w[2 * pr + 1].y * up),
+                   pack_f16x2(w[2 * pr + 1].z * up, w[2 * pr + 1].w * up)};
 }
 
 // B operand of the head-reduction MFMA for head blocks hb0, hb1: lane (g, r)
@@ -299,14 +372,13 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
   }
 
   // Stationary q operands and head weights.  fp8: the weights become the A
-  // operands of the head-reduction MFMAs -- every row of A is w (f16), K =
+  // operands of the head-reduction MFMAs -- every row of A is W (f16), K =
   // 8g + i standing for head 16*hb0 + 4g + i (i < 4) or 16*hb1 + 4g + i - 4 of
-  // the block pair (hb0, hb1) = (0, 1) or (2, 3), as in relu_operand -- scaled
-  // per token by a power of two that puts max |w| in [2^14, 2^15); post[j]
-  // undoes that scale and the score scale at the store.
+  // the block pair (hb0, hb1) = (0, 1) or (2, 3), as in relu_operand -- built
+  // with the per-head score scales once q has arrived (fp8_head_scales).
   constexpr bool kMfmaSum = kKind == kFp8;
   Operand<kKind, kD> qa[kTokPW][4];
-  f32x4 wv[kMfmaSum ? 1 : kTokPW][4];
+  f32x4 wv[kTokPW][4];
   u32x4 wa[kTokPW][2];
   float post[kTokPW];
 #pragma unroll
@@ -333,27 +405,9 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
                        h0 + 3 < a.H ? wp[3] : 0.f};
       }
     }
-    if constexpr (kMfmaSum) {
-      float m = 0.f;
+    post[j] = 1.f;
 #pragma unroll
-      for (int hb = 0; hb < 4; ++hb)
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(wt[hb].x), fabsf(wt[hb].y)), fmaxf(fabsf(wt[hb].z), fabsf(wt[hb].w))));
-      m = fmaxf(m, __shfl_xor(m, 16, kWave));
-      m = fmaxf(m, __shfl_xor(m, 32, kWave));
-      // m = 2^e * f with f in [1, 2): weights x 2^(14 - e), results x 2^(e - 14 + shift).
-      const int e = m > 0.f ? (int)((__float_as_uint(m) >> 23) & 0xff) - 127 : 0;
-      const float up = __uint_as_float((uint32_t)(127 + 14 - e) << 23);
-      post[j] = __uint_as_float((uint32_t)(127 + e - 14 + kFp8ScoreShift) << 23);
-#pragma unroll
-      for (int pr = 0; pr < 2; ++pr)
-        wa[j][pr] = u32x4{pack_f16x2(wt[2 * pr].x * up, wt[2 * pr].y * up), pack_f16x2(wt[2 * pr].z * up, wt[2 * pr].w * up),
-                          pack_f16x2(wt[2 * pr + 1].x * up, wt[2 * pr + 1].y * up),
-                          pack_f16x2(wt[2 * pr + 1].z * up, wt[2 * pr + 1].w * up)};
-    } else {
-      post[j] = 1.f;
-#pragma unroll
-      for (int hb = 0; hb < 4; ++hb) wv[j][hb] = wt[hb];
-    }
+    for (int hb = 0; hb < 4; ++hb) wv[j][hb] = wt[hb];
   }
 
   const int tile_end = min(key1, max_valid);  // keys at or past this are -inf for every token
@@ -415,10 +469,17 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
   using Slot0 = std::integral_constant<int, 0>;
   using Slot1 = std::integral_constant<int, 1>;
 
-  if (ntiles > 0) {
-    fetch(Slot0{}, 0);
-    commit(Slot0{}, 0);
+  // fp8: the per-head score scales and the scaled weights, computed once q has
+  // arrived -- after the first key tile was requested, so the two latencies
+  // overlap, and before the second, which keeps fewer registers live.
+  uint32_t qscale[kTokPW];
+  if (ntiles > 0) fetch(Slot0{}, 0);
+#pragma unroll
+  for (int j = 0; j < kTokPW; ++j) {
+    qscale[j] = 0x7f7f7f7fu;
+    if constexpr (kMfmaSum) fp8_head_scales<kD>(qa[j], wv[j], nhb, r, qscale[j], wa[j], post[j]);
   }
+  if (ntiles > 0) commit(Slot0{}, 0);
   if (ntiles > 1) fetch(Slot1{}, 1);
   __syncthreads();
 
@@ -445,8 +506,11 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
 #pragma unroll
           for (int pr = 0; pr < 2; ++pr) {
             if (2 * pr < nhb) {
-              const f32x4 c0 = mfma_qk<kKind, kD>(qa[j][2 * pr], kb);
-              const f32x4 c1 = 2 * pr + 1 < nhb ? mfma_qk<kKind, kD>(qa[j][2 * pr + 1], kb) : f32x4{0.f, 0.f, 0.f, 0.f};
+              const f32x4 c0 = pr == 0 ? mfma_qk<kKind, kD, 0>(qa[j][0], kb, qscale[j])
+                                       : mfma_qk<kKind, kD, 2>(qa[j][2], kb, qscale[j]);
+              const f32x4 c1 = 2 * pr + 1 >= nhb ? f32x4{0.f, 0.f, 0.f, 0.f}
+                               : pr == 0        ? mfma_qk<kKind, kD, 1>(qa[j][1], kb, qscale[j])
+                                                : mfma_qk<kKind, kD, 3>(qa[j][3], kb, qscale[j]);
               d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, wa[j][pr]),
                                                          __builtin_bit_cast(f16x8, relu_operand(c0, c1)), d, 0, 0, 0);
             }
@@ -457,7 +521,7 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
 #pragma unroll
           for (int hb = 0; hb < 4; ++hb) {
             if (hb < nhb) {
-              const f32x4 c = mfma_qk<kKind, kD>(qa[j][hb], kb);
+              const f32x4 c = mfma_qk<kKind, kD>(qa[j][hb], kb, 127);
               float& acc = acc2[hb & 1];
               acc = fmaf(wv[j][hb].x, relu(c.x), acc);
               acc = fmaf(wv[j][hb].y, relu(c.y), acc);
@@ -548,8 +612,12 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
   }
 }
 
+// fp8 with D = 128 is held to three waves per SIMD (the compiler would
+// otherwise trade a wave for a deeper operand prefetch).
 template <int kKind, int kD, int kTokPW, int kNhb, bool kPaged, int kMode>
-__global__ __launch_bounds__(kIdxThreads) void indexer_logits_kernel(IdxArgs a) {
+__global__ __launch_bounds__(kIdxThreads)
+__attribute__((amdgpu_waves_per_eu(kKind == kFp8 && kD == 128 ? 3 : 1, kKind == kFp8 && kD == 128 ? 3 : 8)))
+void indexer_logits_kernel(IdxArgs a) {
   indexer_body<kKind, kD, kTokPW, kNhb, kPaged, kMode>(a);
 }
 
