@@ -155,17 +155,30 @@ def cpu_baseline_prefill(torch, q, kv, idx, budget_s=12.0):
 
 
 def _cpu_model():
-    """The host CPU's model name (first /proc/cpuinfo entry)."""
+    """The host CPU as /proc/cpuinfo names it: model name, family / model / stepping (which tell the
+    generation where a VM reports only "AMD EPYC"), clock, logical CPUs and AVX-512 support."""
+    info = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if not line.strip():
+                    break  # first processor entry only
+                key, _, val = line.partition(":")
+                info[key.strip()] = val.strip()
     except OSError:
         pass
     import platform
 
-    return platform.processor() or "unknown"
+    name = info.get("model name") or platform.processor() or "unknown"
+    fields = [name]
+    if "cpu family" in info:
+        fields.append(f"family {info['cpu family']} model {info.get('model', '?')} stepping {info.get('stepping', '?')}")
+    if "cpu MHz" in info:
+        fields.append(f"{float(info['cpu MHz']):.0f} MHz")
+    fields.append(f"{os.cpu_count()} logical CPUs")
+    if "flags" in info:
+        fields.append("avx512f" if "avx512f" in info["flags"].split() else "no avx512f")
+    return ", ".join(fields)
 
 
 def cpu_baselines_other(torch):
