@@ -150,15 +150,19 @@ __device__ __forceinline__ int head_score_exponent(float l1) {
 }
 
 // One token's fp8 score scales and reduction weights.  The row sums of |q|
-// come from one MFMA per head block (|q| against a B operand of ones), one
-// block at a time (few registers live).  In: `w` the fp32 weights of heads
-// 16 hb + 4g + i (lane (g, r)), scaled in place to W_h = w_h 2^e_h.  Out:
-// `codes` byte hb = the E8M0 code 127 - e_h of head 16 hb + r (lane (g, r)'s A
-// row); `wa` = W as the f16 A operands of the head-reduction MFMAs (block pairs
-// (0, 1) and (2, 3)), normalised by a power of two so that max |W| lies in
-// [2^14, 2^15); `post` undoes that power at the store.
-template <int kD>
-__device__ __forceinline__ void fp8_head_scales(const Operand<kFp8, kD> (&qa)[4], f32x4 (&w)[4], int nhb, int r,
+// come from MFMAs of |q| against ones, one head block at a time (few registers
+// live): with |q| as A, lane (g, r) receives the sums of heads 16 hb + 4g + i
+// (rows 4g + i); with |q| as B -- the same registers, the operand layouts
+// mirror each other -- it receives the sum of head 16 hb + r (column r) in
+// every component.  In: `w` the fp32 weights of heads 16 hb + 4g + i (lane
+// (g, r)), scaled in place to W_h = w_h 2^e_h.  Out: `codes` byte hb = the E8M0
+// code 127 - e_h of head 16 hb + r (lane (g, r)'s A row); `wa` = W as the f16
+// A operands of the head-reduction MFMAs (block pairs (0, 1) and (2, 3)),
+// normalised by a power of two so that max |W| lies in [2^14, 2^15); `post`
+// undoes that power at the store.  kFixed: every e_h = 25, which bounds any
+// e4m3 row (the sample pass, whose logits only place the filter thresholds).
+template <int kD, bool kFixed>
+__device__ __forceinline__ void fp8_head_scales(const Operand<kFp8, kD> (&qa)[4], f32x4 (&w)[4], int nhb,
                                                 uint32_t& codes, u32x4 (&wa)[2], float& post) {
   Operand<kFp8, kD> ones;
   if constexpr (Operand<kFp8, kD>::kWhole) {
@@ -171,8 +175,8 @@ __device__ __forceinline__ void fp8_head_scales(const Operand<kFp8, kD> (&qa)[4]
   codes = 0;
 #pragma unroll
   for (int hb = 0; hb < 4; ++hb) {
-    f32x4 l1 = {0.f, 0.f, 0.f, 0.f};
-    if (hb < nhb) {
+    f32x4 rows = {0.f, 0.f, 0.f, 0.f}, cols = {0.f, 0.f, 0.f, 0.f};
+    if (!kFixed && hb < nhb) {
       Operand<kFp8, kD> aq;
       if constexpr (Operand<kFp8, kD>::kWhole) {
 #pragma unroll
@@ -180,19 +184,16 @@ __device__ __forceinline__ void fp8_head_scales(const Operand<kFp8, kD> (&qa)[4]
       } else {
         aq.p[0] = qa[hb].p[0] & 0x7f7f7f7fu;
       }
-      l1 = mfma_qk<kFp8, kD>(aq, ones, 127);  // lane (g, r): rows 4g + i = heads 16 hb + 4g + i
+      rows = mfma_qk<kFp8, kD>(aq, ones, 127);
+      cols = mfma_qk<kFp8, kD>(ones, aq, 127);
     }
-    // Lane (g, r) scales A row r: head 16 hb + r, component r % 4 of lane group r / 4.
-    int v = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int e = head_score_exponent(l1[i]);
+      const int e = kFixed ? 25 : head_score_exponent(rows[i]);
       w[hb][i] *= __uint_as_float((uint32_t)(127 + e) << 23);
       m = fmaxf(m, fabsf(w[hb][i]));
-      const int x = __shfl(e, 16 * (r >> 2), kWave);
-      v = (r & 3) == i ? x : v;
     }
-    codes |= (uint32_t)(127 - v) << (8 * hb);
+    codes |= (uint32_t)(127 - (kFixed ? 25 : head_score_exponent(cols.x))) << (8 * hb);
   }
   m = fmaxf(m, __shfl_xor(m, 16, kWave));
   m = fmaxf(m, __shfl_xor(m, 32, kWave));
@@ -477,7 +478,7 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
 #pragma unroll
   for (int j = 0; j < kTokPW; ++j) {
     qscale[j] = 0x7f7f7f7fu;
-    if constexpr (kMfmaSum) fp8_head_scales<kD>(qa[j], wv[j], nhb, r, qscale[j], wa[j], post[j]);
+    if constexpr (kMfmaSum) fp8_head_scales<kD, kMode == kModeSample>(qa[j], wv[j], nhb, qscale[j], wa[j], post[j]);
   }
   if (ntiles > 0) commit(Slot0{}, 0);
   if (ntiles > 1) fetch(Slot1{}, 1);
