@@ -97,6 +97,28 @@ def test_masked_slots_batches_and_heads(dsa, dev, dtype):
     assert torch.count_nonzero(out[0, 0]) == 0
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_decode_rows_masked_slots(dsa, dev, dtype):
+    """At most 8 query rows with at most 192 slots each: the decode-shaped kernel (heads across
+    workgroups, slots across the waves); -1 and out-of-range slots, an all-empty row, a block of
+    16 slots with none valid."""
+    print(f"sparse_attn decode rows b=2 m=3 topk=150 {dtype}", flush=True)
+    q, kv, sink, idx = _inputs(2, 3, 300, 32, 512, 150, dtype, 46)
+    g = torch.Generator().manual_seed(47)
+    drop = torch.rand(idx.shape, generator=g) < 0.3
+    idx = torch.where(drop, torch.full_like(idx, -1), idx)
+    idx[0, 1, :] = -1                      # no valid slot: out 0, lse = sink
+    idx[1, 0, 16:32] = -1                  # a whole 16-slot block masked
+    idx[1, 2, 7] = 300                     # past n: masked
+    scale = 0.05
+    for sk in (sink, None):
+        out = _run(dsa, dev, q, kv, sk, idx, scale)
+        want, want_lse = ref.sparse_attn_sink(q, kv, sk, idx, scale)
+        torch.testing.assert_close(out, want, rtol=1e-2, atol=1e-2)
+        torch.testing.assert_close(_lse(dsa, dev, q, kv, sk, idx, scale), want_lse, rtol=1e-3, atol=1e-3)
+        assert torch.count_nonzero(out[0, 1]) == 0
+
+
 def test_split_path_and_no_sink(dsa, dev):
     """Few rows with long index lists take the split + combine path (sinks join in the combine)."""
     print("sparse_attn split path b=2 m=1 topk=4096", flush=True)

@@ -171,20 +171,21 @@ def test_bsnd_padded_rows_and_hca(dsa, dev):
     assert torch.all(oc[1, 13:] == 0) and torch.all(lc[1, 13:] == 0)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("scenario", ["swa", "hca"])
-def test_bsnd_padded_decode_rows(dsa, dev, scenario):
-    # Decode-shaped padded BSND rows: two batches of 3 rows, the second using 1
-    # of them (padded rows: out 0, lse 0), few enough rows that the slot lists
-    # are split across workgroups and the combine zeroes the padded rows.
+def test_bsnd_padded_decode_rows(dsa, dev, scenario, dtype):
+    # Decode-shaped padded BSND rows (at most 8 rows, at most 192 slots: the
+    # decode kernel, heads across workgroups and slots across waves): two
+    # batches of 3 rows, the second using 1 of them (padded rows: out 0, lse 0).
     B, S, H, D, bs, ratio = 2, 3, 32, 512, 32, 8
     kv_lens = [300, 2]
     g = torch.Generator().manual_seed(18)
-    q = torch.randn((B, S, H, D), generator=g).to(torch.bfloat16)
-    ori, ori_bt = _paged(kv_lens, bs, 12, D, -1, 1, torch.bfloat16, g)
+    q = torch.randn((B, S, H, D), generator=g).to(dtype)
+    ori, ori_bt = _paged(kv_lens, bs, 12, D, -1, 1, dtype, g)
     cmp = cmp_bt = None
     r = None
     if scenario == "hca":
-        cmp, cmp_bt = _paged([max(n // ratio, 1) for n in kv_lens], bs, 4, D, -1, 1, torch.bfloat16, g)
+        cmp, cmp_bt = _paged([max(n // ratio, 1) for n in kv_lens], bs, 4, D, -1, 1, dtype, g)
         r = ratio
     sinks = torch.randn(H, generator=g)
     cu = [0, 3, 4]
@@ -193,15 +194,15 @@ def test_bsnd_padded_decode_rows(dsa, dev, scenario):
     qp = torch.cat([q[0], q[1, :1]])
     wo, wl = _want(qp, cu, kv_lens, ori, ori_bt, sinks, 0.05, cmp=cmp, cmp_bt=cmp_bt, ratio=r, win_left=40)
     oc, lc = out.cpu(), lse.cpu()
-    _check(torch.cat([oc[0], oc[1, :1]]), torch.cat([lc[0], lc[1, :1]]), wo, wl, torch.bfloat16)
+    _check(torch.cat([oc[0], oc[1, :1]]), torch.cat([lc[0], lc[1, :1]]), wo, wl, dtype)
     assert torch.all(oc[1, 1:] == 0) and torch.all(lc[1, 1:] == 0)
 
 
 @pytest.mark.parametrize("scenario", ["swa", "hca", "csa"])
 def test_decode_rows_split_path(dsa, dev, scenario):
     # One query row per sequence against 8193 keys (the reference benchmark's
-    # decode shape, here B = 3): few rows, so the slot list is split across
-    # workgroups and the sinks join in the combine.
+    # decode shape, here B = 3): swa (128 slots) and hca (192) take the decode
+    # kernel, csa (640 slots) the split gather kernel whose combine adds the sinks.
     B, H, D, K, bs = 3, 64, 512, 512, 128
     ratio = 128 if scenario == "hca" else 4
     kv_lens = [8193, 4000, 129]

@@ -131,6 +131,271 @@ __global__ __launch_bounds__(256) void index_row_lists_kernel(const int32_t* __r
   if (lane == 0) count[t] = K;
 }
 
+// ---------------------------------------------------------------------------
+// Decode-shaped row lists (at most kDecodeRows query rows): one workgroup per
+// (query row, 16 heads), its four waves splitting the row's slots into
+// 16-slot blocks (wave w takes blocks w, w + 4, ...), each with its own online
+// softmax and O, merged in LDS at the end.  No split partials and no combine
+// launch: such a call is a chain of latencies, and this removes a launch and
+// a global round trip from it.
+//
+// A block's 16 rows (1 KB each, K = V) go to the wave's 16 KB of LDS by DMA,
+// one row per instruction, lane l carrying 16-byte chunk l ^ 2u of row u (so
+// the Q K^T operand reads, 16 rows at one chunk, fall on distinct banks).
+// S^T = K Q^T by 16x16x32 MFMAs (lane (g, r): keys 4g + i of head r), then
+// O^T += V^T P^T by 16x16x16 MFMAs whose V^T operand comes from
+// ds_read_b64_tr_b16 and whose P operand is the lane's own four scores.  As in
+// the gather kernel, O is normalised by the sum of the 16-bit-rounded P, the
+// LSE by the exact sum, and the sinks join the denominator.
+constexpr int kDecBlk = 16;
+constexpr int64_t kDecodeRows = 8;
+// ... and at most this many slots per row: three blocks per wave.  Longer lists
+// (a csa selection) go through the split gather kernel, which keeps several
+// tiles in flight per workgroup where this kernel loads one block at a time.
+constexpr int64_t kDecodeMaxSlots = 12 * kDecBlk;
+constexpr int kDecWaveLds = kDecBlk * 1024;          // a wave's block of rows
+constexpr int kDecOBytes = 4 * 512 * 16 * 4;          // the four waves' O^T, fp32
+constexpr int kDecLds = kDecOBytes + 3 * 4 * 16 * 4;  // + m, l, rounded l per wave and head
+
+struct DecArgs {
+  const uint16_t* q;      // [T, H, 512]
+  const uint8_t* kv;      // rows of 1 KB
+  const uint8_t* kv2;     // rows tagged kCmpTag, or null
+  const int32_t* rows;    // [T, cap]
+  const int32_t* count;   // [T]; -1: padded row
+  const float* sinks;     // [H] or null
+  uint16_t* out;          // [T, H, 512]
+  float* lse;             // [T, H]
+  int T, H, cap;
+  float scale_log2;
+};
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) void dec_lds_void;
+typedef const __attribute__((address_space(1))) void dec_gbl_void;
+
+template <bool kF16>
+__device__ __forceinline__ f32x4 dec_mfma_qk(const u32x4& a, const u32x4& b, const f32x4& c) {
+  if constexpr (kF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+template <bool kF16>
+__device__ __forceinline__ f32x4 dec_mfma_pv(const s16x4& a, const s16x4& b, const f32x4& c) {
+  if constexpr (kF16)
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+
+// One 16-bit value of p (round to nearest even) and its value back in fp32.
+template <bool kF16>
+__device__ __forceinline__ short dec_round(float p, float& back) {
+  if constexpr (kF16) {
+    const _Float16 h = (_Float16)p;
+    back = (float)h;
+    return __builtin_bit_cast(short, h);
+  } else {
+    const __bf16 h = (__bf16)p;
+    back = (float)h;
+    return __builtin_bit_cast(short, h);
+  }
+}
+
+template <bool kF16>
+__global__ __launch_bounds__(256) void v4_decode_rows_kernel(DecArgs a) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int t = blockIdx.x;
+  const int h0 = blockIdx.y * 16;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int r = lane & 15, g = lane >> 4;
+  const int cnt_raw = a.count[t];
+  if (cnt_raw < 0) {  // padded query row: out 0, lse 0 (workgroup-uniform)
+    for (int e = tid; e < 16 * 64; e += 256)
+      *reinterpret_cast<u32x4*>(a.out + ((int64_t)t * a.H + h0 + e / 64) * 512 + 8 * (e % 64)) = u32x4{0, 0, 0, 0};
+    if (tid < 16) a.lse[(int64_t)t * a.H + h0 + tid] = 0.f;
+    return;
+  }
+  const int cnt = min(cnt_raw, a.cap);
+  // Q^T operands: head h0 + r, dims 32 st + 8g .. +7.
+  u32x4 qb[16];
+  const uint16_t* qp = a.q + ((int64_t)t * a.H + h0 + r) * 512 + 8 * g;
+#pragma unroll
+  for (int st = 0; st < 16; ++st) qb[st] = *reinterpret_cast<const u32x4*>(qp + 32 * st);
+  f32x4 o[32];
+#pragma unroll
+  for (int c = 0; c < 32; ++c) o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -__builtin_huge_valf(), l = 0.f, lr = 0.f;
+  uint8_t* buf = lds + wave * kDecWaveLds;
+  const int32_t* rowl = a.rows + (int64_t)t * a.cap;
+  const int nblk = (cnt + kDecBlk - 1) / kDecBlk;
+  auto load = [&](int blk, uint8_t* bp) -> uint32_t {
+    const int s0 = blk * kDecBlk;
+    // Lane u < 16 holds slot s0 + u's row; invalid slots read row 0 (their scores are masked).
+    const int slot = s0 + (lane & 15);
+    const int32_t rr = rowl[min(slot, cnt - 1)];
+    const bool valid = slot < cnt && rr >= 0;
+    const uint32_t vmask = (uint32_t)__builtin_amdgcn_ballot_w64(valid && lane < 16);
+#pragma unroll
+    for (int u = 0; u < kDecBlk; ++u) {
+      const int ru = __builtin_amdgcn_readlane(valid ? rr : 0, u);
+      const uint8_t* base = (ru & kCmpTag) ? a.kv2 : a.kv;
+      const uint8_t* src = base + (int64_t)(ru & ~kCmpTag) * 1024 + 16 * (lane ^ (2 * u));
+      __builtin_amdgcn_global_load_lds((dec_gbl_void*)src, (dec_lds_void*)(bp + u * 1024), 16, 0, 0);
+    }
+    return vmask;
+  };
+  auto process = [&](const uint8_t* bp, uint32_t vmask) {
+    // S^T = K Q^T: A = K rows r (chunk 4 st + g), B = Q^T.
+    f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 16; ++st) {
+      const u32x4 kr = *reinterpret_cast<const u32x4*>(bp + r * 1024 + 16 * ((4 * st + g) ^ (2 * r)));
+      sc = dec_mfma_qk<kF16>(kr, qb[st], sc);
+    }
+    float s2[4], bm = -__builtin_huge_valf();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s2[i] = ((vmask >> (4 * g + i)) & 1u) ? sc[i] * a.scale_log2 : -__builtin_huge_valf();
+      bm = fmaxf(bm, s2[i]);
+    }
+    bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
+    bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
+    const float mn = fmaxf(m, bm);
+    // Both -inf (nothing valid yet): alpha 1 and every p 0, with no inf - inf.
+    const float alpha = m == mn ? 1.f : fast_exp2(m - mn);
+    m = mn;
+    l *= alpha;
+    lr *= alpha;
+#pragma unroll
+    for (int c = 0; c < 32; ++c) o[c] *= alpha;
+    s16x4 pb;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float p = s2[i] == -__builtin_huge_valf() ? 0.f : fast_exp2(s2[i] - mn);
+      float back;
+      pb[i] = dec_round<kF16>(p, back);
+      l += p;
+      lr += back;
+    }
+    // O^T += V^T P^T: lane (g, L) feeds row 4g + L / 4, columns 16 c + 4 (L % 4) .. +3.
+    const int vrow = 4 * g + (r >> 2);
+#pragma unroll
+    for (int c = 0; c < 32; ++c) {
+      const int chunk = 2 * c + ((r & 3) >> 1);
+      const s16x4 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_s16x4*)(bp + vrow * 1024 + 16 * (chunk ^ (2 * vrow)) + 8 * (r & 1)));
+      o[c] = dec_mfma_pv<kF16>(va, pb, o[c]);
+    }
+  };
+  for (int blk = wave; blk < nblk; blk += 4) {
+    const uint32_t vm = load(blk, buf);
+    __builtin_amdgcn_s_waitcnt(0);  // the block is in LDS
+    process(buf, vm);
+  }
+  l += __shfl_xor(l, 16, kWave);
+  l += __shfl_xor(l, 32, kWave);
+  lr += __shfl_xor(lr, 16, kWave);
+  lr += __shfl_xor(lr, 32, kWave);
+  __syncthreads();  // every wave is done with its block buffer
+  float* ow = reinterpret_cast<float*>(lds) + wave * (512 * 16);
+#pragma unroll
+  for (int c = 0; c < 32; ++c)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ow[(16 * c + 4 * g + i) * 16 + r] = o[c][i];
+  float* stats = reinterpret_cast<float*>(lds + kDecOBytes);  // [3][4 waves][16 heads]
+  if (g == 0) {
+    stats[wave * 16 + r] = m;
+    stats[64 + wave * 16 + r] = l;
+    stats[128 + wave * 16 + r] = lr;
+  }
+  __syncthreads();
+  // Merge: thread handles head e % 16, columns 8 (e / 16) .. +7.
+  const float* of = reinterpret_cast<const float*>(lds);
+  for (int e = tid; e < 16 * 64; e += 256) {
+    const int h = e & 15, c8 = 8 * (e >> 4);
+    float mw[4], mx = -__builtin_huge_valf();
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      mw[w] = stats[w * 16 + h];
+      mx = fmaxf(mx, mw[w]);
+    }
+    const float sink2 = a.sinks ? a.sinks[h0 + h] * 1.4426950408889634f : -__builtin_huge_valf();
+    const float mm = fmaxf(mx, sink2);
+    float den = 0.f, den_r = 0.f, wgt[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      wgt[w] = mm == -__builtin_huge_valf() ? 0.f : fast_exp2(mw[w] - mm);
+      den += stats[64 + w * 16 + h] * wgt[w];
+      den_r += stats[128 + w * 16 + h] * wgt[w];
+    }
+    const float es = a.sinks && mm != -__builtin_huge_valf() ? fast_exp2(sink2 - mm) : 0.f;
+    den += es;
+    den_r += es;
+    const float inv = den_r > 0.f ? 1.f / den_r : 0.f;
+    uint32_t pk[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float v2[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int col = c8 + 2 * j + k;
+        float acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) acc += of[w * (512 * 16) + col * 16 + h] * wgt[w];
+        v2[k] = acc * inv;
+      }
+      if constexpr (kF16) {
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        const h2 hv = {(_Float16)v2[0], (_Float16)v2[1]};
+        pk[j] = __builtin_bit_cast(uint32_t, hv);
+      } else {
+        pk[j] = pack_bf16x2(v2[0], v2[1]);
+      }
+    }
+    *reinterpret_cast<u32x4*>(a.out + ((int64_t)t * a.H + h0 + h) * 512 + c8) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+    if (c8 == 0)
+      a.lse[(int64_t)t * a.H + h0 + h] = den > 0.f ? (mm + fast_log2(den)) * 0.69314718055994531f : -__builtin_huge_valf();
+  }
+}
+
+// Caller: T <= kDecodeRows, H % 16 == 0, rows / count from a row-list kernel on `stream`.
+static hipError_t launch_v4_decode_rows(int is_fp16, const void* q, const void* kv, const void* kv2,
+                                        const int32_t* rows, const int32_t* count, int64_t T, int64_t H, int64_t cap,
+                                        const float* sinks, float sm_scale, void* out, float* lse,
+                                        hipStream_t stream) {
+  DecArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.kv = static_cast<const uint8_t*>(kv);
+  a.kv2 = static_cast<const uint8_t*>(kv2);
+  a.rows = rows;
+  a.count = count;
+  a.sinks = sinks;
+  a.out = static_cast<uint16_t*>(out);
+  a.lse = lse;
+  a.T = (int)T;
+  a.H = (int)H;
+  a.cap = (int)cap;
+  a.scale_log2 = sm_scale * 1.4426950408889634f;
+  const dim3 grid((unsigned)T, (unsigned)(H / 16));
+  if (is_fp16) {
+    const hipError_t e = set_dynamic_lds_once<v4_decode_rows_kernel<true>>(kDecLds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(v4_decode_rows_kernel<true>, grid, dim3(256), kDecLds, stream, a);
+  } else {
+    const hipError_t e = set_dynamic_lds_once<v4_decode_rows_kernel<false>>(kDecLds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(v4_decode_rows_kernel<false>, grid, dim3(256), kDecLds, stream, a);
+  }
+  return hipGetLastError();
+}
+
 static size_t v4_lists_bytes(int64_t T, int64_t cap) {
   return ((size_t)T * (cap + 1) * sizeof(int32_t) + 255) & ~size_t(255);
 }
@@ -176,6 +441,9 @@ hipError_t launch_sparse_flash_mla(int is_fp16, const void* q, int64_t T, int64_
   hipLaunchKernelGGL(v4_row_lists_kernel, dim3((unsigned)((T + per_block - 1) / per_block)), dim3(256), 0, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if (T <= kDecodeRows && cap <= kDecodeMaxSlots)
+    return launch_v4_decode_rows(is_fp16, q, ori_kv, cmp_kv, a.rows, a.count, T, H, cap, sinks, sm_scale, out, lse,
+                                 stream);
   void* mla_ws = static_cast<uint8_t*>(workspace) + v4_lists_bytes(T, cap);
   return launch_sparse_mla_rows(is_fp16, q, ori_kv, cmp_kv, a.rows, a.count, T, H, cap, sinks, sm_scale, out, lse,
                                 mla_ws, stream);
@@ -196,6 +464,8 @@ hipError_t launch_sparse_attn_sink(int is_fp16, const void* q, const void* kv, c
                      idx, (int)T, (int)M, (int)N, (int)K, rows, count);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if (T <= kDecodeRows && K <= kDecodeMaxSlots)
+    return launch_v4_decode_rows(is_fp16, q, kv, nullptr, rows, count, T, H, K, sinks, sm_scale, out, lse, stream);
   void* mla_ws = static_cast<uint8_t*>(workspace) + v4_lists_bytes(T, K);
   return launch_sparse_mla_rows(is_fp16, q, kv, nullptr, rows, count, T, H, K, sinks, sm_scale, out, lse, mla_ws,
                                 stream);
