@@ -137,7 +137,9 @@ __global__ __launch_bounds__(256) void index_row_lists_kernel(const int32_t* __r
 // 16-slot blocks (wave w takes blocks w, w + 4, ...), each with its own online
 // softmax and O, merged in LDS at the end.  No split partials and no combine
 // launch: such a call is a chain of latencies, and this removes a launch and
-// a global round trip from it.
+// a global round trip from it.  For swa and hca rows the kernel also derives
+// the row lists itself (the window, then the compressed rows below the row's
+// threshold, through the block tables), so the call is this one launch.
 //
 // A block's 16 rows (1 KB each, K = V) go to the wave's 16 KB of LDS by DMA,
 // one row per instruction, lane l carrying 16-byte chunk l ^ 2u of row u (so
@@ -168,6 +170,10 @@ struct DecArgs {
   float* lse;             // [T, H]
   int T, H, cap;
   float scale_log2;
+  // swa / hca lists derived here instead (inl): the row's batch, window and
+  // compressed rows, as v4_row_lists_kernel computes them.
+  int inl;
+  V4Args v4;
 };
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -215,7 +221,23 @@ __global__ __launch_bounds__(256) void v4_decode_rows_kernel(DecArgs a) {
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int r = lane & 15, g = lane >> 4;
-  const int cnt_raw = a.count[t];
+  int cnt_raw, vb = 0, vnw = 0, vw0 = 0;
+  const V4Args& v = a.v4;
+  if (a.inl) {  // workgroup-uniform
+    for (int i = 1; i < v.B; ++i) vb = v.q_start[i] <= t ? i : vb;
+    const int sq = t - v.q_start[vb];
+    const int qlb = v.q_len[vb];
+    if (sq < 0 || sq >= qlb) {
+      cnt_raw = -1;
+    } else {
+      const int sg = v.kv_len[vb] - qlb + sq;  // position of this row in its sequence
+      vnw = sg >= 0 ? min(v.win_left, sg) + 1 : 0;
+      vw0 = sg - vnw + 1;
+      cnt_raw = vnw + ((v.mode == 2 && sg >= 0) ? min((sg + 1) / v.cmp_ratio, v.max_cmp) : 0);
+    }
+  } else {
+    cnt_raw = a.count[t];
+  }
   if (cnt_raw < 0) {  // padded query row: out 0, lse 0 (workgroup-uniform)
     for (int e = tid; e < 16 * 64; e += 256)
       *reinterpret_cast<u32x4*>(a.out + ((int64_t)t * a.H + h0 + e / 64) * 512 + 8 * (e % 64)) = u32x4{0, 0, 0, 0};
@@ -239,7 +261,24 @@ __global__ __launch_bounds__(256) void v4_decode_rows_kernel(DecArgs a) {
     const int s0 = blk * kDecBlk;
     // Lane u < 16 holds slot s0 + u's row; invalid slots read row 0 (their scores are masked).
     const int slot = s0 + (lane & 15);
-    const int32_t rr = rowl[min(slot, cnt - 1)];
+    int32_t rr;
+    if (a.inl) {
+      // Window position vw0 + i, then compressed row i - vnw; both lookups go out
+      // (from clamped entries), the slot picks one.
+      const int i = min(slot, cnt - 1);
+      const int pw = max(vw0 + i, 0), ew = pw / v.ori_bs;
+      const int bw = v.ori_bt[(int64_t)vb * v.ori_tl + min(ew, v.ori_tl - 1)];
+      const int32_t rw = (ew < v.ori_tl && bw >= 0 && bw < v.ori_blocks) ? bw * v.ori_bs + pw % v.ori_bs : -1;
+      int32_t rc = -1;
+      if (v.mode == 2) {
+        const int pc = max(i - vnw, 0), ec = pc / v.cmp_bs;
+        const int bc = v.cmp_bt[(int64_t)vb * v.cmp_tl + min(ec, v.cmp_tl - 1)];
+        rc = (ec < v.cmp_tl && bc >= 0 && bc < v.cmp_blocks) ? ((bc * v.cmp_bs + pc % v.cmp_bs) | kCmpTag) : -1;
+      }
+      rr = i < vnw ? rw : rc;
+    } else {
+      rr = rowl[min(slot, cnt - 1)];
+    }
     const bool valid = slot < cnt && rr >= 0;
     const uint32_t vmask = (uint32_t)__builtin_amdgcn_ballot_w64(valid && lane < 16);
 #pragma unroll
@@ -369,8 +408,10 @@ __global__ __launch_bounds__(256) void v4_decode_rows_kernel(DecArgs a) {
 static hipError_t launch_v4_decode_rows(int is_fp16, const void* q, const void* kv, const void* kv2,
                                         const int32_t* rows, const int32_t* count, int64_t T, int64_t H, int64_t cap,
                                         const float* sinks, float sm_scale, void* out, float* lse,
-                                        hipStream_t stream) {
+                                        hipStream_t stream, const V4Args* v4 = nullptr) {
   DecArgs a;
+  a.inl = v4 != nullptr;
+  a.v4 = v4 ? *v4 : V4Args{};
   a.q = static_cast<const uint16_t*>(q);
   a.kv = static_cast<const uint8_t*>(kv);
   a.kv2 = static_cast<const uint8_t*>(kv2);
@@ -437,6 +478,10 @@ hipError_t launch_sparse_flash_mla(int is_fp16, const void* q, int64_t T, int64_
   a.win_left = (int)win_left;
   a.max_cmp = (int)max_cmp;
   a.mode = mode;
+  // swa / hca decode rows: the decode kernel derives the lists itself (one launch fewer).
+  if (mode != 3 && T <= kDecodeRows && cap <= kDecodeMaxSlots)
+    return launch_v4_decode_rows(is_fp16, q, ori_kv, cmp_kv, nullptr, nullptr, T, H, cap, sinks, sm_scale, out, lse,
+                                 stream, &a);
   const int per_block = 256 / kWave;
   hipLaunchKernelGGL(v4_row_lists_kernel, dim3((unsigned)((T + per_block - 1) / per_block)), dim3(256), 0, stream, a);
   hipError_t e = hipGetLastError();
