@@ -623,11 +623,13 @@ def _kname(name):
     return name[5:] if name.startswith("void ") else name
 
 
-def summarize_trace(db, drop=0, label=""):
+def summarize_trace(db, drop=0, label="", groups=1):
     """Per-kernel dispatch statistics from a `rocprofv3 --kernel-trace` rocpd database (durations in us).
 
     The first `drop` dispatches of every (kernel, grid) row are left out (the warmup launches of a
-    bench part), so the averages cover the timed launches only; `label` names the workload."""
+    bench part), so the averages cover the timed launches only; `label` names the workload.  With
+    `groups` > 1 the remaining dispatches of a row are split into that many consecutive runs of equal
+    length, one output row each (labelled #1, #2, ...), for a part that times one call several ways."""
     con = _rocpd(db)
     rows = con.execute("select name, grid_x * grid_y * grid_z, workgroup_x, duration, lds_size, scratch_size, "
                        "vgpr_count, accum_vgpr_count, start from kernels order by start").fetchall()
@@ -642,8 +644,14 @@ def summarize_trace(db, drop=0, label=""):
           f"{'max_us':>10s} lds/scratch/vgpr/agpr")
     for (name, grid, wg), v in sorted(agg.items(), key=lambda kv: -sum(kv[1]["d"])):
         d = v["d"][drop:] if len(v["d"]) > drop else v["d"]
-        print(f"{label:10s} {name:48s} {grid:9d} {wg:4d} {len(d):5d} {sum(d) / len(d):10.1f} {min(d):10.1f} "
-              f"{max(d):10.1f} {'/'.join(str(x) for x in v['meta'])}")
+        runs = [d]
+        if groups > 1 and len(d) % groups == 0:
+            n = len(d) // groups
+            runs = [d[i * n:(i + 1) * n] for i in range(groups)]
+        for i, r in enumerate(runs):
+            tag = f"{label}#{i + 1}" if len(runs) > 1 else label
+            print(f"{tag:10s} {name:48s} {grid:9d} {wg:4d} {len(r):5d} {sum(r) / len(r):10.1f} {min(r):10.1f} "
+                  f"{max(r):10.1f} {'/'.join(str(x) for x in v['meta'])}")
 
 
 def _counter_means(db, counter):
@@ -713,9 +721,9 @@ def main():
     if len(sys.argv) > 1 and sys.argv[1] in ("--rocprof-trace", "--rocprof-traffic", "--rocprof-mfma"):
         # Summaries of rocprofv3 databases written by profiling this script (no GPU needed).
         if sys.argv[1] == "--rocprof-trace":
-            # --rocprof-trace DB [DROP [LABEL]]
+            # --rocprof-trace DB [DROP [LABEL [GROUPS]]]
             summarize_trace(sys.argv[2], int(sys.argv[3]) if len(sys.argv) > 3 else 0,
-                            sys.argv[4] if len(sys.argv) > 4 else "")
+                            sys.argv[4] if len(sys.argv) > 4 else "", int(sys.argv[5]) if len(sys.argv) > 5 else 1)
         elif sys.argv[1] == "--rocprof-mfma":
             summarize_mfma(*sys.argv[2:4])
         else:

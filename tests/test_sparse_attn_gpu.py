@@ -99,9 +99,9 @@ def test_masked_slots_batches_and_heads(dsa, dev, dtype):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_decode_rows_masked_slots(dsa, dev, dtype):
-    """At most 8 query rows with at most 192 slots each: the decode-shaped kernel (heads across
-    workgroups, slots across the waves); -1 and out-of-range slots, an all-empty row, a block of
-    16 slots with none valid."""
+    """At most 8 query rows with at most 256 slots each: the decode-shaped kernel in one workgroup
+    per row and 16 heads (slots across the waves); -1 and out-of-range slots, an all-empty row, a
+    block of 16 slots with none valid."""
     print(f"sparse_attn decode rows b=2 m=3 topk=150 {dtype}", flush=True)
     q, kv, sink, idx = _inputs(2, 3, 300, 32, 512, 150, dtype, 46)
     g = torch.Generator().manual_seed(47)
@@ -110,6 +110,25 @@ def test_decode_rows_masked_slots(dsa, dev, dtype):
     idx[0, 1, :] = -1                      # no valid slot: out 0, lse = sink
     idx[1, 0, 16:32] = -1                  # a whole 16-slot block masked
     idx[1, 2, 7] = 300                     # past n: masked
+    scale = 0.05
+    for sk in (sink, None):
+        out = _run(dsa, dev, q, kv, sk, idx, scale)
+        want, want_lse = ref.sparse_attn_sink(q, kv, sk, idx, scale)
+        torch.testing.assert_close(out, want, rtol=1e-2, atol=1e-2)
+        torch.testing.assert_close(_lse(dsa, dev, q, kv, sk, idx, scale), want_lse, rtol=1e-3, atol=1e-3)
+        assert torch.count_nonzero(out[0, 1]) == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_decode_rows_chunked(dsa, dev, dtype):
+    """At most 8 query rows with 257..1024 slots: the decode kernel in 128-slot chunks whose
+    partials a combine kernel merges (sinks join there); an all-empty row, a chunk with no valid
+    slot, a last chunk that is partly past the list."""
+    print(f"sparse_attn decode chunks b=2 m=2 topk=600 {dtype}", flush=True)
+    q, kv, sink, idx = _inputs(2, 2, 900, 64, 512, 600, dtype, 48)
+    idx[0, 1, :] = -1                      # no valid slot: out 0, lse = sink
+    idx[1, 0, 128:256] = -1                # chunk 1 empty
+    idx[1, 1, 590:] = 900                  # past n: masked
     scale = 0.05
     for sk in (sink, None):
         out = _run(dsa, dev, q, kv, sk, idx, scale)

@@ -174,9 +174,9 @@ def test_bsnd_padded_rows_and_hca(dsa, dev):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("scenario", ["swa", "hca"])
 def test_bsnd_padded_decode_rows(dsa, dev, scenario, dtype):
-    # Decode-shaped padded BSND rows (at most 8 rows, at most 192 slots: the
-    # decode kernel, heads across workgroups and slots across waves): two
-    # batches of 3 rows, the second using 1 of them (padded rows: out 0, lse 0).
+    # Decode-shaped padded BSND rows (at most 8 rows, at most 256 slots: the
+    # decode kernel in one workgroup per row and 16 heads, slots across waves):
+    # two batches of 3 rows, the second using 1 of them (padded rows: out 0, lse 0).
     B, S, H, D, bs, ratio = 2, 3, 32, 512, 32, 8
     kv_lens = [300, 2]
     g = torch.Generator().manual_seed(18)
@@ -202,7 +202,8 @@ def test_bsnd_padded_decode_rows(dsa, dev, scenario, dtype):
 def test_decode_rows_split_path(dsa, dev, scenario):
     # One query row per sequence against 8193 keys (the reference benchmark's
     # decode shape, here B = 3): swa (128 slots) and hca (192) take the decode
-    # kernel, csa (640 slots) the split gather kernel whose combine adds the sinks.
+    # kernel in one workgroup per row and 16 heads, csa (640 slots) in five
+    # 128-slot chunks whose partials the combine kernel merges (adding the sinks).
     B, H, D, K, bs = 3, 64, 512, 512, 128
     ratio = 128 if scenario == "hca" else 4
     kv_lens = [8193, 4000, 129]
@@ -234,3 +235,63 @@ def test_no_sinks_and_rows_before_the_cache(dsa, dev):
     wo, wl = _want(q, cu, kv_lens, ori, ori_bt, None, 0.05, win_left=3)
     assert torch.all(torch.isneginf(lse[:2].cpu())) and torch.all(out[:2].cpu() == 0)
     _check(out[2:], lse[2:], wo[2:], wl[2:], torch.bfloat16)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_decode_csa_selection_edges_chunks_and_padding(dsa, dev, dtype):
+    # csa decode rows with the row lists derived in the decode kernel, cut into
+    # 128-slot chunks (cap = 41 + 400 slots): a -1 ending a selection early,
+    # entries at or above the row's threshold (skipped), a row whose selection
+    # starts with -1, and padded BSND rows (out 0, lse 0, marked by chunk 0).
+    B, S, H, D, bs, ratio, K, win = 2, 3, 32, 512, 32, 4, 400, 40
+    kv_lens = [1700, 900]
+    g = torch.Generator().manual_seed(31)
+    q = torch.randn((B, S, H, D), generator=g).to(dtype)
+    ori, ori_bt = _paged(kv_lens, bs, 90, D, -1, 1, dtype, g)
+    cmp, cmp_bt = _paged([n // ratio for n in kv_lens], bs, 24, D, -1, 1, dtype, g)
+    cu = [0, 3, 5]
+    idx = _csa_indices(cu, kv_lens, K, ratio, g)
+    idx[0, 0, 150:] = -1                   # ends after 150 entries
+    idx[0, 0, 200] = 3                     # after the -1: not read
+    idx[1, 0, 10:20] = 5000                # at or above the threshold: skipped
+    idx[2, 0, :] = -1                      # nothing selected: the window alone
+    idx[3, 0, 5] = -7                      # a negative entry that is not -1: skipped
+    qb = torch.zeros((B, S, H, D), dtype=dtype)
+    qb[0] = q[0]
+    qb[1, :2] = q[1, :2]
+    idx_b = torch.full((B, S, 1, K), -1, dtype=torch.int32)  # BSND selections; the padded row's unused
+    idx_b[0] = idx[0:3]
+    idx_b[1, :2] = idx[3:5]
+    sinks = torch.randn(H, generator=g)
+    for sk in (sinks, None):
+        out, lse = _run(dsa, dev, qb, cu, kv_lens, ori, ori_bt, sk, 0.05, cmp=cmp, cmp_bt=cmp_bt, idx=idx_b,
+                        ratio=ratio, win_left=win, layout_q="BSND")
+        qp = torch.cat([qb[0], qb[1, :2]])
+        wo, wl = _want(qp, cu, kv_lens, ori, ori_bt, sk, 0.05, cmp=cmp, cmp_bt=cmp_bt, idx=idx, ratio=ratio,
+                       win_left=win)
+        oc, lc = out.cpu(), lse.cpu()
+        _check(torch.cat([oc[0], oc[1, :2]]), torch.cat([lc[0], lc[1, :2]]), wo, wl, dtype)
+        assert torch.all(oc[1, 2:] == 0) and torch.all(lc[1, 2:] == 0)
+
+
+def test_decode_rows_many_batches(dsa, dev):
+    # 70 batches (the decode kernel finds a row's batch 64 at a time), most of
+    # them without query rows; 5 decode rows against hca lists in one workgroup each.
+    H, D, bs, ratio, win = 16, 512, 16, 8, 30
+    g = torch.Generator().manual_seed(33)
+    q_lens = [0] * 70
+    for b, n in ((3, 1), (40, 2), (66, 1), (69, 1)):
+        q_lens[b] = n
+    kv_lens = [(37 * b) % 200 + 20 for b in range(70)]
+    cu = [0]
+    for n in q_lens:
+        cu.append(cu[-1] + n)
+    q = torch.randn((cu[-1], H, D), generator=g).to(torch.bfloat16)
+    ori, ori_bt = _paged(kv_lens, bs, sum(math.ceil(n / bs) for n in kv_lens), D, -1, 1, torch.bfloat16, g)
+    cl = [max(n // ratio, 1) for n in kv_lens]
+    cmp, cmp_bt = _paged(cl, bs, sum(math.ceil(n / bs) for n in cl), D, -1, 1, torch.bfloat16, g)
+    sinks = torch.randn(H, generator=g)
+    out, lse = _run(dsa, dev, q, cu, kv_lens, ori, ori_bt, sinks, 0.05, cmp=cmp, cmp_bt=cmp_bt, ratio=ratio,
+                    win_left=win)
+    wo, wl = _want(q, cu, kv_lens, ori, ori_bt, sinks, 0.05, cmp=cmp, cmp_bt=cmp_bt, ratio=ratio, win_left=win)
+    _check(out, lse, wo, wl, torch.bfloat16)

@@ -38,10 +38,13 @@ COMMON_FLAGS = [
 ]
 
 
-# Per-file extras.  indexer.hip: keep MFMA results in VGPRs (its epilogue reads
-# every result with VALU; AGPR results would each need a v_accvgpr_read).
+# Per-file extras: keep MFMA results in VGPRs.  indexer.hip's epilogue reads
+# every result with VALU (AGPR results would each need a v_accvgpr_read), and
+# sparse_flash_mla.hip's decode kernel rescales its O accumulators with VALU
+# (in AGPRs they were copied out and back on every block).
 FILE_FLAGS = {
     "indexer.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "sparse_flash_mla.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 

@@ -132,18 +132,27 @@ __global__ __launch_bounds__(256) void index_row_lists_kernel(const int32_t* __r
 }
 
 // ---------------------------------------------------------------------------
-// Decode-shaped row lists (at most kDecodeRows query rows): one workgroup per
-// (query row, 16 heads), its four waves splitting the row's slots into
-// 16-slot blocks (wave w takes blocks w, w + 4, ...), each with its own online
-// softmax and O, merged in LDS at the end.  No split partials and no combine
-// launch: such a call is a chain of latencies, and this removes a launch and
-// a global round trip from it.  For swa and hca rows the kernel also derives
-// the row lists itself (the window, then the compressed rows below the row's
-// threshold, through the block tables), so the call is this one launch.
+// Decode-shaped row lists (at most kDecodeRows query rows, at most
+// kDecodeMaxSlots slots): one workgroup per (query row, 16 heads, chunk of
+// slots), its four waves splitting the chunk into 16-slot blocks (wave w takes
+// blocks w, w + 4, ...), each with its own online softmax and O, merged in LDS
+// at the end.  A list of at most kDecSingle slots is one chunk, and the
+// workgroup writes the output: no partials and no combine launch, since such a
+// call is a chain of latencies.  Longer lists are cut into kDecChunk-slot
+// chunks (more CUs, fewer blocks per wave) whose partials a small combine
+// kernel merges.  For V4 rows the kernel also derives the row lists itself
+// (the window, then the compressed rows: hca every one below the row's
+// threshold, csa the selection's entries before its first -1 that lie below
+// the threshold), so no list kernel runs.  csa slots are not compacted: a
+// skipped entry is a masked slot, which changes only the order of the softmax
+// sums.
 //
-// A block's 16 rows (1 KB each, K = V) go to the wave's 16 KB of LDS by DMA,
-// one row per instruction, lane l carrying 16-byte chunk l ^ 2u of row u (so
-// the Q K^T operand reads, 16 rows at one chunk, fall on distinct banks).
+// A wave looks up the rows of four of its blocks at once (lane 16 j + u: slot
+// u of its j-th block of the group) and keeps two blocks in LDS: the DMA of
+// block i + 1 is issued before block i is waited for and multiplied.  A
+// block's 16 rows (1 KB each, K = V) go to 16 KB of LDS, one row per DMA
+// instruction, lane l carrying 16-byte chunk l ^ 2u of row u (so the Q K^T
+// operand reads, 16 rows at one chunk, fall on distinct banks).
 // S^T = K Q^T by 16x16x32 MFMAs (lane (g, r): keys 4g + i of head r), then
 // O^T += V^T P^T by 16x16x16 MFMAs whose V^T operand comes from
 // ds_read_b64_tr_b16 and whose P operand is the lane's own four scores.  As in
@@ -151,12 +160,22 @@ __global__ __launch_bounds__(256) void index_row_lists_kernel(const int32_t* __r
 // LSE by the exact sum, and the sinks join the denominator.
 constexpr int kDecBlk = 16;
 constexpr int64_t kDecodeRows = 8;
-// ... and at most this many slots per row: three blocks per wave.  Longer lists
-// (a csa selection) go through the split gather kernel, which keeps several
-// tiles in flight per workgroup where this kernel loads one block at a time.
-constexpr int64_t kDecodeMaxSlots = 12 * kDecBlk;
-constexpr int kDecWaveLds = kDecBlk * 1024;          // a wave's block of rows
-constexpr int kDecOBytes = 4 * 512 * 16 * 4;          // the four waves' O^T, fp32
+// ... and at most this many slots per row.  Longer lists go through the split
+// gather kernel.
+constexpr int64_t kDecodeMaxSlots = 1024;
+// Up to kDecSingle slots one workgroup per (row, 16 heads) takes them all and
+// writes the output; longer lists are cut into chunks of kDecChunk slots, one
+// workgroup each (grid z), whose fp32 partials (O unnormalised, its max, exact
+// and rounded sums) v4_decode_combine_kernel merges.
+constexpr int kDecSingle = 256;
+constexpr int kDecChunk = 128;
+static_assert(kDecSingle % 64 == 0 && kDecChunk % 64 == 0, "whole blocks per wave");
+constexpr float kDecSlack = 8.f;
+constexpr int kDecPart = 516;  // floats per (row, head, chunk): O[512], max, sum, rounded sum, pad
+// Row-lookup groups per wave: four of its blocks each.
+constexpr int kDecGroups = ((kDecSingle > kDecChunk ? kDecSingle : kDecChunk) / 64 + 3) / 4;
+constexpr int kDecBlkLds = kDecBlk * 1024;            // one block of rows
+constexpr int kDecOBytes = 4 * 512 * 16 * 4;          // the four waves' O^T, fp32 (aliases the 4 x 2 blocks)
 constexpr int kDecLds = kDecOBytes + 3 * 4 * 16 * 4;  // + m, l, rounded l per wave and head
 
 struct DecArgs {
@@ -169,16 +188,16 @@ struct DecArgs {
   uint16_t* out;          // [T, H, 512]
   float* lse;             // [T, H]
   int T, H, cap;
+  int chunk, nsplit;      // slots per workgroup, workgroups per (row, 16 heads)
+  float* part;            // [T, H, nsplit, kDecPart] when nsplit > 1
   float scale_log2;
-  // swa / hca lists derived here instead (inl): the row's batch, window and
-  // compressed rows, as v4_row_lists_kernel computes them.
-  int inl;
+  // V4 rows whose lists the kernel derives (kMode 1..3): the row's batch, window
+  // and compressed rows, as v4_row_lists_kernel computes them.
   V4Args v4;
 };
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 typedef __attribute__((address_space(3))) void dec_lds_void;
 typedef const __attribute__((address_space(1))) void dec_gbl_void;
 
@@ -198,6 +217,54 @@ __device__ __forceinline__ f32x4 dec_mfma_pv(const s16x4& a, const s16x4& b, con
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
 }
 
+// s_waitcnt with only vmcnt constrained (expcnt, lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void dec_wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+__device__ __forceinline__ uint32_t dec_lds_u32(const void* p) {
+  return (uint32_t)(uintptr_t)(const dec_lds_void*)p;
+}
+
+// ds_read_b64_tr_b16 as inline asm: through the builtin the compiler waits for
+// every outstanding DMA (the next block's included) before each read.
+// Completion is tracked explicitly with dec_lgkm_wait.
+__device__ __forceinline__ void dec_tr_read(u32x2& out, uint32_t lds_addr) {
+  __asm__ __volatile__("ds_read_b64_tr_b16 %0, %1" : "=v"(out) : "v"(lds_addr));
+}
+
+__device__ __forceinline__ void dec_b128_read(u32x4& out, uint32_t lds_addr) {
+  __asm__ __volatile__("ds_read_b128 %0, %1" : "=v"(out) : "v"(lds_addr));
+}
+
+// Wait until at most N LDS operations are outstanding; the eight values pass
+// through the asm so no use of them can be scheduled before the wait.
+template <int N, typename V>
+__device__ __forceinline__ void dec_lgkm_wait(V (&v)[8]) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  __asm__ __volatile__("s_waitcnt lgkmcnt(%8)"
+                       : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7])
+                       : "i"(N));
+}
+
+// Max and sum over the four lane groups of 16 (lanes r, r + 16, r + 32, r + 48),
+// by lane swaps rather than LDS permutes (which would wait for the pending LDS reads).
+__device__ __forceinline__ float dec_max_across_groups(float x) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+  const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+
+__device__ __forceinline__ float dec_sum_across_groups(float x) {
+  const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
 // One 16-bit value of p (round to nearest even) and its value back in fp32.
 template <bool kF16>
 __device__ __forceinline__ short dec_round(float p, float& back) {
@@ -212,7 +279,8 @@ __device__ __forceinline__ short dec_round(float p, float& back) {
   }
 }
 
-template <bool kF16>
+// kMode: 0 row lists given (rows / count), 1 swa, 2 hca, 3 csa (lists derived here).
+template <bool kF16, int kMode>
 __global__ __launch_bounds__(256) void v4_decode_rows_kernel(DecArgs a) {
   extern __shared__ __align__(16) uint8_t lds[];
   const int t = blockIdx.x;
@@ -221,99 +289,205 @@ __global__ __launch_bounds__(256) void v4_decode_rows_kernel(DecArgs a) {
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int r = lane & 15, g = lane >> 4;
-  int cnt_raw, vb = 0, vnw = 0, vw0 = 0;
+  const int s_lo = blockIdx.z * a.chunk;  // this workgroup's slots: s_lo .. s_lo + chunk - 1
+  // Q^T operands: head h0 + r, dims 32 st + 8g .. +7 (loaded first: they need no row list).
+  u32x4 qb[16];
+  const uint16_t* qp = a.q + ((int64_t)t * a.H + h0 + r) * 512 + 8 * g;
+#pragma unroll
+  for (int st = 0; st < 16; ++st) qb[st] = *reinterpret_cast<const u32x4*>(qp + 32 * st);
+  int cnt_raw, vb = 0, vnw = 0, vw0 = 0, thr = 0, nread = 0;
   const V4Args& v = a.v4;
-  if (a.inl) {  // workgroup-uniform
-    for (int i = 1; i < v.B; ++i) vb = v.q_start[i] <= t ? i : vb;
-    const int sq = t - v.q_start[vb];
-    const int qlb = v.q_len[vb];
+  if constexpr (kMode != 0) {
+    // Batch of row t: the last b with q_start[b] <= t (0 if none).  Past one batch,
+    // 64 batches per step, each lane loading its batch's start, query length and
+    // kv length at once.
+    int qsb = 0, qlb = 0, klb = 0;
+    if (v.B == 1) {
+      qsb = v.q_start[0];
+      qlb = v.q_len[0];
+      klb = v.kv_len[0];
+    }
+    for (int b0 = 0; v.B > 1 && b0 < v.B; b0 += kWave) {
+      const int b = b0 + lane;
+      const bool in = b < v.B;
+      const int qs = in ? v.q_start[b] : 0, ql = in ? v.q_len[b] : 0, kl = in ? v.kv_len[b] : 0;
+      const uint64_t le = __builtin_amdgcn_ballot_w64(in && qs <= t);
+      if (b0 == 0 || le) {
+        const int j = le ? 63 - __builtin_clzll(le) : 0;
+        vb = b0 + j;
+        qsb = __builtin_amdgcn_readlane(qs, j);
+        qlb = __builtin_amdgcn_readlane(ql, j);
+        klb = __builtin_amdgcn_readlane(kl, j);
+      }
+    }
+    const int sq = t - qsb;
     if (sq < 0 || sq >= qlb) {
       cnt_raw = -1;
     } else {
-      const int sg = v.kv_len[vb] - qlb + sq;  // position of this row in its sequence
+      const int sg = klb - qlb + sq;  // position of this row in its sequence
       vnw = sg >= 0 ? min(v.win_left, sg) + 1 : 0;
       vw0 = sg - vnw + 1;
-      cnt_raw = vnw + ((v.mode == 2 && sg >= 0) ? min((sg + 1) / v.cmp_ratio, v.max_cmp) : 0);
+      thr = (kMode >= 2 && sg >= 0) ? (sg + 1) / v.cmp_ratio : 0;
+      // csa: min(K, thr) entries of the selection are read (fewer if one is -1, found below).
+      nread = kMode == 3 ? min(v.K, thr) : 0;
+      cnt_raw = vnw + (kMode == 2 ? min(thr, v.max_cmp) : nread);
     }
   } else {
     cnt_raw = a.count[t];
   }
   if (cnt_raw < 0) {  // padded query row: out 0, lse 0 (workgroup-uniform)
+    if (a.nsplit > 1) {  // chunk 0 marks it (sum -1) for the combine
+      if (blockIdx.z == 0 && tid < 16) a.part[((int64_t)t * a.H + h0 + tid) * a.nsplit * kDecPart + 513] = -1.f;
+      return;
+    }
     for (int e = tid; e < 16 * 64; e += 256)
       *reinterpret_cast<u32x4*>(a.out + ((int64_t)t * a.H + h0 + e / 64) * 512 + 8 * (e % 64)) = u32x4{0, 0, 0, 0};
     if (tid < 16) a.lse[(int64_t)t * a.H + h0 + tid] = 0.f;
     return;
   }
-  const int cnt = min(cnt_raw, a.cap);
-  // Q^T operands: head h0 + r, dims 32 st + 8g .. +7.
-  u32x4 qb[16];
-  const uint16_t* qp = a.q + ((int64_t)t * a.H + h0 + r) * 512 + 8 * g;
+  int cnt = min(cnt_raw, a.cap);
+  const int32_t* rowl = a.rows + (int64_t)t * a.cap;
+  // Physical row of slot i < cnt (kCmpTag on compressed rows), -1 for an empty slot.
+  auto row_of = [&](int i) -> int32_t {
+    if constexpr (kMode == 0) {
+      return rowl[i];
+    } else {
+      // Window position vw0 + i, then compressed entry i - vnw: the lookups of both
+      // go out (from clamped entries) and the slot picks one.
+      const int pw = max(vw0 + i, 0), ew = pw / v.ori_bs;
+      const int bw = v.ori_bt[(int64_t)vb * v.ori_tl + min(ew, v.ori_tl - 1)];
+      int pc = max(i - vnw, 0);
+      bool ok = true;
+      if constexpr (kMode == 3) {
+        const int id = v.cmp_idx[(int64_t)t * v.K + min(pc, v.K - 1)];
+        ok = id >= 0 && id < thr;
+        pc = ok ? id : 0;
+      }
+      int32_t rc = -1;
+      if constexpr (kMode >= 2) {
+        const int ec = pc / v.cmp_bs;
+        const int bc = v.cmp_bt[(int64_t)vb * v.cmp_tl + min(ec, v.cmp_tl - 1)];
+        rc = (ok && ec < v.cmp_tl && bc >= 0 && bc < v.cmp_blocks) ? ((bc * v.cmp_bs + pc % v.cmp_bs) | kCmpTag) : -1;
+      }
+      const int32_t rw = (ew < v.ori_tl && bw >= 0 && bw < v.ori_blocks) ? bw * v.ori_bs + pw % v.ori_bs : -1;
+      return i < vnw ? rw : rc;
+    }
+  };
+  // The wave's blocks are wave, wave + 4, ...; its block i sits in group i / 4, whose
+  // rows are looked up together (lane 16 j + u: slot u of the group's block j), all
+  // groups before the first DMA.
+  auto slot_of = [&](int grp) { return s_lo + (wave + 4 * (4 * grp + (lane >> 4))) * kDecBlk + (lane & 15); };
+  // csa: the first 512 entries of the selection go out with the lookups.
+  constexpr bool csa = kMode == 3;
+  const int32_t* sel = csa ? v.cmp_idx + (int64_t)t * v.K : nullptr;
+  int32_t e0[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (csa && nread > 0) {  // loads from clamped entries, so none waits on a lane branch
 #pragma unroll
-  for (int st = 0; st < 16; ++st) qb[st] = *reinterpret_cast<const u32x4*>(qp + 32 * st);
+    for (int j = 0; j < 8; ++j) e0[j] = sel[min(j * kWave + lane, nread - 1)];
+  }
+  int32_t rowg[kDecGroups];
+#pragma unroll
+  for (int k = 0; k < kDecGroups; ++k) {
+    const int slot = slot_of(k);
+    rowg[k] = -1;
+    if (s_lo + (wave + 16 * k) * kDecBlk < cnt) rowg[k] = row_of(min(slot, cnt - 1));  // wave-uniform test
+  }
+  if constexpr (csa) {
+    // The selection's first -1 among its first nread entries ends it.
+    int f = nread;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint64_t end = __builtin_amdgcn_ballot_w64(e0[j] == -1 && j * kWave + lane < nread);
+      if (end && f == nread) f = j * kWave + (int)__builtin_ctzll(end);
+    }
+    for (int i0 = 8 * kWave; i0 < nread && f == nread; i0 += 8 * kWave) {
+      int32_t e[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int i = i0 + j * kWave + lane;
+        e[j] = i < nread ? sel[i] : 0;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint64_t end = __builtin_amdgcn_ballot_w64(e[j] == -1);
+        if (end && f == nread) f = i0 + j * kWave + (int)__builtin_ctzll(end);
+      }
+    }
+    cnt = min(vnw + f, cnt);
+  }
   f32x4 o[32];
 #pragma unroll
   for (int c = 0; c < 32; ++c) o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -__builtin_huge_valf(), l = 0.f, lr = 0.f;
-  uint8_t* buf = lds + wave * kDecWaveLds;
-  const int32_t* rowl = a.rows + (int64_t)t * a.cap;
-  const int nblk = (cnt + kDecBlk - 1) / kDecBlk;
-  auto load = [&](int blk, uint8_t* bp) -> uint32_t {
-    const int s0 = blk * kDecBlk;
-    // Lane u < 16 holds slot s0 + u's row; invalid slots read row 0 (their scores are masked).
-    const int slot = s0 + (lane & 15);
-    int32_t rr;
-    if (a.inl) {
-      // Window position vw0 + i, then compressed row i - vnw; both lookups go out
-      // (from clamped entries), the slot picks one.
-      const int i = min(slot, cnt - 1);
-      const int pw = max(vw0 + i, 0), ew = pw / v.ori_bs;
-      const int bw = v.ori_bt[(int64_t)vb * v.ori_tl + min(ew, v.ori_tl - 1)];
-      const int32_t rw = (ew < v.ori_tl && bw >= 0 && bw < v.ori_blocks) ? bw * v.ori_bs + pw % v.ori_bs : -1;
-      int32_t rc = -1;
-      if (v.mode == 2) {
-        const int pc = max(i - vnw, 0), ec = pc / v.cmp_bs;
-        const int bc = v.cmp_bt[(int64_t)vb * v.cmp_tl + min(ec, v.cmp_tl - 1)];
-        rc = (ec < v.cmp_tl && bc >= 0 && bc < v.cmp_blocks) ? ((bc * v.cmp_bs + pc % v.cmp_bs) | kCmpTag) : -1;
-      }
-      rr = i < vnw ? rw : rc;
-    } else {
-      rr = rowl[min(slot, cnt - 1)];
+  uint8_t* wbuf = lds + wave * (2 * kDecBlkLds);
+  const int s_hi = min(cnt, s_lo + a.chunk);
+  const int nblk = s_hi > s_lo ? (s_hi - s_lo + kDecBlk - 1) / kDecBlk : 0;
+  // DMA of the wave's block i to bp; returns its valid-slot mask.  rowg[0] holds
+  // block i's group: the groups shift down when block i starts one.
+  auto load = [&](int i, uint8_t* bp) -> uint32_t {
+    const int k = i >> 2, j = i & 3;
+    if (j == 0 && k > 0) {
+#pragma unroll
+      for (int kk = 0; kk + 1 < kDecGroups; ++kk) rowg[kk] = rowg[kk + 1];
     }
-    const bool valid = slot < cnt && rr >= 0;
-    const uint32_t vmask = (uint32_t)__builtin_amdgcn_ballot_w64(valid && lane < 16);
+    const int32_t rows = rowg[0];
+    const bool valid = rows >= 0 && slot_of(k) < cnt;
+    const uint32_t vmask = (uint32_t)(__builtin_amdgcn_ballot_w64(valid) >> (16 * j)) & 0xffffu;
+    const int32_t rz = valid ? rows : 0;  // empty slots read row 0 (their scores are masked)
 #pragma unroll
     for (int u = 0; u < kDecBlk; ++u) {
-      const int ru = __builtin_amdgcn_readlane(valid ? rr : 0, u);
+      const int ru = __builtin_amdgcn_readlane(rz, 16 * j + u);
       const uint8_t* base = (ru & kCmpTag) ? a.kv2 : a.kv;
       const uint8_t* src = base + (int64_t)(ru & ~kCmpTag) * 1024 + 16 * (lane ^ (2 * u));
       __builtin_amdgcn_global_load_lds((dec_gbl_void*)src, (dec_lds_void*)(bp + u * 1024), 16, 0, 0);
     }
     return vmask;
   };
+  const int vrow = 4 * g + (r >> 2);
   auto process = [&](const uint8_t* bp, uint32_t vmask) {
-    // S^T = K Q^T: A = K rows r (chunk 4 st + g), B = Q^T.
-    f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+    // S^T = K Q^T: A = K rows r (chunk 4 st + g), B = Q^T; the first two groups of V^T
+    // reads (below) go out behind the K reads.
+    const uint32_t kb0 = dec_lds_u32(bp) + r * 1024;
+    u32x4 kr[2][8];
 #pragma unroll
-    for (int st = 0; st < 16; ++st) {
-      const u32x4 kr = *reinterpret_cast<const u32x4*>(bp + r * 1024 + 16 * ((4 * st + g) ^ (2 * r)));
-      sc = dec_mfma_qk<kF16>(kr, qb[st], sc);
-    }
+    for (int st = 0; st < 16; ++st) dec_b128_read(kr[st >> 3][st & 7], kb0 + 16 * ((4 * st + g) ^ (2 * r)));
+    // O^T += V^T P^T: lane (g, L) feeds row 4g + L / 4, columns 16 c + 4 (L % 4) .. +3,
+    // i.e. chunk (2c + (L % 4) / 2) ^ 2 vrow of the row, at bytes vb0 + 32 (c ^ vrow).
+    const uint32_t vb0 = dec_lds_u32(bp) + vrow * 1024 + 16 * ((r & 3) >> 1) + 8 * (r & 1);
+    u32x2 va[4][8];
+    auto reads = [&](int grp) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) dec_tr_read(va[grp][k], vb0 + 32 * ((8 * grp + k) ^ vrow));
+    };
+    f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+    dec_lgkm_wait<8>(kr[0]);
+#pragma unroll
+    for (int st = 0; st < 8; ++st) sc = dec_mfma_qk<kF16>(kr[0][st], qb[st], sc);
+    reads(0);
+    dec_lgkm_wait<8>(kr[1]);
+#pragma unroll
+    for (int st = 0; st < 8; ++st) sc = dec_mfma_qk<kF16>(kr[1][st], qb[8 + st], sc);
+    reads(1);
     float s2[4], bm = -__builtin_huge_valf();
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       s2[i] = ((vmask >> (4 * g + i)) & 1u) ? sc[i] * a.scale_log2 : -__builtin_huge_valf();
       bm = fmaxf(bm, s2[i]);
     }
-    bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
-    bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
-    const float mn = fmaxf(m, bm);
-    // Both -inf (nothing valid yet): alpha 1 and every p 0, with no inf - inf.
+    bm = dec_max_across_groups(bm);
+    // The reference max moves only when a score passes it by more than kDecSlack
+    // (p <= 2^kDecSlack then), so O is seldom rescaled.  Both -inf (nothing valid
+    // yet): alpha 1 and every p 0, with no inf - inf.
+    const float mn = (m == -__builtin_huge_valf() || bm > m + kDecSlack) ? fmaxf(m, bm) : m;
     const float alpha = m == mn ? 1.f : fast_exp2(m - mn);
+    // O is still 0 while m is -inf; otherwise it is rescaled when some head's max moved.
+    if (__builtin_amdgcn_ballot_w64(m != mn && m != -__builtin_huge_valf())) {
+#pragma unroll
+      for (int c = 0; c < 32; ++c) o[c] *= alpha;
+    }
     m = mn;
     l *= alpha;
     lr *= alpha;
-#pragma unroll
-    for (int c = 0; c < 32; ++c) o[c] *= alpha;
     s16x4 pb;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -323,31 +497,44 @@ __global__ __launch_bounds__(256) void v4_decode_rows_kernel(DecArgs a) {
       l += p;
       lr += back;
     }
-    // O^T += V^T P^T: lane (g, L) feeds row 4g + L / 4, columns 16 c + 4 (L % 4) .. +3.
-    const int vrow = 4 * g + (r >> 2);
+    auto mfmas = [&](int grp) {
 #pragma unroll
-    for (int c = 0; c < 32; ++c) {
-      const int chunk = 2 * c + ((r & 3) >> 1);
-      const s16x4 va = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (lds_s16x4*)(bp + vrow * 1024 + 16 * (chunk ^ (2 * vrow)) + 8 * (r & 1)));
-      o[c] = dec_mfma_pv<kF16>(va, pb, o[c]);
-    }
+      for (int k = 0; k < 8; ++k)
+        o[8 * grp + k] = dec_mfma_pv<kF16>(__builtin_bit_cast(s16x4, va[grp][k]), pb, o[8 * grp + k]);
+    };
+    dec_lgkm_wait<8>(va[0]);
+    mfmas(0);
+    reads(2);
+    dec_lgkm_wait<8>(va[1]);
+    mfmas(1);
+    reads(3);
+    dec_lgkm_wait<8>(va[2]);
+    mfmas(2);
+    dec_lgkm_wait<0>(va[3]);
+    mfmas(3);
   };
-  for (int blk = wave; blk < nblk; blk += 4) {
-    const uint32_t vm = load(blk, buf);
-    __builtin_amdgcn_s_waitcnt(0);  // the block is in LDS
-    process(buf, vm);
+  // Block i of the wave goes to buffer i % 2; the DMA of block i + 1 is issued
+  // before block i is waited for.
+  const int nmine = nblk > wave ? (nblk - 1 - wave) / 4 + 1 : 0;
+  uint32_t vm = nmine > 0 ? load(0, wbuf) : 0u;
+  for (int i = 0; i < nmine; ++i) {
+    uint32_t vn = 0;
+    if (i + 1 < nmine) {
+      vn = load(i + 1, wbuf + ((i + 1) & 1) * kDecBlkLds);
+      dec_wait_vmcnt<kDecBlk>();  // block i is in LDS, block i + 1 in flight
+    } else {
+      dec_wait_vmcnt<0>();
+    }
+    process(wbuf + (i & 1) * kDecBlkLds, vm);
+    vm = vn;
   }
-  l += __shfl_xor(l, 16, kWave);
-  l += __shfl_xor(l, 32, kWave);
-  lr += __shfl_xor(lr, 16, kWave);
-  lr += __shfl_xor(lr, 32, kWave);
-  __syncthreads();  // every wave is done with its block buffer
-  float* ow = reinterpret_cast<float*>(lds) + wave * (512 * 16);
+  l = dec_sum_across_groups(l);
+  lr = dec_sum_across_groups(lr);
+  __syncthreads();  // every wave is done with its block buffers
+  // Wave w's O^T: f32x4 (c * 64 + lane) of its area holds head r, columns 16 c + 4 g .. +3.
+  f32x4* ow = reinterpret_cast<f32x4*>(lds) + wave * (32 * 64);
 #pragma unroll
-  for (int c = 0; c < 32; ++c)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ow[(16 * c + 4 * g + i) * 16 + r] = o[c][i];
+  for (int c = 0; c < 32; ++c) ow[c * 64 + lane] = o[c];
   float* stats = reinterpret_cast<float*>(lds + kDecOBytes);  // [3][4 waves][16 heads]
   if (g == 0) {
     stats[wave * 16 + r] = m;
@@ -355,63 +542,162 @@ __global__ __launch_bounds__(256) void v4_decode_rows_kernel(DecArgs a) {
     stats[128 + wave * 16 + r] = lr;
   }
   __syncthreads();
-  // Merge: thread handles head e % 16, columns 8 (e / 16) .. +7.
-  const float* of = reinterpret_cast<const float*>(lds);
-  for (int e = tid; e < 16 * 64; e += 256) {
-    const int h = e & 15, c8 = 8 * (e >> 4);
-    float mw[4], mx = -__builtin_huge_valf();
+  // Merge: thread tid takes head h = tid % 16 and the f32x4 items tid + 256 j (j < 8)
+  // of every wave's area: columns 4 q .. 4 q + 3, q = tid / 16 + 16 j.  A chunk's
+  // workgroup leaves the sinks to the combine and writes its partial instead.
+  const f32x4* of = reinterpret_cast<const f32x4*>(lds);
+  const bool split = a.nsplit > 1;
+  const int h = tid & 15;
+  float mw[4], mx = -__builtin_huge_valf();
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      mw[w] = stats[w * 16 + h];
-      mx = fmaxf(mx, mw[w]);
+  for (int w = 0; w < 4; ++w) {
+    mw[w] = stats[w * 16 + h];
+    mx = fmaxf(mx, mw[w]);
+  }
+  const float sink2 = a.sinks && !split ? a.sinks[h0 + h] * 1.4426950408889634f : -__builtin_huge_valf();
+  const float mm = fmaxf(mx, sink2);
+  float den = 0.f, den_r = 0.f, wgt[4];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    wgt[w] = mm == -__builtin_huge_valf() ? 0.f : fast_exp2(mw[w] - mm);
+    den += stats[64 + w * 16 + h] * wgt[w];
+    den_r += stats[128 + w * 16 + h] * wgt[w];
+  }
+  const int64_t th = (int64_t)t * a.H + h0 + h;
+  // sum_w wgt[w] O_w for item j.
+  auto merged = [&](int j) -> f32x4 {
+    const int item = tid + 256 * j;
+    f32x4 acc = of[item] * wgt[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) acc += of[w * (32 * 64) + item] * wgt[w];
+    return acc;
+  };
+  if (split) {
+    float* pp = a.part + (th * a.nsplit + blockIdx.z) * kDecPart;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) *reinterpret_cast<f32x4*>(pp + 4 * ((tid + 256 * j) >> 4)) = merged(j);
+    if (tid < 16) {
+      pp[512] = mm;
+      pp[513] = den;
+      pp[514] = den_r;
     }
-    const float sink2 = a.sinks ? a.sinks[h0 + h] * 1.4426950408889634f : -__builtin_huge_valf();
-    const float mm = fmaxf(mx, sink2);
-    float den = 0.f, den_r = 0.f, wgt[4];
+    return;
+  }
+  const float es = a.sinks && mm != -__builtin_huge_valf() ? fast_exp2(sink2 - mm) : 0.f;
+  den += es;
+  den_r += es;
+  const float inv = den_r > 0.f ? 1.f / den_r : 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      wgt[w] = mm == -__builtin_huge_valf() ? 0.f : fast_exp2(mw[w] - mm);
-      den += stats[64 + w * 16 + h] * wgt[w];
-      den_r += stats[128 + w * 16 + h] * wgt[w];
-    }
-    const float es = a.sinks && mm != -__builtin_huge_valf() ? fast_exp2(sink2 - mm) : 0.f;
-    den += es;
-    den_r += es;
-    const float inv = den_r > 0.f ? 1.f / den_r : 0.f;
-    uint32_t pk[4];
+  for (int j = 0; j < 8; ++j) {
+    const int item = tid + 256 * j;
+    const f32x4 acc = merged(j) * inv;
+    uint32_t pk[2];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float v2[2];
-#pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        const int col = c8 + 2 * j + k;
-        float acc = 0.f;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) acc += of[w * (512 * 16) + col * 16 + h] * wgt[w];
-        v2[k] = acc * inv;
-      }
+    for (int k = 0; k < 2; ++k) {
       if constexpr (kF16) {
         typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-        const h2 hv = {(_Float16)v2[0], (_Float16)v2[1]};
-        pk[j] = __builtin_bit_cast(uint32_t, hv);
+        const h2 hv = {(_Float16)acc[2 * k], (_Float16)acc[2 * k + 1]};
+        pk[k] = __builtin_bit_cast(uint32_t, hv);
       } else {
-        pk[j] = pack_bf16x2(v2[0], v2[1]);
+        pk[k] = pack_bf16x2(acc[2 * k], acc[2 * k + 1]);
       }
     }
-    *reinterpret_cast<u32x4*>(a.out + ((int64_t)t * a.H + h0 + h) * 512 + c8) = u32x4{pk[0], pk[1], pk[2], pk[3]};
-    if (c8 == 0)
-      a.lse[(int64_t)t * a.H + h0 + h] = den > 0.f ? (mm + fast_log2(den)) * 0.69314718055994531f : -__builtin_huge_valf();
+    *reinterpret_cast<u32x2*>(a.out + th * 512 + 4 * (item >> 4)) = u32x2{pk[0], pk[1]};
+  }
+  if (tid < 16) a.lse[th] = den > 0.f ? (mm + fast_log2(den)) * 0.69314718055994531f : -__builtin_huge_valf();
+}
+
+// Merge of the chunk partials: thread = (row, head, 8 columns); the sinks join
+// the denominator here.  A row whose chunk 0 carries sum -1 is padded: out 0, lse 0.
+template <bool kF16>
+__global__ __launch_bounds__(256) void v4_decode_combine_kernel(const float* __restrict__ part,
+                                                                const float* __restrict__ sinks, int TH, int H,
+                                                                int nsplit, uint16_t* __restrict__ out,
+                                                                float* __restrict__ lse) {
+  const int hh = blockIdx.x * 4 + (int)(threadIdx.x / 64);  // row * H + head
+  if (hh >= TH) return;
+  const int c8 = 8 * (threadIdx.x % 64);
+  const float* base = part + (int64_t)hh * nsplit * kDecPart;
+  uint16_t* op = out + (int64_t)hh * 512 + c8;
+  if (base[513] < 0.f) {
+    *reinterpret_cast<u32x4*>(op) = u32x4{0, 0, 0, 0};
+    if (c8 == 0) lse[hh] = 0.f;
+    return;
+  }
+  const float sink2 = sinks ? sinks[hh % H] * 1.4426950408889634f : -__builtin_huge_valf();
+  float mm = sink2;
+  for (int z = 0; z < nsplit; ++z) mm = fmaxf(mm, base[z * kDecPart + 512]);
+  float den = 0.f, den_r = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int z = 0; z < nsplit; ++z) {
+    const float* pz = base + z * kDecPart;
+    const float mz = pz[512];
+    if (mz == -__builtin_huge_valf()) continue;  // a chunk with no valid slot
+    const float w = fast_exp2(mz - mm);
+    den += pz[513] * w;
+    den_r += pz[514] * w;
+    const f32x4 lo = *reinterpret_cast<const f32x4*>(pz + c8);
+    const f32x4 hi = *reinterpret_cast<const f32x4*>(pz + c8 + 4);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      acc[k] += lo[k] * w;
+      acc[4 + k] += hi[k] * w;
+    }
+  }
+  const float es = sinks && mm != -__builtin_huge_valf() ? fast_exp2(sink2 - mm) : 0.f;
+  den += es;
+  den_r += es;
+  const float inv = den_r > 0.f ? 1.f / den_r : 0.f;
+  uint32_t pk[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if constexpr (kF16) {
+      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+      const h2 hv = {(_Float16)(acc[2 * j] * inv), (_Float16)(acc[2 * j + 1] * inv)};
+      pk[j] = __builtin_bit_cast(uint32_t, hv);
+    } else {
+      pk[j] = pack_bf16x2(acc[2 * j] * inv, acc[2 * j + 1] * inv);
+    }
+  }
+  *reinterpret_cast<u32x4*>(op) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+  if (c8 == 0) lse[hh] = den > 0.f ? (mm + fast_log2(den)) * 0.69314718055994531f : -__builtin_huge_valf();
+}
+
+template <bool kF16, int kMode>
+static hipError_t dec_launch_mode(dim3 grid, hipStream_t stream, const DecArgs& a) {
+  const hipError_t e = set_dynamic_lds_once<v4_decode_rows_kernel<kF16, kMode>>(kDecLds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((v4_decode_rows_kernel<kF16, kMode>), grid, dim3(256), kDecLds, stream, a);
+  return hipSuccess;
+}
+
+template <bool kF16>
+static hipError_t dec_launch(int mode, dim3 grid, hipStream_t stream, const DecArgs& a) {
+  switch (mode) {
+    case 1: return dec_launch_mode<kF16, 1>(grid, stream, a);
+    case 2: return dec_launch_mode<kF16, 2>(grid, stream, a);
+    case 3: return dec_launch_mode<kF16, 3>(grid, stream, a);
+    default: return dec_launch_mode<kF16, 0>(grid, stream, a);
   }
 }
 
-// Caller: T <= kDecodeRows, H % 16 == 0, rows / count from a row-list kernel on `stream`.
+// Workgroups per (row, 16 heads) of the decode kernel for `cap` slots.
+static int dec_splits(int64_t cap) { return cap <= kDecSingle ? 1 : (int)((cap + kDecChunk - 1) / kDecChunk); }
+
+static size_t dec_part_bytes(int64_t T, int64_t H, int64_t cap) {
+  if (T > kDecodeRows || cap > kDecodeMaxSlots || dec_splits(cap) == 1) return 0;
+  return (size_t)T * H * dec_splits(cap) * kDecPart * sizeof(float);
+}
+
+// Caller: T <= kDecodeRows, cap <= kDecodeMaxSlots, H % 16 == 0; rows / count from
+// a row-list kernel on `stream` (or v4 set: the kernel derives them); `part`
+// holds dec_part_bytes(T, H, cap).
 static hipError_t launch_v4_decode_rows(int is_fp16, const void* q, const void* kv, const void* kv2,
                                         const int32_t* rows, const int32_t* count, int64_t T, int64_t H, int64_t cap,
-                                        const float* sinks, float sm_scale, void* out, float* lse,
+                                        const float* sinks, float sm_scale, void* out, float* lse, void* part,
                                         hipStream_t stream, const V4Args* v4 = nullptr) {
   DecArgs a;
-  a.inl = v4 != nullptr;
   a.v4 = v4 ? *v4 : V4Args{};
+  const int mode = v4 ? v4->mode : 0;
   a.q = static_cast<const uint16_t*>(q);
   a.kv = static_cast<const uint8_t*>(kv);
   a.kv2 = static_cast<const uint8_t*>(kv2);
@@ -423,16 +709,22 @@ static hipError_t launch_v4_decode_rows(int is_fp16, const void* q, const void* 
   a.T = (int)T;
   a.H = (int)H;
   a.cap = (int)cap;
+  a.nsplit = dec_splits(cap);
+  a.chunk = a.nsplit == 1 ? (int)cap : kDecChunk;
+  a.part = static_cast<float*>(part);
   a.scale_log2 = sm_scale * 1.4426950408889634f;
-  const dim3 grid((unsigned)T, (unsigned)(H / 16));
-  if (is_fp16) {
-    const hipError_t e = set_dynamic_lds_once<v4_decode_rows_kernel<true>>(kDecLds);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(v4_decode_rows_kernel<true>, grid, dim3(256), kDecLds, stream, a);
-  } else {
-    const hipError_t e = set_dynamic_lds_once<v4_decode_rows_kernel<false>>(kDecLds);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(v4_decode_rows_kernel<false>, grid, dim3(256), kDecLds, stream, a);
+  const dim3 grid((unsigned)T, (unsigned)(H / 16), (unsigned)a.nsplit);
+  const int TH = (int)(T * H);
+  const dim3 cgrid((unsigned)((TH + 3) / 4));
+  const hipError_t e = is_fp16 ? dec_launch<true>(mode, grid, stream, a) : dec_launch<false>(mode, grid, stream, a);
+  if (e != hipSuccess) return e;
+  if (a.nsplit > 1) {
+    if (is_fp16)
+      hipLaunchKernelGGL(v4_decode_combine_kernel<true>, cgrid, dim3(256), 0, stream, a.part, sinks, TH, (int)H,
+                         a.nsplit, a.out, lse);
+    else
+      hipLaunchKernelGGL(v4_decode_combine_kernel<false>, cgrid, dim3(256), 0, stream, a.part, sinks, TH, (int)H,
+                         a.nsplit, a.out, lse);
   }
   return hipGetLastError();
 }
@@ -441,8 +733,10 @@ static size_t v4_lists_bytes(int64_t T, int64_t cap) {
   return ((size_t)T * (cap + 1) * sizeof(int32_t) + 255) & ~size_t(255);
 }
 
+// Row lists, then the split partials of the gather kernel or of the decode kernel.
 size_t v4_workspace_bytes(int64_t T, int64_t H, int64_t cap) {
-  return v4_lists_bytes(T, cap) + mla_workspace_bytes(T, H, cap);
+  const size_t a = mla_workspace_bytes(T, H, cap), b = dec_part_bytes(T, H, cap);
+  return v4_lists_bytes(T, cap) + (a > b ? a : b);
 }
 
 // Caller validated shapes; cap = win_left + 1 + (hca: max_cmp, csa: K).
@@ -478,20 +772,17 @@ hipError_t launch_sparse_flash_mla(int is_fp16, const void* q, int64_t T, int64_
   a.win_left = (int)win_left;
   a.max_cmp = (int)max_cmp;
   a.mode = mode;
-  // swa / hca decode rows: the decode kernel derives the lists itself (one launch fewer).
-  if (mode != 3 && T <= kDecodeRows && cap <= kDecodeMaxSlots)
+  // Decode rows: the decode kernel derives the lists itself (one launch).
+  void* part = static_cast<uint8_t*>(workspace) + v4_lists_bytes(T, cap);
+  if (T <= kDecodeRows && cap <= kDecodeMaxSlots)
     return launch_v4_decode_rows(is_fp16, q, ori_kv, cmp_kv, nullptr, nullptr, T, H, cap, sinks, sm_scale, out, lse,
-                                 stream, &a);
+                                 part, stream, &a);
   const int per_block = 256 / kWave;
   hipLaunchKernelGGL(v4_row_lists_kernel, dim3((unsigned)((T + per_block - 1) / per_block)), dim3(256), 0, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  if (T <= kDecodeRows && cap <= kDecodeMaxSlots)
-    return launch_v4_decode_rows(is_fp16, q, ori_kv, cmp_kv, a.rows, a.count, T, H, cap, sinks, sm_scale, out, lse,
-                                 stream);
-  void* mla_ws = static_cast<uint8_t*>(workspace) + v4_lists_bytes(T, cap);
   return launch_sparse_mla_rows(is_fp16, q, ori_kv, cmp_kv, a.rows, a.count, T, H, cap, sinks, sm_scale, out, lse,
-                                mla_ws, stream);
+                                part, stream);
 }
 
 size_t sparse_attn_sink_workspace_bytes(int64_t T, int64_t H, int64_t K) { return v4_workspace_bytes(T, H, K); }
@@ -509,9 +800,10 @@ hipError_t launch_sparse_attn_sink(int is_fp16, const void* q, const void* kv, c
                      idx, (int)T, (int)M, (int)N, (int)K, rows, count);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  if (T <= kDecodeRows && K <= kDecodeMaxSlots)
-    return launch_v4_decode_rows(is_fp16, q, kv, nullptr, rows, count, T, H, K, sinks, sm_scale, out, lse, stream);
   void* mla_ws = static_cast<uint8_t*>(workspace) + v4_lists_bytes(T, K);
+  if (T <= kDecodeRows && K <= kDecodeMaxSlots)
+    return launch_v4_decode_rows(is_fp16, q, kv, nullptr, rows, count, T, H, K, sinks, sm_scale, out, lse, mla_ws,
+                                 stream);
   return launch_sparse_mla_rows(is_fp16, q, kv, nullptr, rows, count, T, H, K, sinks, sm_scale, out, lse, mla_ws,
                                 stream);
 }
