@@ -78,6 +78,37 @@ def test_fp8_skewed_head_norms(dsa, dev):
     assert torch.all(d <= 3e-3 * (want.abs() + rms)), f"max err {d.max().item()} (rms {rms})"
 
 
+@pytest.mark.parametrize("S1", [1, 3, 4])
+def test_few_query_rows(dsa, dev, S1):
+    # Up to 4 query rows per batch: the workgroup's waves split each key tile
+    # (one token per workgroup); causal bound, key lengths, odd head counts, paged keys.
+    B, S2, bs = 2, 1500, 64
+    ak = torch.tensor([1500, 777], dtype=torch.int32)
+    for H, D, dtype in ((64, 128, torch.float8_e4m3fn), (40, 128, torch.float8_e4m3fn), (16, 64, torch.float16),
+                        (64, 128, torch.bfloat16)):
+        q, k, w, ks = _inputs(B, S1, S2, H, D, dtype, seed=60 + S1 + H + D)
+        ksd = None if ks is None else ks.to(dev)
+        got = dsa.indexer_logits(q.to(dev), k.unsqueeze(2).to(dev), w.to(dev), ksd, sparse_mode=3,
+                                 actual_seq_lengths_key=ak.to(dev)).cpu()
+        want = ref.indexer_logits(q, k, w, ks, sparse_mode=3, actual_k_len=ak.tolist())
+        _assert_logits(got, want)
+        # The same keys through a shuffled block table.
+        nblk = (S2 + bs - 1) // bs
+        table = torch.randperm(B * nblk, generator=torch.Generator().manual_seed(S1)).view(B, nblk).to(torch.int32)
+        pool = torch.zeros(B * nblk, bs, 1, D, dtype=k.dtype)
+        pscale = torch.ones(B * nblk, bs)
+        for b in range(B):
+            for j in range(nblk):
+                rows = k[b, j * bs:(j + 1) * bs]
+                pool[table[b, j], :rows.shape[0], 0] = rows
+                if ks is not None:
+                    pscale[table[b, j], :rows.shape[0]] = ks[b, j * bs:(j + 1) * bs]
+        got_pa = dsa.indexer_logits(q.to(dev), pool.to(dev), w.to(dev), None if ks is None else pscale.to(dev),
+                                    sparse_mode=3, actual_seq_lengths_key=ak.to(dev), block_table=table.to(dev),
+                                    layout_key="PA_BSND").cpu()
+        assert torch.equal(got_pa[:, :, :S2], got)
+
+
 def test_actual_lengths_and_paged_keys(dsa, dev):
     B, S1, S2, H, D, bs = 3, 40, 700, 64, 128, 64
     q, k, w, ks = _inputs(B, S1, S2, H, D, torch.float8_e4m3fn, seed=12)

@@ -300,12 +300,17 @@ __device__ __forceinline__ float row_threshold(const float* __restrict__ sr, int
 // per token, the valid keys whose logit is >= thr[row] (and > -1e30), appending
 // (logit, position) in key order to the row's slot of this key chunk -- a ballot
 // prefix gives each lane its slot, so no atomics -- and finally the kept count.
-template <int kKind, int kD, int kTokPW, int kNhb, bool kPaged, int kMode>
+//
+// kSplit (dense mode, few query rows): the four waves share the workgroup's
+// kTokPW tokens and split each 64-key tile instead, wave w taking keys
+// 16 w .. 16 w + 15 -- with one token per row no wave idles.
+template <int kKind, int kD, int kTokPW, int kNhb, bool kPaged, int kMode, bool kSplit = false>
 __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
+  static_assert(!kSplit || kMode == kModeDense, "key split: dense logits only");
   constexpr int kRB = IdxTraits<kKind, kD>::kRowBytes;
   constexpr int kLB = IdxTraits<kKind, kD>::kLaneBytes;
   constexpr int kPitch = lds_pitch<kKind, kD>();
-  constexpr int kTok = kTokPW * kIdxWaves;
+  constexpr int kTok = kSplit ? kTokPW : kTokPW * kIdxWaves;
   constexpr int kTileBytes = kIdxKeyTile * kRB;
   constexpr int kLoads = kTileBytes / 16 / kIdxThreads;  // 16-byte loads per thread per tile
   static_assert(kLoads >= 1, "tile too small");
@@ -318,6 +323,7 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
   const int g = lane >> 4;   // K-slice of the operand, output row group
   const int b = blockIdx.z;
   const int t_base = blockIdx.y * kTok;
+  const int tw = kSplit ? 0 : wave * kTokPW;  // this wave's first token, from t_base
   const int key0 = blockIdx.x * a.key_chunk;
   const int key1 = min(a.S2, key0 + a.key_chunk);
   // Row bases of batch b and its real lengths.  Padded layouts write -inf rows
@@ -346,7 +352,7 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
   int max_valid = 0;
 #pragma unroll
   for (int j = 0; j < kTokPW; ++j) {
-    const int t = t_base + wave * kTokPW + j;
+    const int t = t_base + tw + j;
     int nv = 0;
     if (t < aq && t < a.S1 && ak > 0) {
       if (a.sparse_mode == 3) {
@@ -384,7 +390,7 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
   float post[kTokPW];
 #pragma unroll
   for (int j = 0; j < kTokPW; ++j) {
-    const int t = t_base + wave * kTokPW + j;
+    const int t = t_base + tw + j;
     const bool tv = t < t_rows;
     const int64_t trow = q_base + (tv ? t : 0);
     f32x4 wt[4];
@@ -420,7 +426,7 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
   u32x2* crow[kTokPW];
 #pragma unroll
   for (int j = 0; j < kTokPW; ++j) {
-    const int t = t_base + wave * kTokPW + j;
+    const int t = t_base + tw + j;
     kept[j] = 0;
     crow[j] = kMode == kModeFilter ? a.cand + ((q_base + t) * gridDim.x + blockIdx.x) * a.cand_cap : nullptr;
     // Raised to the float just above -1e30: v >= thr then also rejects masked keys
@@ -437,9 +443,49 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
   constexpr int kRowsPerLoad = kIdxThreads / (kRB / 16);
   const int kr0 = tid / (kRB / 16);
   const uint8_t* kthread = a.k + (k_base + key0 + kr0) * kRB + (tid % (kRB / 16)) * 16;
+  // The key whose scale this lane applies in the epilogue of a tile (at this offset).
+  const int sc_off = kSplit ? 16 * wave + r : lane;
+  // Scale of key tile * tstride + sc_off of the chunk (1 past the valid keys or without scales).
+  auto load_scale = [&](int tile, int blk) -> float {
+    const int ss = key0 + tile * tstride + sc_off;
+    if (!a.k_scale || ss >= tile_end) return 1.f;
+    if constexpr (kPaged) {
+      if (!kSplit) blk = a.block_table[(int64_t)b * a.max_blocks + ss / a.block_size];
+      return a.k_scale[(int64_t)blk * a.block_size + ss % a.block_size];
+    } else {
+      return a.k_scale[k_base + ss];
+    }
+  };
+  // kSplit, whose steps hold little work to hide a load behind: the scales of the
+  // tiles in the two staging slots, loaded with their keys; with paged keys a
+  // fetch also takes its block ids (of this thread's key rows and of its scale
+  // key) from the previous fetch, which issues them before its own key rows, so
+  // waiting for them never waits for key rows.
+  float scl[2] = {1.f, 1.f};
+  int bid[kLoads], sbid = 0;
+  auto block_ids = [&](int tile, int (&ids)[kLoads], int& sid) {
+    const int64_t tb = (int64_t)b * a.max_blocks;
+    const int base = key0 + tile * tstride;
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int s = min(max(base + kr0 + i * kRowsPerLoad, key0), tile_end - 1);  // clamped: always a real entry
+      ids[i] = a.block_table[tb + s / a.block_size];
+    }
+    const int ss = min(max(base + sc_off, key0), tile_end - 1);
+    sid = a.block_table[tb + ss / a.block_size];
+  };
+  if constexpr (kPaged && kSplit) {
+    if (ntiles > 0) block_ids(0, bid, sbid);
+  }
   auto fetch = [&](auto slot_c, int tile) {
     constexpr int slot = decltype(slot_c)::value;
     const int rows_left = tile_end - key0 - tile * tstride;  // block-uniform
+    int nid[kLoads], nsid = sbid;
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) nid[i] = bid[i];
+    if constexpr (kPaged && kSplit) {
+      if (tile + 1 < ntiles) block_ids(tile + 1, nid, nsid);
+    }
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
       const int kr = kr0 + i * kRowsPerLoad;    // key row in tile
@@ -447,7 +493,7 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
       if (kr < rows_left) {
         if constexpr (kPaged) {
           const int s = key0 + tile * tstride + kr;
-          const int blk = a.block_table[(int64_t)b * a.max_blocks + s / a.block_size];
+          const int blk = kSplit ? bid[i] : a.block_table[(int64_t)b * a.max_blocks + s / a.block_size];
           const int64_t rowi = (int64_t)blk * a.block_size + s % a.block_size;
           v = *reinterpret_cast<const u32x4*>(a.k + rowi * kRB + (tid % (kRB / 16)) * 16);
         } else {
@@ -455,6 +501,14 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
         }
       }
       stage[slot][i] = v;
+    }
+    if constexpr (kSplit) {
+      scl[slot] = load_scale(tile, sbid);
+      if constexpr (kPaged) {
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) bid[i] = nid[i];
+        sbid = nsid;
+      }
     }
   };
   auto commit = [&](auto slot_c, int buf) {
@@ -489,13 +543,19 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
   auto step = [&](auto slot_c, int tile) {
     constexpr int slot = decltype(slot_c)::value;
     const int buf = tile % 3;
+    // This tile's scale: kSplit's from its slot before the fetch below reuses it;
+    // otherwise loaded now, its latency behind the tile's MFMAs -- except in the
+    // filter pass, whose registers are full: there it is loaded at the epilogue.
+    constexpr bool kEarly = kSplit || kMode != kModeFilter;
+    const float sc_early = kSplit ? scl[slot] : kEarly ? load_scale(tile, 0) : 0.f;
     if (tile + 2 < ntiles) fetch(slot_c, tile + 2);
 
     float res[kTokPW];
 #pragma unroll
     for (int j = 0; j < kTokPW; ++j) res[j] = 0.f;
 #pragma unroll
-    for (int sub = 0; sub < kIdxKeyTile / 16; ++sub) {
+    for (int si = 0; si < (kSplit ? 1 : kIdxKeyTile / 16); ++si) {
+      const int sub = kSplit ? wave : si;
       Operand<kKind, kD> kb;
       load_operand_lds<kKind, kD>(kb, &ktile[buf][(sub * 16 + r) * kPitch + g * kLB]);
 #pragma unroll
@@ -516,7 +576,7 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
                                                          __builtin_bit_cast(f16x8, relu_operand(c0, c1)), d, 0, 0, 0);
             }
           }
-          res[j] = (g == sub) ? d.x : res[j];
+          res[j] = (kSplit || g == sub) ? d.x : res[j];
         } else {
           float acc2[2] = {0.f, 0.f};  // two chains: head blocks 0, 2 and 1, 3
 #pragma unroll
@@ -533,27 +593,21 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
           float acc = acc2[0] + acc2[1];
           acc += __shfl_xor(acc, 16, kWave);
           acc += __shfl_xor(acc, 32, kWave);
-          res[j] = (g == sub) ? acc : res[j];
+          res[j] = (kSplit || g == sub) ? acc : res[j];
         }
       }
     }
-    // Lane l now holds key (tile * tstride + l) of the chunk for each token.
-    const int s = key0 + tile * tstride + lane;
-    float sc = 1.f;
-    if (a.k_scale && s < tile_end) {
-      if constexpr (kPaged) {
-        const int blk = a.block_table[(int64_t)b * a.max_blocks + s / a.block_size];
-        sc = a.k_scale[(int64_t)blk * a.block_size + s % a.block_size];
-      } else {
-        sc = a.k_scale[k_base + s];
-      }
-    }
+    // Lane l now holds key (tile * tstride + l) of the chunk for each token
+    // (kSplit: lane (g, r) of wave w holds key 16 w + r, and group 0 stores it).
+    const int s = key0 + tile * tstride + sc_off;
+    const bool storer = !kSplit || g == 0;
+    const float sc = kEarly ? sc_early : load_scale(tile, 0);
 #pragma unroll
     for (int j = 0; j < kTokPW; ++j) {
-      const int t = t_base + wave * kTokPW + j;
+      const int t = t_base + tw + j;
       const float v = (s < nvalid[j]) ? res[j] * (sc * post[j]) : -__builtin_huge_valf();
       if constexpr (kMode == kModeDense) {
-        if (t < t_rows && s < key1) __builtin_nontemporal_store(v, &a.logits[(q_base + t) * a.ld + s]);
+        if (storer && t < t_rows && s < key1) __builtin_nontemporal_store(v, &a.logits[(q_base + t) * a.ld + s]);
       } else if constexpr (kMode == kModeSample) {
         if (t < t_rows && s < key1)
           a.sample[(q_base + t) * a.sample_ld + (int64_t)(key0 / tstride + tile) * kIdxKeyTile + lane] = v;
@@ -584,10 +638,11 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
     const int masked0 = key0 + ntiles * kIdxKeyTile;
 #pragma unroll
     for (int j = 0; j < kTokPW; ++j) {
-      const int t = t_base + wave * kTokPW + j;
+      const int t = t_base + tw + j;
       if (t < t_rows) {
         float* row = a.logits + (q_base + t) * a.ld;
-        for (int s = masked0 + lane; s < key1; s += kWave) __builtin_nontemporal_store(-__builtin_huge_valf(), &row[s]);
+        for (int s = masked0 + (kSplit ? tid : lane); s < key1; s += kSplit ? kIdxThreads : kWave)
+          __builtin_nontemporal_store(-__builtin_huge_valf(), &row[s]);
       }
     }
   } else if constexpr (kMode == kModeSample) {
@@ -596,7 +651,7 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
     const int slot1 = (key1 + tstride - 1) / tstride * kIdxKeyTile;
 #pragma unroll
     for (int j = 0; j < kTokPW; ++j) {
-      const int t = t_base + wave * kTokPW + j;
+      const int t = t_base + tw + j;
       if (t < t_rows) {
         float* row = a.sample + (q_base + t) * a.sample_ld;
         for (int c = slot0 + ntiles * kIdxKeyTile + lane; c < slot1; c += kWave) row[c] = -__builtin_huge_valf();
@@ -607,19 +662,21 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
   } else {
 #pragma unroll
     for (int j = 0; j < kTokPW; ++j) {
-      const int t = t_base + wave * kTokPW + j;
+      const int t = t_base + tw + j;
       if (t < t_rows && lane == 0) a.cand_cnt[(q_base + t) * gridDim.x + blockIdx.x] = kept[j];
     }
   }
 }
 
 // fp8 with D = 128 is held to three waves per SIMD (the compiler would
-// otherwise trade a wave for a deeper operand prefetch).
-template <int kKind, int kD, int kTokPW, int kNhb, bool kPaged, int kMode>
+// otherwise trade a wave for a deeper operand prefetch); the key split, with
+// one token's operands per wave, leaves the compiler free.
+template <int kKind, int kD, int kTokPW, int kNhb, bool kPaged, int kMode, bool kSplit = false>
 __global__ __launch_bounds__(kIdxThreads)
-__attribute__((amdgpu_waves_per_eu(kKind == kFp8 && kD == 128 ? 3 : 1, kKind == kFp8 && kD == 128 ? 3 : 8)))
+__attribute__((amdgpu_waves_per_eu(kKind == kFp8 && kD == 128 && !kSplit ? 3 : 1,
+                                   kKind == kFp8 && kD == 128 && !kSplit ? 3 : 8)))
 void indexer_logits_kernel(IdxArgs a) {
-  indexer_body<kKind, kD, kTokPW, kNhb, kPaged, kMode>(a);
+  indexer_body<kKind, kD, kTokPW, kNhb, kPaged, kMode, kSplit>(a);
 }
 
 // The fp8 filter pass, held to the dense pass's three waves per SIMD (its few
@@ -630,8 +687,32 @@ void indexer_filter_fp8_kernel(IdxArgs a) {
   indexer_body<kFp8, kD, kTokPW, kNhb, kPaged, kModeFilter>(a);
 }
 
+// Query rows per batch up to which dense logits split each key tile over the
+// waves (one token per workgroup) instead of giving each wave its own tokens.
+constexpr int kIdxSplitRows = 4;
+
+template <int kKind, int kD>
+static hipError_t launch_indexer_split(const IdxArgs& a, int B, hipStream_t stream) {
+  const dim3 grid((unsigned)((a.S2 + a.key_chunk - 1) / a.key_chunk), (unsigned)a.S1, (unsigned)B);
+#define DSA_IDX(N, P) \
+  hipLaunchKernelGGL((indexer_logits_kernel<kKind, kD, 1, N, P, kModeDense, true>), grid, dim3(kIdxThreads), 0, stream, a)
+#define DSA_IDX2(N) \
+  if (a.block_table) DSA_IDX(N, true); else DSA_IDX(N, false)
+  switch ((a.H + 15) >> 4) {
+    case 1: DSA_IDX2(1); break;
+    case 2: DSA_IDX2(2); break;
+    case 3: DSA_IDX2(3); break;
+    default: DSA_IDX2(4); break;
+  }
+#undef DSA_IDX2
+#undef DSA_IDX
+  return hipGetLastError();
+}
+
 template <int kKind, int kD, int kMode = kModeDense>
 static hipError_t launch_indexer_kind(const IdxArgs& a, int B, hipStream_t stream) {
+  if constexpr (kMode == kModeDense)
+    if (a.S1 <= kIdxSplitRows) return launch_indexer_split<kKind, kD>(a, B, stream);
   constexpr int kTokPW = 2;
   constexpr int kTok = kTokPW * kIdxWaves;
   const dim3 grid((unsigned)((a.S2 + a.key_chunk - 1) / a.key_chunk), (unsigned)((a.S1 + kTok - 1) / kTok), (unsigned)B);
@@ -678,8 +759,9 @@ static IdxArgs make_idx_args(const void* q, const void* k, const float* k_scale,
 }
 
 // Keys per workgroup: enough workgroups to fill 256 CUs several times over.
-static int64_t indexer_key_chunk(int64_t B, int64_t S1, int64_t S2) {
-  const int64_t tok_groups = B * ((S1 + 7) / 8);
+// split: one token per workgroup (dense logits of few query rows).
+static int64_t indexer_key_chunk(int64_t B, int64_t S1, int64_t S2, bool split = false) {
+  const int64_t tok_groups = B * (split ? S1 : (S1 + 7) / 8);
   const int64_t chunks = (2048 + tok_groups - 1) / tok_groups;
   int64_t chunk = (S2 + chunks - 1) / chunks;
   chunk = ((chunk + kIdxKeyTile - 1) / kIdxKeyTile) * kIdxKeyTile;
@@ -711,7 +793,7 @@ hipError_t launch_indexer_logits(int kind, const void* q, const void* k, const f
                             max_blocks, sparse_mode);
   a.logits = logits;
   a.ld = ld;
-  a.key_chunk = (int)indexer_key_chunk(B, S1, S2);
+  a.key_chunk = (int)indexer_key_chunk(B, S1, S2, S1 <= kIdxSplitRows);
   return launch_indexer_mode<kModeDense>(kind, D, a, B, stream);
 }
 
