@@ -726,11 +726,15 @@ static hipError_t launch_reg(const float* x, int64_t ld, int64_t rows, int64_t n
 
 // Segments per row for the two-stage path (0: not used).  A segment holds at
 // most kRegMax scores and at least k; the candidates (nseg * k) must fit the
-// register path again; small row counts get more segments to fill the GPU.
+// register path again.  Small row counts get more segments to fill the GPU,
+// while a segment keeps at least 16 k scores: selecting a larger share of a
+// segment costs more than the workgroups it adds (32 rows x 131072, k = 2048:
+// 4 segments 26 us, 16 segments 34 us).
 static int long_row_segments(int64_t rows, int64_t n, int64_t k) {
   if (n <= kRegMax || k > kListCap) return 0;
   int nseg = (int)((n + kRegMax - 1) / kRegMax);
-  while (rows * nseg < 512 && (int64_t)(nseg * 2) * k <= kRegMax && (n + nseg * 2 - 1) / (nseg * 2) >= k) nseg *= 2;
+  while (rows * nseg < 512 && (int64_t)(nseg * 2) * k <= kRegMax && (n + nseg * 2 - 1) / (nseg * 2) >= 16 * k)
+    nseg *= 2;
   if ((int64_t)nseg * k > kRegMax) return 0;
   return nseg;
 }
