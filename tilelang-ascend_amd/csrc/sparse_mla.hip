@@ -978,23 +978,43 @@ __global__ __launch_bounds__(256) void sparse_mla_combine_kernel(const uint16_t*
     if (c == 0) lse[row] = 0.f;
     return;
   }
+  // Splits are visited kU at a time, every load of a group issued before any is
+  // used (a split-serial loop is a chain of load latencies); the sums keep the
+  // split order.
+  constexpr int kU = 8;
   const float sink = sinks ? sinks[row % H] : -__builtin_huge_valf();
   float mx = sink;
-  for (int i = 0; i < splits; ++i) mx = fmaxf(mx, part_lse[(int64_t)i * rows + row]);
+  for (int i0 = 0; i0 < splits; i0 += kU) {
+    float li[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+      li[u] = i0 + u < splits ? part_lse[(int64_t)(i0 + u) * rows + row] : -__builtin_huge_valf();
+#pragma unroll
+    for (int u = 0; u < kU; ++u) mx = fmaxf(mx, li[u]);
+  }
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float wsum = sinks && mx != -__builtin_huge_valf() ? __expf(sink - mx) : 0.f;
   if (mx != -__builtin_huge_valf()) {
-    for (int i = 0; i < splits; ++i) {
-      const float li = part_lse[(int64_t)i * rows + row];
-      if (li == -__builtin_huge_valf()) continue;
-      const float w = __expf(li - mx);
-      wsum += w;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(part_o + ((int64_t)i * rows + row) * kMlaDV + c);
-      const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+    for (int i0 = 0; i0 < splits; i0 += kU) {
+      float li[kU];
+      u32x4 v[kU];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        acc[2 * j] += w * unpack_lo<kF16>(vv[j]);
-        acc[2 * j + 1] += w * unpack_hi<kF16>(vv[j]);
+      for (int u = 0; u < kU; ++u) {
+        const int i = min(i0 + u, splits - 1);  // clamped: a real partial, unused past splits
+        li[u] = i0 + u < splits ? part_lse[(int64_t)i * rows + row] : -__builtin_huge_valf();
+        v[u] = *reinterpret_cast<const u32x4*>(part_o + ((int64_t)i * rows + row) * kMlaDV + c);
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        if (li[u] == -__builtin_huge_valf()) continue;
+        const float w = __expf(li[u] - mx);
+        wsum += w;
+        const uint32_t vv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc[2 * j] += w * unpack_lo<kF16>(vv[j]);
+          acc[2 * j + 1] += w * unpack_hi<kF16>(vv[j]);
+        }
       }
     }
   }
