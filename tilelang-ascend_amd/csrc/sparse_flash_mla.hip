@@ -624,23 +624,38 @@ __global__ __launch_bounds__(256) void v4_decode_combine_kernel(const float* __r
     if (c8 == 0) lse[hh] = 0.f;
     return;
   }
+  // Chunks kU at a time, every load of a group issued before any is used.
+  constexpr int kU = 4;
   const float sink2 = sinks ? sinks[hh % H] * 1.4426950408889634f : -__builtin_huge_valf();
   float mm = sink2;
-  for (int z = 0; z < nsplit; ++z) mm = fmaxf(mm, base[z * kDecPart + 512]);
-  float den = 0.f, den_r = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int z = 0; z < nsplit; ++z) {
-    const float* pz = base + z * kDecPart;
-    const float mz = pz[512];
-    if (mz == -__builtin_huge_valf()) continue;  // a chunk with no valid slot
-    const float w = fast_exp2(mz - mm);
-    den += pz[513] * w;
-    den_r += pz[514] * w;
-    const f32x4 lo = *reinterpret_cast<const f32x4*>(pz + c8);
-    const f32x4 hi = *reinterpret_cast<const f32x4*>(pz + c8 + 4);
+  for (int z0 = 0; z0 < nsplit; z0 += kU) {
+    float mz[kU];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      acc[k] += lo[k] * w;
-      acc[4 + k] += hi[k] * w;
+    for (int u = 0; u < kU; ++u) mz[u] = z0 + u < nsplit ? base[(z0 + u) * kDecPart + 512] : -__builtin_huge_valf();
+#pragma unroll
+    for (int u = 0; u < kU; ++u) mm = fmaxf(mm, mz[u]);
+  }
+  float den = 0.f, den_r = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int z0 = 0; z0 < nsplit; z0 += kU) {
+    f32x4 st[kU], lo[kU], hi[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const float* pz = base + min(z0 + u, nsplit - 1) * kDecPart;  // clamped: a real partial, unused past nsplit
+      st[u] = *reinterpret_cast<const f32x4*>(pz + 512);          // max, sum, rounded sum, pad
+      lo[u] = *reinterpret_cast<const f32x4*>(pz + c8);
+      hi[u] = *reinterpret_cast<const f32x4*>(pz + c8 + 4);
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      if (z0 + u >= nsplit || st[u][0] == -__builtin_huge_valf()) continue;  // past the chunks / no valid slot
+      const float w = fast_exp2(st[u][0] - mm);
+      den += st[u][1] * w;
+      den_r += st[u][2] * w;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        acc[k] += lo[u][k] * w;
+        acc[4 + k] += hi[u][k] * w;
+      }
     }
   }
   const float es = sinks && mm != -__builtin_huge_valf() ? fast_exp2(sink2 - mm) : 0.f;
