@@ -200,7 +200,8 @@ __device__ __forceinline__ void fp8_head_scales(const Operand<kFp8, kD> (&qa)[4]
   // m = 2^e * f with f in [1, 2): weights x 2^(14 - e), results x 2^(e - 14).
   const int e = m > 0.f ? (int)((__float_as_uint(m) >> 23) & 0xff) - 127 : 0;
   const float up = __uint_as_float((uint32_t)(127 + 14 - e) << 23);
-  post = __uint_as_float((uint32_t)(127 + e - 14) << 23);
+  // m, and with it post, is the same in every lane (lane (g, r) saw the weights of heads 4g + i + 16 hb).
+  post = __uint_as_float((uint32_t)__builtin_amdgcn_readfirstlane((int)((uint32_t)(127 + e - 14) << 23)));
 #pragma unroll
   for (int pr = 0; pr < 2; ++pr)
     wa[pr] = u32x4{pack_f16x2(w[2 * pr].x * up, w[2 * pr].y * up), pack_f16x2(w[2 * pr].z * up, w[2 * pr].w * up),
@@ -433,6 +434,7 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
     // (-inf), scores the top-k never selects (<= -1e30) and NaN.
     thr[j] = (kMode == kModeFilter && t < t_rows) ? fmaxf(a.thr[q_base + t], __uint_as_float(0xF149F2C9u))
                                                   : __builtin_huge_valf();
+    thr[j] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(thr[j])));  // wave-uniform
   }
 
   // Global -> register staging, two tiles in flight: tile t lands in
@@ -544,10 +546,8 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
     constexpr int slot = decltype(slot_c)::value;
     const int buf = tile % 3;
     // This tile's scale: kSplit's from its slot before the fetch below reuses it;
-    // otherwise loaded now, its latency behind the tile's MFMAs -- except in the
-    // filter pass, whose registers are full: there it is loaded at the epilogue.
-    constexpr bool kEarly = kSplit || kMode != kModeFilter;
-    const float sc_early = kSplit ? scl[slot] : kEarly ? load_scale(tile, 0) : 0.f;
+    // otherwise loaded now, its latency behind the tile's MFMAs.
+    const float sc_early = kSplit ? scl[slot] : load_scale(tile, 0);
     if (tile + 2 < ntiles) fetch(slot_c, tile + 2);
 
     float res[kTokPW];
@@ -601,7 +601,7 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
     // (kSplit: lane (g, r) of wave w holds key 16 w + r, and group 0 stores it).
     const int s = key0 + tile * tstride + sc_off;
     const bool storer = !kSplit || g == 0;
-    const float sc = kEarly ? sc_early : load_scale(tile, 0);
+    const float sc = sc_early;
 #pragma unroll
     for (int j = 0; j < kTokPW; ++j) {
       const int t = t_base + tw + j;
