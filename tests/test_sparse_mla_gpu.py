@@ -84,6 +84,44 @@ def test_padding_causal_and_actual_lengths(dsa, dev):
     assert torch.all(out[0, 4].cpu() == 0) and torch.all(torch.isneginf(lse[0, 4].cpu()))
 
 
+@pytest.mark.parametrize("topk", [40, 300, 1500])
+@pytest.mark.parametrize("paged", [False, True])
+def test_decode_rows_edges(dsa, dev, topk, paged):
+    # At most 8 query rows: the decode kernel (one workgroup per row and 16 heads up to
+    # 256 slots, 128-slot chunks and a combine past that).  Padded rows (out 0, lse -inf),
+    # key lengths, the causal bound, -1 and out-of-range slots, an empty 128-slot chunk, fp16.
+    B, S, Skv, H, bs = 2, 3, 1800, 32, 48
+    for dtype in (torch.bfloat16, torch.float16):
+        print(f"sparse_mla decode rows topk={topk} paged={paged} {dtype}", flush=True)
+        g = torch.Generator().manual_seed(topk + paged)
+        q = (torch.randn(B, S, H, 576, generator=g) * 0.5).to(dtype)
+        kv = (torch.randn(B, Skv, 1, 576, generator=g) * 0.5).to(dtype)
+        idx = torch.stack([torch.randperm(Skv, generator=g)[:topk] for _ in range(B * S)]).view(B, S, 1, topk)
+        idx = idx.to(torch.int32)
+        idx[0, 0, 0, : topk // 3] = -1                 # leading empty slots (a whole chunk at topk 1500)
+        idx[0, 1, 0, 5] = Skv + 7                      # out of range
+        if topk > 256:
+            idx[1, 0, 0, 128:256] = -1                 # chunk 1 empty
+        ql = torch.tensor([3, 2], dtype=torch.int32)   # row (1, 2) padded
+        kl = torch.tensor([Skv, 1000], dtype=torch.int32)
+        args = dict(actual_seq_lengths_query=ql.to(dev), actual_seq_lengths_kv=kl.to(dev))
+        if paged:
+            nblk = (Skv + bs - 1) // bs
+            table = torch.randperm(B * nblk, generator=g).view(B, nblk).to(torch.int32)
+            pool = torch.zeros(B * nblk, bs, 1, 576, dtype=dtype)
+            for b in range(B):
+                for j in range(nblk):
+                    rows = kv[b, j * bs:(j + 1) * bs]
+                    pool[table[b, j], :rows.shape[0]] = rows
+            out, lse = dsa.sparse_mla_fwd(q.to(dev), pool.to(dev), idx.to(dev), block_table=table.to(dev), **args)
+        else:
+            out, lse = dsa.sparse_mla_fwd(q.to(dev), kv.to(dev), idx.to(dev), **args)
+        ro, rl = ref.sparse_mla_fwd(q, kv, idx, actual_seq_lengths_query=ql.tolist(),
+                                    actual_seq_lengths_kv=kl.tolist())
+        _check(out, lse, ro, rl)
+        assert torch.all(out[1, 2].cpu() == 0) and torch.all(torch.isneginf(lse[1, 2].cpu()))
+
+
 def test_split_and_unsplit_agree(dsa, dev):
     # 1 token -> the index list is split across workgroups; 512 tokens -> no split.
     q, kv, idx = _inputs(1, 512, 4096, 128, 512, seed=9)

@@ -28,6 +28,7 @@ hipError_t launch_sparse_mla(int is_fp16, const void* q, const void* kv, const i
                              int64_t Skv, int64_t block_size, int64_t max_blocks, int64_t topk, float sm_scale,
                              int causal, void* out, float* lse, void* workspace, hipStream_t stream);
 size_t mla_workspace_bytes(int64_t tokens, int64_t H, int64_t topk);
+size_t sparse_mla_workspace_bytes(int64_t tokens, int64_t H, int64_t topk);
 size_t mla_scratch_bytes();
 hipError_t mla_scratch_ptr(void** out);
 size_t v4_workspace_bytes(int64_t T, int64_t H, int64_t cap);
@@ -306,7 +307,7 @@ int dsa_lightning_indexer_tnd_fused(int kind, const void* q, const void* k, cons
 
 size_t dsa_sparse_mla_workspace_size(int64_t B, int64_t S, int64_t H, int64_t topk) {
   if (B <= 0 || S <= 0 || H <= 0 || topk <= 0) return 0;
-  return dsa::mla_workspace_bytes(B * S, H, topk);
+  return dsa::sparse_mla_workspace_bytes(B * S, H, topk);
 }
 
 int dsa_sparse_mla_fwd(int kind, const void* q, const void* kv, const int32_t* indices,

@@ -174,9 +174,16 @@ constexpr float kDecSlack = 8.f;
 constexpr int kDecPart = 516;  // floats per (row, head, chunk): O[512], max, sum, rounded sum, pad
 // Row-lookup groups per wave: four of its blocks each.
 constexpr int kDecGroups = ((kDecSingle > kDecChunk ? kDecSingle : kDecChunk) / 64 + 3) / 4;
-constexpr int kDecBlkLds = kDecBlk * 1024;            // one block of rows
-constexpr int kDecOBytes = 4 * 512 * 16 * 4;          // the four waves' O^T, fp32 (aliases the 4 x 2 blocks)
-constexpr int kDecLds = kDecOBytes + 3 * 4 * 16 * 4;  // + m, l, rounded l per wave and head
+// One block of rows in LDS: 16 rows x 1 KB (K = V), then for 576-wide rows
+// (sparse MLA: 512 latent + 64 rope) their 128-byte tails, 16 x 128 B.
+template <int kD>
+constexpr int dec_blk_lds() { return kDecBlk * 1024 + (kD == 576 ? kDecBlk * 128 : 0); }
+constexpr int kDecOBytes = 4 * 512 * 16 * 4;  // the four waves' O^T, fp32 (aliases the 4 x 2 blocks)
+// LDS of the kernel: the 4 waves' two blocks, or the merge's O^T + m, l, rounded l per wave and head.
+template <int kD>
+constexpr int dec_lds() {
+  return 8 * dec_blk_lds<kD>() > kDecOBytes + 3 * 4 * 16 * 4 ? 8 * dec_blk_lds<kD>() : kDecOBytes + 3 * 4 * 16 * 4;
+}
 
 struct DecArgs {
   const uint16_t* q;      // [T, H, 512]
@@ -194,6 +201,15 @@ struct DecArgs {
   // V4 rows whose lists the kernel derives (kMode 1..3): the row's batch, window
   // and compressed rows, as v4_row_lists_kernel computes them.
   V4Args v4;
+  // Sparse MLA decode rows (kMode 4): query row t = b * S + s attends to the KV
+  // rows of indices[t][j] (paged through the block table, or b * Skv + idx).
+  struct {
+    const int32_t* idx;          // [T, cap]
+    const int32_t* block_table;  // [B, max_blocks] or null
+    const int32_t* q_len;        // [B] or null (S)
+    const int32_t* kv_len;       // [B] or null (Skv)
+    int S, Skv, block_size, max_blocks, causal;
+  } mla;
 };
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -249,6 +265,12 @@ __device__ __forceinline__ void dec_lgkm_wait(V (&v)[8]) {
                        : "i"(N));
 }
 
+template <int N, typename V>
+__device__ __forceinline__ void dec_lgkm_wait(V (&v)[2]) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  __asm__ __volatile__("s_waitcnt lgkmcnt(%2)" : "+v"(v[0]), "+v"(v[1]) : "i"(N));
+}
+
 // Max and sum over the four lane groups of 16 (lanes r, r + 16, r + 32, r + 48),
 // by lane swaps rather than LDS permutes (which would wait for the pending LDS reads).
 __device__ __forceinline__ float dec_max_across_groups(float x) {
@@ -279,9 +301,14 @@ __device__ __forceinline__ short dec_round(float p, float& back) {
   }
 }
 
-// kMode: 0 row lists given (rows / count), 1 swa, 2 hca, 3 csa (lists derived here).
-template <bool kF16, int kMode>
+// kMode: 0 row lists given (rows / count), 1 swa, 2 hca, 3 csa (lists derived
+// here), 4 sparse MLA index rows (kD = 576: K is the whole row, V its first 512).
+template <bool kF16, int kMode, int kD = 512>
 __global__ __launch_bounds__(256) void v4_decode_rows_kernel(DecArgs a) {
+  static_assert(kD == 512 || (kD == 576 && kMode == 4), "576-wide rows: sparse MLA index rows");
+  constexpr int kBlkLds = dec_blk_lds<kD>();
+  constexpr int kSteps = kD / 32;                      // Q K^T steps of 32 dims
+  constexpr int kDmaPerBlk = kD == 576 ? kDecBlk + 2 : kDecBlk;  // DMA instructions per block
   extern __shared__ __align__(16) uint8_t lds[];
   const int t = blockIdx.x;
   const int h0 = blockIdx.y * 16;
@@ -291,13 +318,24 @@ __global__ __launch_bounds__(256) void v4_decode_rows_kernel(DecArgs a) {
   const int r = lane & 15, g = lane >> 4;
   const int s_lo = blockIdx.z * a.chunk;  // this workgroup's slots: s_lo .. s_lo + chunk - 1
   // Q^T operands: head h0 + r, dims 32 st + 8g .. +7 (loaded first: they need no row list).
-  u32x4 qb[16];
-  const uint16_t* qp = a.q + ((int64_t)t * a.H + h0 + r) * 512 + 8 * g;
+  u32x4 qb[kSteps];
+  const uint16_t* qp = a.q + ((int64_t)t * a.H + h0 + r) * kD + 8 * g;
 #pragma unroll
-  for (int st = 0; st < 16; ++st) qb[st] = *reinterpret_cast<const u32x4*>(qp + 32 * st);
+  for (int st = 0; st < kSteps; ++st) qb[st] = *reinterpret_cast<const u32x4*>(qp + 32 * st);
   int cnt_raw, vb = 0, vnw = 0, vw0 = 0, thr = 0, nread = 0;
   const V4Args& v = a.v4;
-  if constexpr (kMode != 0) {
+  int mb = 0, mkl = 0, mlim = 0;  // kMode 4: batch, kv length, causal bound of the row
+  if constexpr (kMode == 4) {
+    // A row past its batch's query length has no valid slot (out 0, lse -inf, as
+    // the gather kernel gives it); a slot is valid iff 0 <= idx < kv_len and, when
+    // causal, idx <= kv_len - q_len + s.
+    mb = t / a.mla.S;
+    const int sq = t - mb * a.mla.S;
+    const int ql = min(max(a.mla.q_len ? a.mla.q_len[mb] : a.mla.S, 0), a.mla.S);
+    mkl = min(max(a.mla.kv_len ? a.mla.kv_len[mb] : a.mla.Skv, 0), a.mla.Skv);
+    mlim = a.mla.causal ? mkl - ql + sq : 0x7fffffff;
+    cnt_raw = sq < ql ? a.cap : 0;
+  } else if constexpr (kMode != 0) {
     // Batch of row t: the last b with q_start[b] <= t (0 if none).  Past one batch,
     // 64 batches per step, each lane loading its batch's start, query length and
     // kv length at once.
@@ -351,6 +389,14 @@ __global__ __launch_bounds__(256) void v4_decode_rows_kernel(DecArgs a) {
   auto row_of = [&](int i) -> int32_t {
     if constexpr (kMode == 0) {
       return rowl[i];
+    } else if constexpr (kMode == 4) {
+      const int idx = a.mla.idx[(int64_t)t * a.cap + i];
+      const bool ok = idx >= 0 && idx < mkl && idx <= mlim;
+      if (a.mla.block_table) {
+        const int blk = a.mla.block_table[(int64_t)mb * a.mla.max_blocks + (ok ? idx / a.mla.block_size : 0)];
+        return ok ? blk * a.mla.block_size + idx % a.mla.block_size : -1;
+      }
+      return ok ? mb * a.mla.Skv + idx : -1;
     } else {
       // Window position vw0 + i, then compressed entry i - vnw: the lookups of both
       // go out (from clamped entries) and the slot picks one.
@@ -419,7 +465,7 @@ __global__ __launch_bounds__(256) void v4_decode_rows_kernel(DecArgs a) {
 #pragma unroll
   for (int c = 0; c < 32; ++c) o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -__builtin_huge_valf(), l = 0.f, lr = 0.f;
-  uint8_t* wbuf = lds + wave * (2 * kDecBlkLds);
+  uint8_t* wbuf = lds + wave * (2 * kBlkLds);
   const int s_hi = min(cnt, s_lo + a.chunk);
   const int nblk = s_hi > s_lo ? (s_hi - s_lo + kDecBlk - 1) / kDecBlk : 0;
   // DMA of the wave's block i to bp; returns its valid-slot mask.  rowg[0] holds
@@ -434,12 +480,28 @@ __global__ __launch_bounds__(256) void v4_decode_rows_kernel(DecArgs a) {
     const bool valid = rows >= 0 && slot_of(k) < cnt;
     const uint32_t vmask = (uint32_t)(__builtin_amdgcn_ballot_w64(valid) >> (16 * j)) & 0xffffu;
     const int32_t rz = valid ? rows : 0;  // empty slots read row 0 (their scores are masked)
+    constexpr int kRowBytes = kD * 2;
 #pragma unroll
     for (int u = 0; u < kDecBlk; ++u) {
       const int ru = __builtin_amdgcn_readlane(rz, 16 * j + u);
-      const uint8_t* base = (ru & kCmpTag) ? a.kv2 : a.kv;
-      const uint8_t* src = base + (int64_t)(ru & ~kCmpTag) * 1024 + 16 * (lane ^ (2 * u));
+      // Index rows (kMode 4) use all 31 bits; V4 lists tag compressed rows.
+      const uint8_t* base = (kMode != 4 && (ru & kCmpTag)) ? a.kv2 : a.kv;
+      const int64_t pr = kMode == 4 ? (int64_t)ru : (int64_t)(ru & ~kCmpTag);
+      const uint8_t* src = base + pr * kRowBytes + 16 * (lane ^ (2 * u));
       __builtin_amdgcn_global_load_lds((dec_gbl_void*)src, (dec_lds_void*)(bp + u * 1024), 16, 0, 0);
+    }
+    if constexpr (kD == 576) {
+      // The rows' 128-byte tails: instruction q carries rows 8q .. 8q + 7, lane l chunk
+      // (l % 8) ^ f(u) of row u = 8q + l / 8 to slot l % 8, f(u) = 2 ((u / 4) % 4), so the
+      // Q K^T reads of a half-wave (16 rows, two chunks each) fall on distinct banks.
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int ruq = __shfl(rz, 16 * j + 8 * q + (lane >> 3), kWave);
+        const int u = 8 * q + (lane >> 3);
+        const int c = (lane & 7) ^ (2 * ((u >> 2) & 3));
+        const uint8_t* src = a.kv + (int64_t)ruq * kRowBytes + 1024 + 16 * c;
+        __builtin_amdgcn_global_load_lds((dec_gbl_void*)src, (dec_lds_void*)(bp + kDecBlk * 1024 + q * 1024), 16, 0, 0);
+      }
     }
     return vmask;
   };
@@ -451,6 +513,9 @@ __global__ __launch_bounds__(256) void v4_decode_rows_kernel(DecArgs a) {
     u32x4 kr[2][8];
 #pragma unroll
     for (int st = 0; st < 16; ++st) dec_b128_read(kr[st >> 3][st & 7], kb0 + 16 * ((4 * st + g) ^ (2 * r)));
+    // 576-wide rows: steps 16 and 17 from the tails (row r, chunk 4 (st - 16) + g, stored at slot chunk ^ f(r)).
+    u32x4 krt[2];
+    const uint32_t kt0 = dec_lds_u32(bp) + kDecBlk * 1024 + r * 128;
     // O^T += V^T P^T: lane (g, L) feeds row 4g + L / 4, columns 16 c + 4 (L % 4) .. +3,
     // i.e. chunk (2c + (L % 4) / 2) ^ 2 vrow of the row, at bytes vb0 + 32 (c ^ vrow).
     const uint32_t vb0 = dec_lds_u32(bp) + vrow * 1024 + 16 * ((r & 3) >> 1) + 8 * (r & 1);
@@ -463,10 +528,23 @@ __global__ __launch_bounds__(256) void v4_decode_rows_kernel(DecArgs a) {
     dec_lgkm_wait<8>(kr[0]);
 #pragma unroll
     for (int st = 0; st < 8; ++st) sc = dec_mfma_qk<kF16>(kr[0][st], qb[st], sc);
-    reads(0);
-    dec_lgkm_wait<8>(kr[1]);
+    if constexpr (kD == 576) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) dec_b128_read(krt[q], kt0 + 16 * ((4 * q + g) ^ (2 * ((r >> 2) & 3))));
+      dec_lgkm_wait<2>(kr[1]);
+    } else {
+      dec_lgkm_wait<8>(kr[1]);
+    }
 #pragma unroll
     for (int st = 0; st < 8; ++st) sc = dec_mfma_qk<kF16>(kr[1][st], qb[8 + st], sc);
+    if constexpr (kD == 576) {
+      reads(0);
+      dec_lgkm_wait<8>(krt);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) sc = dec_mfma_qk<kF16>(krt[q], qb[16 + q], sc);
+    } else {
+      reads(0);
+    }
     reads(1);
     float s2[4], bm = -__builtin_huge_valf();
 #pragma unroll
@@ -516,16 +594,20 @@ __global__ __launch_bounds__(256) void v4_decode_rows_kernel(DecArgs a) {
   // Block i of the wave goes to buffer i % 2; the DMA of block i + 1 is issued
   // before block i is waited for.
   const int nmine = nblk > wave ? (nblk - 1 - wave) / 4 + 1 : 0;
+  // Q and the lookups have landed before the first DMA (the lookups are needed for
+  // it): waiting here once keeps the compiler from waiting, inside the loop, for a
+  // Q register it loaded -- a wait that would also drain the next block's DMA.
+  dec_wait_vmcnt<0>();
   uint32_t vm = nmine > 0 ? load(0, wbuf) : 0u;
   for (int i = 0; i < nmine; ++i) {
     uint32_t vn = 0;
     if (i + 1 < nmine) {
-      vn = load(i + 1, wbuf + ((i + 1) & 1) * kDecBlkLds);
-      dec_wait_vmcnt<kDecBlk>();  // block i is in LDS, block i + 1 in flight
+      vn = load(i + 1, wbuf + ((i + 1) & 1) * kBlkLds);
+      dec_wait_vmcnt<kDmaPerBlk>();  // block i is in LDS, block i + 1 in flight
     } else {
       dec_wait_vmcnt<0>();
     }
-    process(wbuf + (i & 1) * kDecBlkLds, vm);
+    process(wbuf + (i & 1) * kBlkLds, vm);
     vm = vn;
   }
   l = dec_sum_across_groups(l);
@@ -677,11 +759,12 @@ __global__ __launch_bounds__(256) void v4_decode_combine_kernel(const float* __r
   if (c8 == 0) lse[hh] = den > 0.f ? (mm + fast_log2(den)) * 0.69314718055994531f : -__builtin_huge_valf();
 }
 
-template <bool kF16, int kMode>
+template <bool kF16, int kMode, int kD = 512>
 static hipError_t dec_launch_mode(dim3 grid, hipStream_t stream, const DecArgs& a) {
-  const hipError_t e = set_dynamic_lds_once<v4_decode_rows_kernel<kF16, kMode>>(kDecLds);
+  constexpr int kLds = dec_lds<kD>();
+  const hipError_t e = set_dynamic_lds_once<v4_decode_rows_kernel<kF16, kMode, kD>>(kLds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((v4_decode_rows_kernel<kF16, kMode>), grid, dim3(256), kDecLds, stream, a);
+  hipLaunchKernelGGL((v4_decode_rows_kernel<kF16, kMode, kD>), grid, dim3(256), kLds, stream, a);
   return hipSuccess;
 }
 
@@ -691,6 +774,7 @@ static hipError_t dec_launch(int mode, dim3 grid, hipStream_t stream, const DecA
     case 1: return dec_launch_mode<kF16, 1>(grid, stream, a);
     case 2: return dec_launch_mode<kF16, 2>(grid, stream, a);
     case 3: return dec_launch_mode<kF16, 3>(grid, stream, a);
+    case 4: return dec_launch_mode<kF16, 4, 576>(grid, stream, a);
     default: return dec_launch_mode<kF16, 0>(grid, stream, a);
   }
 }
@@ -706,18 +790,14 @@ static size_t dec_part_bytes(int64_t T, int64_t H, int64_t cap) {
 // Caller: T <= kDecodeRows, cap <= kDecodeMaxSlots, H % 16 == 0; rows / count from
 // a row-list kernel on `stream` (or v4 set: the kernel derives them); `part`
 // holds dec_part_bytes(T, H, cap).
-static hipError_t launch_v4_decode_rows(int is_fp16, const void* q, const void* kv, const void* kv2,
-                                        const int32_t* rows, const int32_t* count, int64_t T, int64_t H, int64_t cap,
-                                        const float* sinks, float sm_scale, void* out, float* lse, void* part,
-                                        hipStream_t stream, const V4Args* v4 = nullptr) {
-  DecArgs a;
-  a.v4 = v4 ? *v4 : V4Args{};
-  const int mode = v4 ? v4->mode : 0;
+// The decode kernel (and, past kDecSingle slots, its combine) for kernel mode
+// `mode`; `a` holds the mode's own arguments.
+static hipError_t dec_run(int is_fp16, int mode, DecArgs& a, const void* q, const void* kv, const void* kv2,
+                          int64_t T, int64_t H, int64_t cap, const float* sinks, float sm_scale, void* out, float* lse,
+                          void* part, hipStream_t stream) {
   a.q = static_cast<const uint16_t*>(q);
   a.kv = static_cast<const uint8_t*>(kv);
   a.kv2 = static_cast<const uint8_t*>(kv2);
-  a.rows = rows;
-  a.count = count;
   a.sinks = sinks;
   a.out = static_cast<uint16_t*>(out);
   a.lse = lse;
@@ -742,6 +822,51 @@ static hipError_t launch_v4_decode_rows(int is_fp16, const void* q, const void* 
                          a.nsplit, a.out, lse);
   }
   return hipGetLastError();
+}
+
+static hipError_t launch_v4_decode_rows(int is_fp16, const void* q, const void* kv, const void* kv2,
+                                        const int32_t* rows, const int32_t* count, int64_t T, int64_t H, int64_t cap,
+                                        const float* sinks, float sm_scale, void* out, float* lse, void* part,
+                                        hipStream_t stream, const V4Args* v4 = nullptr) {
+  DecArgs a = {};
+  a.v4 = v4 ? *v4 : V4Args{};
+  a.rows = rows;
+  a.count = count;
+  return dec_run(is_fp16, v4 ? v4->mode : 0, a, q, kv, kv2, T, H, cap, sinks, sm_scale, out, lse, part, stream);
+}
+
+// Sparse MLA (576-wide rows, V = the first 512) decode rows through the decode
+// kernel: at most kDecodeRows query rows, at most 1024 (row, head) pairs (so the
+// partials stay within the allocation-free entry's scratch), at most
+// kMlaDecodeMaxSlots index slots.
+constexpr int64_t kMlaDecodeMaxSlots = 2048;
+
+bool mla_decode_applies(int64_t T, int64_t H, int64_t topk) {
+  return T <= kDecodeRows && T * H <= 1024 && topk <= kMlaDecodeMaxSlots;
+}
+
+size_t mla_decode_part_bytes(int64_t T, int64_t H, int64_t topk) {
+  if (!mla_decode_applies(T, H, topk) || dec_splits(topk) == 1) return 0;
+  return (size_t)T * H * dec_splits(topk) * kDecPart * sizeof(float);
+}
+
+// Caller: mla_decode_applies(B * S, H, topk), H % 16 == 0, workspace >= mla_decode_part_bytes.
+hipError_t launch_mla_decode_rows(int is_fp16, const void* q, const void* kv, const int32_t* indices,
+                                  const int32_t* block_table, const int32_t* q_len, const int32_t* kv_len, int64_t B,
+                                  int64_t S, int64_t H, int64_t Skv, int64_t block_size, int64_t max_blocks,
+                                  int64_t topk, float sm_scale, int causal, void* out, float* lse, void* workspace,
+                                  hipStream_t stream) {
+  DecArgs a = {};
+  a.mla.idx = indices;
+  a.mla.block_table = block_table;
+  a.mla.q_len = q_len;
+  a.mla.kv_len = kv_len;
+  a.mla.S = (int)S;
+  a.mla.Skv = (int)Skv;
+  a.mla.block_size = (int)block_size;
+  a.mla.max_blocks = (int)max_blocks;
+  a.mla.causal = causal;
+  return dec_run(is_fp16, 4, a, q, kv, nullptr, B * S, H, topk, nullptr, sm_scale, out, lse, workspace, stream);
 }
 
 static size_t v4_lists_bytes(int64_t T, int64_t cap) {

@@ -1054,6 +1054,20 @@ size_t mla_workspace_bytes(int64_t tokens, int64_t H, int64_t topk) {
   return (size_t)splits * tokens * H * (kMlaDV * 2 + 4) + 256;
 }
 
+bool mla_decode_applies(int64_t T, int64_t H, int64_t topk);
+size_t mla_decode_part_bytes(int64_t T, int64_t H, int64_t topk);
+hipError_t launch_mla_decode_rows(int is_fp16, const void* q, const void* kv, const int32_t* indices,
+                                  const int32_t* block_table, const int32_t* q_len, const int32_t* kv_len, int64_t B,
+                                  int64_t S, int64_t H, int64_t Skv, int64_t block_size, int64_t max_blocks,
+                                  int64_t topk, float sm_scale, int causal, void* out, float* lse, void* workspace,
+                                  hipStream_t stream);
+
+// Workspace of launch_sparse_mla: decode rows take the decode kernel's partials.
+size_t sparse_mla_workspace_bytes(int64_t tokens, int64_t H, int64_t topk) {
+  return mla_decode_applies(tokens, H, topk) ? mla_decode_part_bytes(tokens, H, topk)
+                                             : mla_workspace_bytes(tokens, H, topk);
+}
+
 // Split partials of the allocation-free entry (dsa_sparse_mla_fwd_noalloc): one
 // array per GPU, resident from the library's load on that GPU until the process
 // ends.  64 MiB holds the split partials of decode batches up to 64 sequences x
@@ -1128,7 +1142,7 @@ static void mla_set_splits(MlaArgs& a, int64_t T, int64_t H, int64_t topk, void*
   }
 }
 
-// Caller validated: d_qk 576, d_v 512, H % 16 == 0, 16-bit inputs, workspace >= mla_workspace_bytes,
+// Caller validated: d_qk 576, d_v 512, H % 16 == 0, 16-bit inputs, workspace >= sparse_mla_workspace_bytes,
 // physical KV rows < 2^31.
 hipError_t launch_sparse_mla(int is_fp16, const void* q, const void* kv, const int32_t* indices,
                              const int32_t* block_table, const int32_t* q_len, const int32_t* kv_len, int64_t B,
@@ -1136,6 +1150,10 @@ hipError_t launch_sparse_mla(int is_fp16, const void* q, const void* kv, const i
                              float sm_scale, int causal, void* out, float* lse, void* workspace, hipStream_t stream) {
   const int64_t T = B * S;
   if (T == 0 || H == 0) return hipSuccess;
+  // Few query rows (decode): the decode kernel, slots across waves and chunks.
+  if (mla_decode_applies(T, H, topk))
+    return launch_mla_decode_rows(is_fp16, q, kv, indices, block_table, q_len, kv_len, B, S, H, Skv, block_size,
+                                  max_blocks, topk, sm_scale, causal, out, lse, workspace, stream);
   MlaArgs a;
   a.q = static_cast<const uint16_t*>(q);
   a.kv = static_cast<const uint16_t*>(kv);
