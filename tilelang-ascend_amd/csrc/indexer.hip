@@ -899,18 +899,17 @@ __global__ __launch_bounds__(256) void fused_pack_kernel(const u32x2* __restrict
   __shared__ int offs[kFusedMaxSeg + 2];
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
-  if (tid == 0) {
-    int tot = 0;
-    bool bad = false;
-    for (int s = 0; s < nseg; ++s) {
-      const int c = ccnt[row * nseg + s];
-      bad |= c > cap;
-      offs[s] = tot;
-      tot += min(c, cap);
+  if (tid < kWave) {  // wave 0: the chunks' counts at once, their prefix sums by a wave scan
+    const int c = tid < nseg ? ccnt[row * nseg + tid] : 0;
+    const int cc = min(c, cap);
+    const int inc = (int)wave_incl_scan((uint32_t)cc);
+    if (tid < nseg) offs[tid] = inc - cc;
+    const int tot = __shfl(inc, nseg - 1, kWave);
+    const bool over = __builtin_amdgcn_ballot_w64(tid < nseg && c > cap) != 0;
+    if (tid == 0) {
+      offs[nseg] = tot;
+      offs[kFusedMaxSeg + 1] = over || tot > ldc || (tot < k && thr[row] != -__builtin_huge_valf());
     }
-    bad |= tot > ldc || (tot < k && thr[row] != -__builtin_huge_valf());
-    offs[nseg] = tot;
-    offs[kFusedMaxSeg + 1] = bad;
   }
   __syncthreads();
   const int tot = offs[nseg];
@@ -923,13 +922,25 @@ __global__ __launch_bounds__(256) void fused_pack_kernel(const u32x2* __restrict
     return;
   }
   float* pv = pval + row * ldc;
-  for (int s = 0; s < nseg; ++s) {
-    const int64_t src = (row * nseg + s) * cap;
-    const int n = offs[s + 1] - offs[s];
-    for (int i = tid; i < n; i += 256) {
-      const u32x2 c = cand[src + i];
-      pv[offs[s] + i] = __uint_as_float(c.x);
-      pi[offs[s] + i] = (int32_t)c.y;
+  // Entry e of the packed row is entry e - offs[s] of chunk s (the last s with
+  // offs[s] <= e); four entries per thread per step, their loads issued together.
+  constexpr int kU = 4;
+  for (int e0 = tid; e0 < tot; e0 += 256 * kU) {
+    u32x2 c[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int e = min(e0 + 256 * u, tot - 1);  // clamped: a real entry, unused past tot
+      int sg = 0;
+      for (int z = 1; z < nseg; ++z) sg += e >= offs[z];
+      c[u] = cand[(row * nseg + sg) * cap + (e - offs[sg])];
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int e = e0 + 256 * u;
+      if (e < tot) {
+        pv[e] = __uint_as_float(c[u].x);
+        pi[e] = (int32_t)c[u].y;
+      }
     }
   }
   // The register top-k reads pidx[j * k] as segment flags: no stale flag past the row.
