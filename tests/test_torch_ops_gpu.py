@@ -80,6 +80,49 @@ def test_hip_graph_capture_and_replay(dsa, dev):
             assert torch.equal(a, b), f"replay {rep}"
 
 
+def test_hip_graph_capture_decode_shapes(dsa, dev):
+    # Decode-shaped calls in one graph: the key-split indexer (2 query rows), the decode
+    # kernel in 128-slot chunks with its combine (sparse MLA, 576-wide, topk 512) and in
+    # one workgroup per row (sparse_attn, topk 200); replays equal the eager results.
+    ops = dsa.load_torch_ops()
+    g = torch.Generator().manual_seed(8)
+    B, S, Skv, Hi, H, D, K = 1, 2, 2048, 64, 32, 128, 512
+    t = dict(qi=torch.randn(B * S * Hi, D, generator=g).to(torch.bfloat16).to(dev),
+             ki=torch.randn(B * Skv, D, generator=g).to(torch.bfloat16).to(dev),
+             w=(torch.randn(B, S, Hi, generator=g) / 8).to(dev),
+             q=(torch.randn(B, S, H, 576, generator=g) * 0.5).to(torch.bfloat16).to(dev),
+             kv=(torch.randn(B, Skv, 1, 576, generator=g) * 0.5).to(torch.bfloat16).to(dev),
+             shape=(B, S, Skv, Hi, H, D, K))
+    qa = (torch.randn(2, 3, 16, 512, generator=g)).to(torch.bfloat16).to(dev)
+    kva = (torch.randn(2, 300, 512, generator=g)).to(torch.bfloat16).to(dev)
+    sink = torch.randn(16, generator=g).to(dev)
+    ia = torch.randint(0, 300, (2, 3, 200), generator=g, dtype=torch.int32).to(dev)
+
+    def run():
+        a = ops.sparse_attn(qa, kva, sink, ia, 0.05)
+        return _pipeline(ops, t) + (tuple(a) if isinstance(a, (tuple, list)) else (a,))
+
+    want = run()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        got = run()
+    for rep in range(3):
+        for o in got:
+            o.zero_()
+        junk = torch.randn(1 << 20, device=dev).sum()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert junk.isfinite()
+        for a, b in zip(got, want):
+            assert torch.equal(a, b), f"replay {rep}"
+
+
 def _raises(fn, match):
     with pytest.raises(RuntimeError, match=match):
         fn()
