@@ -67,6 +67,26 @@ constexpr uint32_t kKeyInvalidMax = float_key_host(0xF149F2CAu);
 // out_idx[row][0] marker of the top-k paths: the row needs the exact radix path.
 constexpr int32_t kFallbackFlag = (int32_t)0x80000000;
 
+// Candidate (value bits, key) pairs of the fused indexer, read where its filter
+// pass left them: key chunk s of row r holds min(count[r * nseg + s], cap)
+// pairs from cand[(r * nseg + s) * cap] on, in key order; the row's packed
+// position p is entry p - (pairs in chunks below s) of the chunk s holding it.
+// A row goes back to the dense path (out_idx[row][0] = kFallbackFlag,
+// plen[row] = -1) when a chunk overflowed, when the chunks hold more than ldc
+// pairs, or when thr[row] is finite and fewer than k pairs reached it; every
+// other row gets plen[row] = its pair count.  pval / pidx (ldc per row) receive
+// the packed pairs of the rows the register top-k hands to the radix kernel.
+constexpr int kCandMaxSeg = 8;
+struct CandSegments {
+  const u32x2* cand;
+  const int32_t* count;
+  const float* thr;
+  int nseg, cap, ldc;
+  float* pval;
+  int32_t* pidx;
+  int32_t* plen;
+};
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));

@@ -807,23 +807,23 @@ hipError_t launch_indexer_logits(int kind, const void* q, const void* k, const f
 //      row has at most k valid keys);
 //   3. filter pass: the indexer again, keeping (logit, key) for logit >= thr,
 //      per (row, key chunk) in key order;
-//   4. per row, the kept keys of all chunks packed in key order; the row is
-//      flagged when a chunk overflowed or when thr is finite and fewer than k
-//      keys reached it -- otherwise every key outside the kept set is below thr,
-//      which is at most the k-th largest logit, so the top k (ties to the lower
-//      index included) lie in the kept set;
-//   5. the register top-k over the packed rows (positions map back to keys), and
-//      the exact radix top-k over the packed rows it could not bound (ties);
+//   4. per row, the kept keys of all chunks read in key order as one packed
+//      row, in place (no copy); the row is flagged when a chunk overflowed or
+//      when thr is finite and fewer than k keys reached it -- otherwise every
+//      key outside the kept set is below thr, which is at most the k-th largest
+//      logit, so the top k (ties to the lower index included) lie in the kept set;
+//   5. the register top-k over those rows (positions map back to keys), and the
+//      exact radix top-k over packed copies of the rows it could not bound (ties);
 //   6. rows flagged in step 4 only: their dense logits and the exact radix top-k.
 // Steps 5-6 give the same output as the dense path bit for bit; step 6 costs an
 // early exit per workgroup when nothing is flagged.
-hipError_t launch_topk_candidates(const float* cval, const int32_t* cidx, const int32_t* row_len, int64_t rows,
-                                  int64_t ldc, int64_t k, int32_t* out_idx, float* out_val, hipStream_t stream);
+hipError_t launch_topk_candidates(const CandSegments& cs, int64_t rows, int64_t k, int32_t* out_idx,
+                                  float* out_val, hipStream_t stream);
 hipError_t launch_topk_flagged(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k, int32_t* out_idx,
                                float* out_val, hipStream_t stream);
 
 constexpr int kFusedSampleTiles = 32;  // ~2048 sampled keys per row
-constexpr int kFusedMaxSeg = 8;
+constexpr int kFusedMaxSeg = kCandMaxSeg;
 constexpr int kFusedSampleChunkTiles = 8;  // sampled tiles per workgroup of the sample pass
 
 struct FusedPlan {
@@ -891,69 +891,11 @@ __global__ __launch_bounds__(256) void fused_threshold_kernel(const float* __res
   if (lane == 0) thr[row] = t;
 }
 
-__global__ __launch_bounds__(256) void fused_pack_kernel(const u32x2* __restrict__ cand,
-                                                         const int32_t* __restrict__ ccnt, int nseg, int cap,
-                                                         const float* __restrict__ thr, int k, int ldc,
-                                                         float* __restrict__ pval, int32_t* __restrict__ pidx,
-                                                         int32_t* __restrict__ plen) {
-  __shared__ int offs[kFusedMaxSeg + 2];
-  const int64_t row = blockIdx.x;
-  const int tid = threadIdx.x;
-  if (tid < kWave) {  // wave 0: the chunks' counts at once, their prefix sums by a wave scan
-    const int c = tid < nseg ? ccnt[row * nseg + tid] : 0;
-    const int cc = min(c, cap);
-    const int inc = (int)wave_incl_scan((uint32_t)cc);
-    if (tid < nseg) offs[tid] = inc - cc;
-    const int tot = __shfl(inc, nseg - 1, kWave);
-    const bool over = __builtin_amdgcn_ballot_w64(tid < nseg && c > cap) != 0;
-    if (tid == 0) {
-      offs[nseg] = tot;
-      offs[kFusedMaxSeg + 1] = over || tot > ldc || (tot < k && thr[row] != -__builtin_huge_valf());
-    }
-  }
-  __syncthreads();
-  const int tot = offs[nseg];
-  int32_t* pi = pidx + row * ldc;
-  if (offs[kFusedMaxSeg + 1]) {  // block-uniform
-    if (tid == 0) {
-      pi[0] = kFallbackFlag;  // the register top-k passes the flag on to the row's output
-      plen[row] = -1;         // and the exact kernel leaves it there
-    }
-    return;
-  }
-  float* pv = pval + row * ldc;
-  // Entry e of the packed row is entry e - offs[s] of chunk s (the last s with
-  // offs[s] <= e); four entries per thread per step, their loads issued together.
-  constexpr int kU = 4;
-  for (int e0 = tid; e0 < tot; e0 += 256 * kU) {
-    u32x2 c[kU];
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const int e = min(e0 + 256 * u, tot - 1);  // clamped: a real entry, unused past tot
-      int sg = 0;
-      for (int z = 1; z < nseg; ++z) sg += e >= offs[z];
-      c[u] = cand[(row * nseg + sg) * cap + (e - offs[sg])];
-    }
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const int e = e0 + 256 * u;
-      if (e < tot) {
-        pv[e] = __uint_as_float(c[u].x);
-        pi[e] = (int32_t)c[u].y;
-      }
-    }
-  }
-  // The register top-k reads pidx[j * k] as segment flags: no stale flag past the row.
-  for (int j = tid; (int64_t)j * k < ldc; j += 256)
-    if (j * k >= tot) pi[j * k] = -1;
-  if (tid == 0) plen[row] = tot;
-}
-
-__global__ __launch_bounds__(256) void fused_count_flagged_kernel(const int32_t* __restrict__ pidx, int64_t rows,
-                                                                  int64_t ldc, int32_t* __restrict__ count) {
+__global__ __launch_bounds__(256) void fused_count_flagged_kernel(const int32_t* __restrict__ plen, int64_t rows,
+                                                                  int32_t* __restrict__ count) {
   __shared__ int part[256 / kWave];
   int c = 0;
-  for (int64_t r = threadIdx.x; r < rows; r += 256) c += pidx[r * ldc] == kFallbackFlag;
+  for (int64_t r = threadIdx.x; r < rows; r += 256) c += plen[r] < 0;
   c = wave_sum_i(c);
   if ((threadIdx.x & (kWave - 1)) == 0) part[threadIdx.x / kWave] = c;
   __syncthreads();
@@ -966,8 +908,8 @@ hipError_t launch_fused_fallback_rows(const void* workspace, int64_t rows, int64
                                       int64_t k, int32_t* count, hipStream_t stream) {
   const FusedPlan p = fused_plan(rows, B, S1, S2, k);
   if (!p.fused) return hipErrorInvalidValue;
-  const int32_t* pidx = reinterpret_cast<const int32_t*>(static_cast<const uint8_t*>(workspace) + p.pidx);
-  hipLaunchKernelGGL(fused_count_flagged_kernel, dim3(1), dim3(256), 0, stream, pidx, p.rows, p.ldc, count);
+  const int32_t* plen = reinterpret_cast<const int32_t*>(static_cast<const uint8_t*>(workspace) + p.plen);
+  hipLaunchKernelGGL(fused_count_flagged_kernel, dim3(1), dim3(256), 0, stream, plen, p.rows, count);
   return hipGetLastError();
 }
 
@@ -1005,16 +947,11 @@ hipError_t launch_indexer_topk_fused(int kind, const void* q, const void* k, con
   a.tile_stride = kIdxKeyTile;
   a.key_chunk = (int)p.key_chunk;
   if ((e = launch_indexer_mode<kModeFilter>(kind, D, a, B, stream)) != hipSuccess) return e;
-  // 4. Pack.
-  float* pval = reinterpret_cast<float*>(ws + p.pval);
-  int32_t* pidx = reinterpret_cast<int32_t*>(ws + p.pidx);
-  int32_t* plen = reinterpret_cast<int32_t*>(ws + p.plen);
-  hipLaunchKernelGGL(fused_pack_kernel, dim3((unsigned)p.rows), dim3(256), 0, stream, a.cand,
-                     a.cand_cnt, p.nseg, p.cap, a.thr, (int)topk, (int)p.ldc, pval, pidx, plen);
-  if ((e = hipGetLastError()) != hipSuccess) return e;
-  // 5. Top-k over the packed rows.
-  if ((e = launch_topk_candidates(pval, pidx, plen, p.rows, p.ldc, topk, out_idx, out_val, stream)) != hipSuccess)
-    return e;
+  // 4-5. Top-k over the candidates where the filter left them.
+  const CandSegments cs = {a.cand, a.cand_cnt, a.thr, p.nseg, p.cap, (int)p.ldc,
+                           reinterpret_cast<float*>(ws + p.pval), reinterpret_cast<int32_t*>(ws + p.pidx),
+                           reinterpret_cast<int32_t*>(ws + p.plen)};
+  if ((e = launch_topk_candidates(cs, p.rows, topk, out_idx, out_val, stream)) != hipSuccess) return e;
   // 6. Rows still flagged: dense logits, then the exact radix top-k.
   float* dense = reinterpret_cast<float*>(ws);
   a.logits = dense;

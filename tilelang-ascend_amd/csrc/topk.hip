@@ -355,8 +355,9 @@ __device__ __forceinline__ uint32_t cand_key(float x) {
 
 // Ballot compaction of the scores >= t among a thread's registers into
 // lv/lp from index `base` on (wave-uniform), in register order; returns the
-// wave's count.  Position of register (c, j): e4 + 4096 c + j.
-template <int kChunks>
+// wave's count.  Position of register (c, j): e4 + 4096 c + j, or with
+// kLaneMajor e4 + 1024 (4 c + j).
+template <int kChunks, bool kLaneMajor = false>
 __device__ __forceinline__ uint32_t compact_scores(const float (&v)[kChunks][4], float t, uint32_t base, uint32_t e4,
                                                    uint32_t* lv, uint32_t* lp) {
   uint32_t wcnt = 0;  // wave-uniform
@@ -373,7 +374,7 @@ __device__ __forceinline__ uint32_t compact_scores(const float (&v)[kChunks][4],
       if (p) {
         const uint32_t i = lane_prefix(m, base + wcnt);
         lv[i] = __float_as_uint(val);
-        lp[i] = e4o + (uint32_t)(4 * kTopkThreads * c + j);
+        lp[i] = e4o + (uint32_t)(kLaneMajor ? kTopkThreads * (4 * c + j) : 4 * kTopkThreads * c + j);
       }
       wcnt += (uint32_t)__builtin_popcountll(m);
     }
@@ -407,11 +408,37 @@ __device__ __forceinline__ int rank_bin(const uint32_t* h, uint32_t r, uint32_t&
   return kSampleBins - 1 - 16 * L - i;
 }
 
-template <int kChunks, bool kFull>
+// Slot, in its row's candidate block, of packed position p (soff[z]: pairs in
+// the chunks below z; 2^30 past the last chunk).
+__device__ __forceinline__ int cand_slot(const int (&soff)[kCandMaxSeg], int cap, int p) {
+  int s = p;
+#pragma unroll
+  for (int z = 1; z < kCandMaxSeg; ++z) s += p >= soff[z] ? cap - (soff[z] - soff[z - 1]) : 0;
+  return s;
+}
+
+// A candidate row the register path hands to the radix kernel: its pairs
+// packed in position order into pval / pidx.
+__device__ void cand_spill(const CandSegments& cs, const u32x2* crow, const int (&soff)[kCandMaxSeg], int row,
+                           int nv) {
+  float* pv = cs.pval + (int64_t)row * cs.ldc;
+  int32_t* pi = cs.pidx + (int64_t)row * cs.ldc;
+  for (int p = threadIdx.x; p < nv; p += kTopkThreads) {
+    const u32x2 e = crow[cand_slot(soff, cs.cap, p)];
+    pv[p] = __uint_as_float(e.x);
+    pi[p] = (int32_t)e.y;
+  }
+}
+
+// kCand: the rows are the fused indexer's candidates in their key chunks (cs;
+// x, row_len and idx_map unused), positions 0..ldc; thread t holds positions
+// t + 1024 (4 c + j), so a wave's loads of one register are contiguous.
+template <int kChunks, bool kFull, bool kCand = false>
 __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8, 8))) void topk_reg_kernel(
     const float* __restrict__ x, int64_t ld, int n, int k, const int32_t* __restrict__ row_len,
     int32_t* __restrict__ out_idx, float* __restrict__ out_val, int nseg, int seg_len,
-    const int32_t* __restrict__ idx_map) {
+    const int32_t* __restrict__ idx_map, const CandSegments cs) {
+  static_assert(!(kFull && kCand), "candidate rows are ragged");
   __shared__ __align__(16) uint32_t lds[kLdsRegWords];
   uint32_t* lv = lds + kLdsVal;
   uint32_t* lp = lds + kLdsPos;
@@ -434,6 +461,29 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
   int nv = n;
   if (row_len) nv = min(max(row_len[row], 0), n);
   nv = min(max(nv - base, 0), seg_len);
+  int soff[kCandMaxSeg];
+  const u32x2* crow = nullptr;
+  if constexpr (kCand) {
+    crow = cs.cand + (int64_t)row * cs.nseg * cs.cap;
+    int tot = 0;
+    bool over = false;
+#pragma unroll
+    for (int z = 0; z < kCandMaxSeg; ++z) {
+      soff[z] = z < cs.nseg ? tot : (1 << 30);
+      if (z < cs.nseg) {
+        const int c = cs.count[(int64_t)row * cs.nseg + z];
+        over |= c > cs.cap;
+        tot += min(c, cs.cap);
+      }
+    }
+    const bool back = over || tot > cs.ldc || (tot < k && cs.thr[row] != -__builtin_huge_valf());
+    if (tid == 0) cs.plen[row] = back ? -1 : tot;
+    if (back) {
+      if (tid == 0) oi[0] = kFallbackFlag;  // the radix kernel leaves it for the dense path
+      return;                               // block-uniform
+    }
+    nv = tot;
+  }
   if (imap) {
     // Stage 2: a flagged segment (its first candidate index) sends the whole row to the exact path.
     bool flagged = false;
@@ -449,7 +499,15 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
   // 16-byte aligned, so the loads are straight-line.
   float v[kChunks][4];
   const int g_full = nv >> 2;
-  if constexpr (kFull) {
+  if constexpr (kCand) {
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int p = tid + kTopkThreads * (4 * c + j);
+        v[c][j] = p < nv ? __uint_as_float(crow[cand_slot(soff, cs.cap, p)].x) : -__builtin_huge_valf();
+      }
+  } else if constexpr (kFull) {
 #pragma unroll
     for (int c = 0; c < kChunks; ++c) {
       const f32x4 t = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(xr) + tid + c * kTopkThreads);
@@ -517,7 +575,7 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
   int lo = 0, hi = s_present + 1;
   int r = (int)(((int64_t)((k + kCandCap) / 2) * kTopkThreads + span - 1) / span);
   r = min(max(r, 1), hi);
-  const uint32_t e4 = 4u * (uint32_t)tid;
+  const uint32_t e4 = kCand ? (uint32_t)tid : 4u * (uint32_t)tid;
   const uint32_t wreg = (uint32_t)wave * kWaveCap;
   uint32_t total = 0, held = 0;
   bool all_present = false, dense = false;
@@ -548,7 +606,7 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
       __syncthreads();
       t = fmaxf(key_to_float(red[kRedThresh]), floor_t);
     }
-    const uint32_t wcnt = compact_scores<kChunks>(v, t, wreg, e4, lv, lp);
+    const uint32_t wcnt = compact_scores<kChunks, kCand>(v, t, wreg, e4, lv, lp);
     // cnt may hold an overrun's positions; clear it for the candidate histogram.
     reinterpret_cast<u32x4*>(cnt)[tid] = u32x4{0u, 0u, 0u, 0u};
     if (lane == 0) red[kRedCount + wave] = wcnt;
@@ -570,6 +628,7 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
     else lo = r;
     if (hi - lo <= 1 || tries + 1 == kMaxTries) {
       if (tid == 0) oi[0] = kFallbackFlag;
+      if constexpr (kCand) cand_spill(cs, crow, soff, row, nv);
       return;  // block-uniform
     }
     r = (lo + hi + 1) / 2;
@@ -583,7 +642,7 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
     cw += (uint32_t)DSA_DPP(0, cw, 0x114, 0xf);
     cw += (uint32_t)DSA_DPP(0, cw, 0x118, 0xf);
     const uint32_t start = (uint32_t)__builtin_amdgcn_readlane((int)(cw - own), wave);
-    (void)compact_scores<kChunks>(v, t, start, e4, lv, lp);
+    (void)compact_scores<kChunks, kCand>(v, t, start, e4, lv, lp);
     reinterpret_cast<u32x4*>(cnt)[tid] = u32x4{0u, 0u, 0u, 0u};  // the regions' overrun reached it
     __syncthreads();
   }
@@ -680,7 +739,8 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
       const uint32_t fin = start + rank;
       if (fin < (uint32_t)kk) {
         const uint32_t pp = bp & ((1u << kPosBits) - 1);
-        oi[fin] = imap ? imap[pp] : base + (int)pp;
+        if constexpr (kCand) oi[fin] = (int32_t)crow[cand_slot(soff, cs.cap, (int)pp)].y;
+        else oi[fin] = imap ? imap[pp] : base + (int)pp;
         if (ov) ov[fin] = val;
       }
     }
@@ -691,7 +751,10 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
   }
   if (kk > 0) {
     __syncthreads();
-    if (tid == 0 && red[kRedFlag]) oi[0] = kFallbackFlag;
+    if (red[kRedFlag]) {  // block-uniform
+      if (tid == 0) oi[0] = kFallbackFlag;
+      if constexpr (kCand) cand_spill(cs, crow, soff, row, nv);
+    }
   }
 }
 
@@ -712,7 +775,7 @@ static hipError_t launch_reg(const float* x, int64_t ld, int64_t rows, int64_t n
                     (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (ld & 3) == 0;
 #define DSA_REG(C, F)                                                                                         \
   hipLaunchKernelGGL((topk_reg_kernel<C, F>), grid, block, 0, stream, x, ld, (int)n, (int)k, row_len, out_idx, \
-                     out_val, nseg, (int)seg_len, idx_map)
+                     out_val, nseg, (int)seg_len, idx_map, CandSegments{})
 #define DSA_REG2(C) \
   if (full) DSA_REG(C, true); else DSA_REG(C, false)
   if (chunks == 1) DSA_REG2(1);
@@ -784,17 +847,27 @@ hipError_t launch_topk(const float* x, int64_t ld, int64_t rows, int64_t n, int6
   return launch_rows(x, ld, rows, n, k, row_len, sorted, out_idx, out_val, only_flagged, nullptr, stream);
 }
 
-// Top-k over packed candidate rows (the fused indexer): values cval [rows, ldc], the first
-// row_len[row] present, positions mapped to key indices through cidx (whose entries at
-// multiples of k must not be stale flags).  The register path, then the exact radix
-// kernel on the rows it could not bound.  Rows marked with row_len -1 and cidx[row][0] =
-// kFallbackFlag come out flagged in out_idx[row][0].
-hipError_t launch_topk_candidates(const float* cval, const int32_t* cidx, const int32_t* row_len, int64_t rows,
-                                  int64_t ldc, int64_t k, int32_t* out_idx, float* out_val, hipStream_t stream) {
+// Top-k over the fused indexer's candidate rows (cs: 1 <= nseg <= kCandMaxSeg, ldc <= kRegMax):
+// the register path reads the pairs in their key chunks; the exact radix kernel then takes the
+// rows it could not bound, from the packed copies it left in cs.pval / cs.pidx.  Rows that go
+// back to the dense path come out flagged in out_idx[row][0].
+hipError_t launch_topk_candidates(const CandSegments& cs, int64_t rows, int64_t k, int32_t* out_idx,
+                                  float* out_val, hipStream_t stream) {
   if (rows == 0) return hipSuccess;
-  hipError_t e = launch_reg(cval, ldc, rows, ldc, k, row_len, out_idx, out_val, 1, ldc, cidx, stream);
+  if (cs.nseg < 1 || cs.nseg > kCandMaxSeg || cs.ldc > kRegMax || k > kListCap) return hipErrorInvalidValue;
+  const int n = cs.ldc;
+  const dim3 grid((unsigned)rows), block(kTopkThreads);
+#define DSA_CAND(C)                                                                                             \
+  hipLaunchKernelGGL((topk_reg_kernel<C, false, true>), grid, block, 0, stream, cs.pval, (int64_t)n, n, (int)k, \
+                     nullptr, out_idx, out_val, 1, n, nullptr, cs)
+  if (n <= 4 * kTopkThreads) DSA_CAND(1);
+  else if (n <= 8 * kTopkThreads) DSA_CAND(2);
+  else if (n <= 16 * kTopkThreads) DSA_CAND(4);
+  else DSA_CAND(8);
+#undef DSA_CAND
+  hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  return launch_rows(cval, ldc, rows, ldc, k, row_len, 1, out_idx, out_val, 1, cidx, stream);
+  return launch_rows(cs.pval, cs.ldc, rows, cs.ldc, k, cs.plen, 1, out_idx, out_val, 1, cs.pidx, stream);
 }
 
 // The exact radix kernel for the rows whose out_idx[row][0] is kFallbackFlag (sorted output).
