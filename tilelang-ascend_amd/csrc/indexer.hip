@@ -801,10 +801,10 @@ hipError_t launch_indexer_logits(int kind, const void* q, const void* k, const f
 // Fused indexer -> top-k.  The logits of a row are never written whole:
 //   1. sample pass: the logits of the first 64 keys of every 64 F (about 2048
 //      keys per row);
-//   2. per row (at the end of the sample pass, or in a kernel of its own when
-//      the sample spans several key chunks): thr = the r-th largest valid sampled logit, r = mu + 4 sqrt(mu) + 2 with mu = k * sampled / valid the
-//      expected number of sampled keys in the row's top k (thr = -inf when the
-//      row has at most k valid keys);
+//   2. per row, in a kernel of its own (the sample spans several workgroups):
+//      thr = the r-th largest valid sampled logit, r = mu + 4 sqrt(mu) + 2 with
+//      mu = k * sampled / valid the expected number of sampled keys in the
+//      row's top k (thr = -inf when the row has at most k valid keys);
 //   3. filter pass: the indexer again, keeping (logit, key) for logit >= thr,
 //      per (row, key chunk) in key order;
 //   4. per row, the kept keys of all chunks read in key order as one packed
