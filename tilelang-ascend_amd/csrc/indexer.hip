@@ -29,6 +29,8 @@
 // multiply by w[t, h], sum the lane's 4 head rows, then two cross-lane adds
 // over the 4 row groups.  After four 16-key slices lane l holds key l of the
 // 64-key tile, so each token's logits go out as one coalesced 256-byte store.
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace dsa {
@@ -799,8 +801,8 @@ hipError_t launch_indexer_logits(int kind, const void* q, const void* k, const f
 
 // ---------------------------------------------------------------------------
 // Fused indexer -> top-k.  The logits of a row are never written whole:
-//   1. sample pass: the logits of the first 64 keys of every 64 F (about 2048
-//      keys per row);
+//   1. sample pass: the logits of the first 64 keys of every 64 F (1024 to
+//      2048 keys per row);
 //   2. per row, in a kernel of its own (the sample spans several workgroups):
 //      thr = the r-th largest valid sampled logit, r = mu + 4 sqrt(mu) + 2 with
 //      mu = k * sampled / valid the expected number of sampled keys in the
@@ -822,7 +824,13 @@ hipError_t launch_topk_candidates(const CandSegments& cs, int64_t rows, int64_t 
 hipError_t launch_topk_flagged(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k, int32_t* out_idx,
                                float* out_val, hipStream_t stream);
 
-constexpr int kFusedSampleTiles = 32;  // ~2048 sampled keys per row
+// Sampled tiles per row: S2 / (2 k) clamped to [16, 32], so that mu = k * sampled / S2 stays
+// at least 32 where the row allows it (a smaller mu widens the spread of the kept count
+// relative to its mean, and rows whose kept keys outrun ldc = 4 k go back to the dense
+// path: 8 tiles at 131072 keys, k = 2048, sent 2% of the rows back), while short rows
+// sample half as many keys as long ones (C2: the sample pass at 1/32 of the keys, not 1/16).
+constexpr int kFusedSampleTilesMin = 16;
+constexpr int kFusedSampleTilesMax = 32;
 constexpr int kFusedMaxSeg = kCandMaxSeg;
 constexpr int kFusedSampleChunkTiles = 8;  // sampled tiles per workgroup of the sample pass
 
@@ -847,7 +855,9 @@ static FusedPlan fused_plan(int64_t rows, int64_t B, int64_t S1, int64_t S2, int
   if (p.key_chunk < min_chunk) p.key_chunk = min_chunk;
   p.nseg = (int)((S2 + p.key_chunk - 1) / p.key_chunk);
   const int64_t tiles = (S2 + kIdxKeyTile - 1) / kIdxKeyTile;
-  const int64_t F = tiles / kFusedSampleTiles > 1 ? tiles / kFusedSampleTiles : 1;
+  const int64_t sample_tiles = std::min<int64_t>(std::max<int64_t>(S2 / (2 * k), kFusedSampleTilesMin),
+                                                 kFusedSampleTilesMax);
+  const int64_t F = tiles / sample_tiles > 1 ? tiles / sample_tiles : 1;
   p.tile_stride = F * kIdxKeyTile;
   p.sample_ld = (S2 + p.tile_stride - 1) / p.tile_stride * kIdxKeyTile;  // <= 4096: F >= tiles / 64
   const int64_t cap4k = (4 * k + 63) & ~int64_t(63);
