@@ -896,8 +896,9 @@ __global__ __launch_bounds__(256) void fused_threshold_kernel(const float* __res
   const int64_t row = (int64_t)blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
   if (row >= rows) return;
   const float* sr = sample + row * sld;
-  const float t = sld <= 32 * kWave ? row_threshold<32>(sr, (int)sld, row_valid[row], k, lane)
-                                    : row_threshold<64>(sr, (int)sld, row_valid[row], k, lane);
+  const float t = sld <= 16 * kWave   ? row_threshold<16>(sr, (int)sld, row_valid[row], k, lane)
+                  : sld <= 32 * kWave ? row_threshold<32>(sr, (int)sld, row_valid[row], k, lane)
+                                      : row_threshold<64>(sr, (int)sld, row_valid[row], k, lane);
   if (lane == 0) thr[row] = t;
 }
 
