@@ -18,6 +18,8 @@
 // (k - #above) lowest-index elements equal to the threshold win the ties,
 // deterministically.  `sorted` then runs a bitonic network over
 // (key << 32 | ~index) in LDS.
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace dsa {
@@ -27,6 +29,7 @@ constexpr int kTopkWaves = kTopkThreads / kWave;
 constexpr int kHistBins = 2048;
 constexpr int kRedWords = 64;
 constexpr int kLdsBytes = 160 * 1024;
+constexpr int kRowsStaticLds = (kTopkThreads / kWave) * 8;  // topk_rows_kernel's flag masks
 
 // Inclusive wave scan and wave reductions on DPP (row shifts, then the row
 // broadcasts 15 and 31).
@@ -70,18 +73,18 @@ __device__ __forceinline__ uint32_t load_key(const float* __restrict__ xr, const
   return float_key(xr[i]);
 }
 
+// One row by the whole workgroup (every thread calls it, with the same row).
 template <bool kCached>
-__global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(
-    const float* __restrict__ x, int64_t ld, int n, int k, const int32_t* __restrict__ row_len,
-    int sorted, int kpad, int32_t* __restrict__ out_idx, float* __restrict__ out_val, int only_flagged,
-    const int32_t* __restrict__ idx_map) {
+__device__ __forceinline__ void radix_row(const int row, const float* __restrict__ x, int64_t ld, int n, int k,
+                                          const int32_t* __restrict__ row_len, int sorted, int kpad,
+                                          int32_t* __restrict__ out_idx, float* __restrict__ out_val,
+                                          int only_flagged, const int32_t* __restrict__ idx_map) {
   extern __shared__ __align__(16) uint32_t lds[];
   uint32_t* hist = lds;                                     // kHistBins
   uint32_t* red = hist + kHistBins;                         // kRedWords
   uint64_t* sbuf = reinterpret_cast<uint64_t*>(red + kRedWords);  // kpad (sorted only)
   uint32_t* keys = reinterpret_cast<uint32_t*>(sbuf + (sorted ? kpad : 0));
 
-  const int row = blockIdx.x;
   const int tid = threadIdx.x;
   const float* __restrict__ xr = x + (int64_t)row * ld;
   int32_t* __restrict__ oi = out_idx + (int64_t)row * k;
@@ -231,6 +234,44 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(
   for (int i = kk + tid; i < k; i += kTopkThreads) {
     oi[i] = -1;
     if (ov) ov[i] = -__builtin_huge_valf();
+  }
+}
+
+// Every row (grid = rows), or with only_flagged the rows whose out_idx[row][0]
+// is kFallbackFlag: workgroup g then takes rows g, g + G, g + 2G, ... (G =
+// gridDim.x), reads 1024 of their flags at once and runs the flagged ones, so a
+// launch with nothing flagged costs one flag load per thread instead of a
+// workgroup (and its LDS allocation) per row.
+template <bool kCached>
+__global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(
+    const float* __restrict__ x, int64_t ld, int n, int k, const int32_t* __restrict__ row_len,
+    int sorted, int kpad, int32_t* __restrict__ out_idx, float* __restrict__ out_val, int only_flagged,
+    const int32_t* __restrict__ idx_map, int rows) {
+  if (!only_flagged) {
+    radix_row<kCached>(blockIdx.x, x, ld, n, k, row_len, sorted, kpad, out_idx, out_val, 0, idx_map);
+    return;
+  }
+  __shared__ uint64_t flagged[kTopkWaves];
+  static_assert(sizeof(flagged) == kRowsStaticLds, "static LDS of the flagged walk");
+  const int tid = threadIdx.x;
+  const int G = gridDim.x;
+  for (int64_t r0 = blockIdx.x; r0 < rows; r0 += (int64_t)G * kTopkThreads) {
+    const int64_t r = r0 + (int64_t)tid * G;
+    const bool f = r < rows && out_idx[r * k] == kFallbackFlag;
+    const uint64_t m = __builtin_amdgcn_ballot_w64(f);
+    if ((tid & (kWave - 1)) == 0) flagged[tid / kWave] = m;
+    __syncthreads();
+    for (int w = 0; w < kTopkWaves; ++w) {
+      uint64_t mw = flagged[w];  // block-uniform
+      while (mw) {
+        const int b = __builtin_ctzll(mw);
+        mw &= mw - 1;
+        radix_row<kCached>((int)(r0 + (int64_t)(w * kWave + b) * G), x, ld, n, k, row_len, sorted, kpad, out_idx,
+                           out_val, 1, idx_map);
+        __syncthreads();  // the row's LDS is free before the next one
+      }
+    }
+    __syncthreads();  // every wave has read `flagged` before the next round writes it
   }
 }
 
@@ -883,19 +924,21 @@ static hipError_t launch_rows(const float* x, int64_t ld, int64_t rows, int64_t 
   const int kpad = sorted ? next_pow2((int)(k < 2 ? 2 : k)) : 0;
   const size_t base = (size_t)(kHistBins + kRedWords) * 4 + (size_t)kpad * 8;
   const size_t cached = base + (size_t)n * 4;
-  const bool use_cache = cached <= (size_t)kLdsBytes;
+  const bool use_cache = cached <= (size_t)(kLdsBytes - kRowsStaticLds);
   const size_t lds = use_cache ? cached : base;
-  const dim3 grid((unsigned)rows), block(kTopkThreads);
+  // Flagged rows only: one workgroup per CU (two without the LDS row cache) walks its share.
+  const int64_t g = only_flagged ? std::min<int64_t>(rows, use_cache ? 256 : 512) : rows;
+  const dim3 grid((unsigned)g), block(kTopkThreads);
   if (use_cache) {
-    const hipError_t ea = set_dynamic_lds_once<topk_rows_kernel<true>>(kLdsBytes);
+    const hipError_t ea = set_dynamic_lds_once<topk_rows_kernel<true>>(kLdsBytes - kRowsStaticLds);
     if (ea != hipSuccess) return ea;
     hipLaunchKernelGGL(topk_rows_kernel<true>, grid, block, lds, stream, x, ld, (int)n, (int)k, row_len,
-                       sorted, kpad, out_idx, out_val, only_flagged, idx_map);
+                       sorted, kpad, out_idx, out_val, only_flagged, idx_map, (int)rows);
   } else {
-    const hipError_t ea = set_dynamic_lds_once<topk_rows_kernel<false>>(kLdsBytes);
+    const hipError_t ea = set_dynamic_lds_once<topk_rows_kernel<false>>(kLdsBytes - kRowsStaticLds);
     if (ea != hipSuccess) return ea;
     hipLaunchKernelGGL(topk_rows_kernel<false>, grid, block, lds, stream, x, ld, (int)n, (int)k, row_len,
-                       sorted, kpad, out_idx, out_val, only_flagged, idx_map);
+                       sorted, kpad, out_idx, out_val, only_flagged, idx_map, (int)rows);
   }
   return hipGetLastError();
 }
