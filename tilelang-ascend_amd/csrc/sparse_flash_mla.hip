@@ -528,11 +528,15 @@ __global__ __launch_bounds__(256) void v4_decode_rows_kernel(DecArgs a) {
     dec_lgkm_wait<8>(kr[0]);
 #pragma unroll
     for (int st = 0; st < 8; ++st) sc = dec_mfma_qk<kF16>(kr[0][st], qb[st], sc);
+    // LDS reads retire in issue order: the wait for kr[1] must count the reads
+    // issued after it (the two tails, or the first eight V^T reads), since with
+    // nothing behind kr[1] a count of 8 would not wait for it at all.
     if constexpr (kD == 576) {
 #pragma unroll
       for (int q = 0; q < 2; ++q) dec_b128_read(krt[q], kt0 + 16 * ((4 * q + g) ^ (2 * ((r >> 2) & 3))));
       dec_lgkm_wait<2>(kr[1]);
     } else {
+      reads(0);
       dec_lgkm_wait<8>(kr[1]);
     }
 #pragma unroll
@@ -542,8 +546,6 @@ __global__ __launch_bounds__(256) void v4_decode_rows_kernel(DecArgs a) {
       dec_lgkm_wait<8>(krt);
 #pragma unroll
       for (int q = 0; q < 2; ++q) sc = dec_mfma_qk<kF16>(krt[q], qb[16 + q], sc);
-    } else {
-      reads(0);
     }
     reads(1);
     float s2[4], bm = -__builtin_huge_valf();
