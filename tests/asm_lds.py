@@ -145,18 +145,17 @@ def _step(state: tuple, inst, kernel: str, findings: list) -> tuple:
         elif ops.strip() == "0":
             state = ()
         return state
-    used = _regs(ops)
-    if used:
-        for o in state:
-            if o.regs & used:
-                findings.append(Finding(kernel, ln, text, o.line))
-                break
-    if mn.startswith("ds_"):
-        writes = mn.startswith(("ds_read", "ds_load", "ds_bpermute", "ds_permute", "ds_swizzle")) or "_rtn" in mn
-        dst = set()
-        if writes:
-            first = ops.split(",")[0]
-            dst = _regs(first)
+    lds = mn.startswith("ds_")
+    writes = lds and (mn.startswith(("ds_read", "ds_load", "ds_bpermute", "ds_permute", "ds_swizzle")) or "_rtn" in mn)
+    dst = _regs(ops.split(",")[0]) if writes else set()
+    # An LDS load may target a register that an earlier LDS load still has in flight: they
+    # return in order.  Its other operands, and every other instruction's, must have landed.
+    used = _regs(ops.split(",", 1)[1]) if writes and "," in ops else _regs(ops)
+    for o in state:
+        if o.regs & used or (o.scalar and o.regs & dst):
+            findings.append(Finding(kernel, ln, text, o.line))
+            break
+    if lds:
         state = _retire(state, _LGKM_MAX - 1) + (Op(False, frozenset(dst), ln),)
     elif mn.startswith(("s_load", "s_buffer_load", "s_memtime", "s_memrealtime", "s_dcache", "s_sendmsg",
                         "s_scratch_load", "s_get_waveid")) or mn.startswith("flat_"):

@@ -60,7 +60,7 @@ def test_checker_sees_a_short_wait():
         (19, "\tv_mfma_f32_16x16x32_f16 v[80:83], v[32:35], v[90:93], v[80:83]"), (20, "\ts_endpgm")]
     assert [f.line for f in asm_lds.check_kernel("k", body2)] == [19]
     # Across a loop back edge: a read issued at the bottom and used at the top after no wait.
-    loop = [(1, "\ts_mov_b32 s2, 0"), (2, ".LBB0_1:"), (3, "\tv_add_u32_e32 v1, v0, v0"),
+    loop = [(1, "\ts_mov_b32 s2, 0"), (2, ".LBB0_1:"), (3, "\tv_add_u32_e32 v1, v0, v3"),
             (4, "\tds_read_b32 v0, v2"), (5, "\ts_cbranch_scc1 .LBB0_1"), (6, "\ts_waitcnt lgkmcnt(0)"),
             (7, "\ts_endpgm")]
     assert [f.line for f in asm_lds.check_kernel("k", loop)] == [3]
