@@ -295,7 +295,8 @@ int dsa_sparse_flash_mla(int kind, const void* q, int64_t T, int64_t H, int64_t 
  * count twice, as in the golden), K = V = the 512-wide row, and the sink of
  * head h adds exp(sinks[h]) to the softmax denominator.
  *  q [B, M, H, 512]; kv [B, N, 512]; topk_idxs [B, M, topk] int32;
- *  sinks [H] fp32 or NULL; out [B, M, H, 512] (input dtype); lse [B, M, H] fp32.
+ *  sinks [H] fp32 or NULL; out [B, M, H, 512] fp32 (the fp32 accumulator, as the
+ *  reference kernel writes it: sparse_attention.py:56); lse [B, M, H] fp32.
  */
 size_t dsa_sparse_attn_sink_workspace_size(int64_t B, int64_t M, int64_t H, int64_t topk);
 

@@ -40,7 +40,7 @@ def test_binding_signatures_cover_the_header(dsa):
 
 def test_abi_rejects_bad_arguments_without_launching(dsa):
     lib = dsa.load_library()
-    assert lib.dsa_abi_version() == 104
+    assert lib.dsa_abi_version() == 105
     # k out of range
     assert lib.dsa_topk_select(None, 8, 1, 8, 0, None, 1, None, None, None) == 1
     assert b"k must be" in lib.dsa_last_error_message()

@@ -3,9 +3,14 @@ SFA decode entry ``sparse_attn_tilelang`` against the CPU oracle.
 
 ``sparse_attn`` (examples/deepseek_v4/sparse_attention.py:171-241): the reference
 test's own shape (b=1, m=256, n=256, h=64, d=512, topk=128, indices from randint, so
-duplicates occur, bf16 randn inputs, fp32 sinks) at its own tolerance, atol = rtol =
-1e-2, plus -1 slots, batches, 128 heads, fp16 and the split path (long index lists
-on few rows).  LSE within 1e-3 of the exact oracle.
+duplicates occur, bf16 randn inputs, fp32 sinks), plus -1 slots, batches, 128 heads,
+fp16 and the split path (long index lists on few rows).  The output is the fp32
+accumulator, as the reference kernel writes it (sparse_attention.py:56): out within
+rtol = 2e-3 of the exact oracle, atol 2e-3 for fp16 and 4e-3 for bf16 (the reference
+test's own bar is 1e-2; the probabilities enter P V rounded to the input dtype, which on
+unit-scale data moves an output by up to ~2e-3 for bf16), and most elements not
+representable in 16 bits: a 16-bit rounding of the output (2^-9 relative for bf16) would
+slip under those bars, so that check is what sees it.  LSE within 1e-3 of the exact oracle.
 
 ``sparse_attn_tilelang`` (examples/sparse_flash_attention/bench_sfa/bench_sfa.py:10-120):
 the benchmark's inputs (T=1, 128 heads, 512 + 64 rope, paged KV in 128-row blocks,
@@ -36,13 +41,23 @@ def _run(dsa, dev, q, kv, sink, idx, scale):
     return out.cpu()
 
 
+def _check_out(out, want, dtype):
+    """fp32 output within the bar of the oracle, and not a 16-bit value widened."""
+    assert out.dtype == torch.float32
+    torch.testing.assert_close(out, want, rtol=2e-3, atol=4e-3 if dtype == torch.bfloat16 else 2e-3)
+    nz = out != 0
+    if nz.sum() > 0:
+        exact16 = (out[nz].to(dtype).float() == out[nz]).float().mean().item()
+        assert exact16 < 0.05, f"{exact16:.3f} of the outputs are {dtype} values"
+
+
 def _lse(dsa, dev, q, kv, sink, idx, scale):
     """The LSE the kernel writes, read through the C ABI."""
     b, m, h, d = q.shape
     lib = dsa.load_library()
     qd, kvd, idxd = q.to(dev), kv.to(dev), idx.to(dev)
     sk = None if sink is None else sink.to(dev)
-    out = torch.empty((b, m, h, d), dtype=q.dtype, device=dev)
+    out = torch.empty((b, m, h, d), dtype=torch.float32, device=dev)
     lse = torch.empty((b, m, h), dtype=torch.float32, device=dev)
     nbytes = lib.dsa_sparse_attn_sink_workspace_size(b, m, h, idx.shape[2])
     ws = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=dev)
@@ -56,14 +71,14 @@ def _lse(dsa, dev, q, kv, sink, idx, scale):
 
 
 def test_reference_test_shape(dsa, dev):
-    """sparse_attention.py:216-241: shape 1, bf16, scale 512**-0.5, tolerance 1e-2."""
+    """sparse_attention.py:216-241: shape 1, bf16, scale 512**-0.5 (the reference's bar is 1e-2)."""
     print("sparse_attn reference shape b=1 m=256 n=256 h=64 topk=128", flush=True)
     q, kv, sink, idx = _inputs(1, 256, 256, 64, 512, 128, torch.bfloat16, 41)
     scale = 512 ** -0.5
     out = _run(dsa, dev, q, kv, sink, idx, scale)
     want, want_lse = ref.sparse_attn_sink(q, kv, sink, idx, scale)
-    assert out.dtype == torch.float32 and out.shape == (1, 256, 64, 512)
-    torch.testing.assert_close(out, want, rtol=1e-2, atol=1e-2)
+    assert out.shape == (1, 256, 64, 512)
+    _check_out(out, want, torch.bfloat16)
     torch.testing.assert_close(_lse(dsa, dev, q, kv, sink, idx, scale), want_lse, rtol=1e-3, atol=1e-3)
 
 
@@ -73,7 +88,7 @@ def test_reference_small_shape_via_builder(dsa, dev):
     kernel = dsa.sparse_attn_kernel(h=16, d=512, scale=512 ** -0.5)
     out = kernel(q.to(dev), kv.to(dev), sink.to(dev), idx.to(dev)).cpu()
     want, _ = ref.sparse_attn_sink(q, kv, sink, idx, 512 ** -0.5)
-    torch.testing.assert_close(out, want, rtol=1e-2, atol=1e-2)
+    _check_out(out, want, torch.bfloat16)
     # Default scale is 1/sqrt(d), as in the reference builder.
     out2 = dsa.sparse_attn_kernel(h=16, d=512)(q.to(dev), kv.to(dev), sink.to(dev), idx.to(dev)).cpu()
     torch.testing.assert_close(out2, out, rtol=0, atol=0)
@@ -92,7 +107,7 @@ def test_masked_slots_batches_and_heads(dsa, dev, dtype):
     scale = 0.05
     out = _run(dsa, dev, q, kv, sink, idx, scale)
     want, want_lse = ref.sparse_attn_sink(q, kv, sink, idx, scale)
-    torch.testing.assert_close(out, want, rtol=1e-2, atol=1e-2)
+    _check_out(out, want, dtype)
     torch.testing.assert_close(_lse(dsa, dev, q, kv, sink, idx, scale), want_lse, rtol=1e-3, atol=1e-3)
     assert torch.count_nonzero(out[0, 0]) == 0
 
@@ -114,7 +129,7 @@ def test_decode_rows_masked_slots(dsa, dev, dtype):
     for sk in (sink, None):
         out = _run(dsa, dev, q, kv, sk, idx, scale)
         want, want_lse = ref.sparse_attn_sink(q, kv, sk, idx, scale)
-        torch.testing.assert_close(out, want, rtol=1e-2, atol=1e-2)
+        _check_out(out, want, dtype)
         torch.testing.assert_close(_lse(dsa, dev, q, kv, sk, idx, scale), want_lse, rtol=1e-3, atol=1e-3)
         assert torch.count_nonzero(out[0, 1]) == 0
 
@@ -133,7 +148,7 @@ def test_decode_rows_chunked(dsa, dev, dtype):
     for sk in (sink, None):
         out = _run(dsa, dev, q, kv, sk, idx, scale)
         want, want_lse = ref.sparse_attn_sink(q, kv, sk, idx, scale)
-        torch.testing.assert_close(out, want, rtol=1e-2, atol=1e-2)
+        _check_out(out, want, dtype)
         torch.testing.assert_close(_lse(dsa, dev, q, kv, sk, idx, scale), want_lse, rtol=1e-3, atol=1e-3)
         assert torch.count_nonzero(out[0, 1]) == 0
 
@@ -146,7 +161,7 @@ def test_split_path_and_no_sink(dsa, dev):
     for sk in (sink, None):
         out = _run(dsa, dev, q, kv, sk, idx, scale)
         want, want_lse = ref.sparse_attn_sink(q, kv, sk, idx, scale)
-        torch.testing.assert_close(out, want, rtol=1e-2, atol=1e-2)
+        _check_out(out, want, torch.bfloat16)
         torch.testing.assert_close(_lse(dsa, dev, q, kv, sk, idx, scale), want_lse, rtol=1e-3, atol=1e-3)
 
 

@@ -27,11 +27,10 @@ hipError_t launch_sparse_mla(int is_fp16, const void* q, const void* kv, const i
                              const int32_t* q_len, const int32_t* kv_len, int64_t B, int64_t S, int64_t H,
                              int64_t Skv, int64_t block_size, int64_t max_blocks, int64_t topk, float sm_scale,
                              int causal, void* out, float* lse, void* workspace, hipStream_t stream);
-size_t mla_workspace_bytes(int64_t tokens, int64_t H, int64_t topk);
 size_t sparse_mla_workspace_bytes(int64_t tokens, int64_t H, int64_t topk);
 size_t mla_scratch_bytes();
 hipError_t mla_scratch_ptr(void** out);
-size_t v4_workspace_bytes(int64_t T, int64_t H, int64_t cap);
+size_t v4_workspace_bytes(int64_t T, int64_t H, int64_t cap, bool out_f32);
 size_t sparse_attn_sink_workspace_bytes(int64_t T, int64_t H, int64_t K);
 hipError_t launch_sparse_attn_sink(int is_fp16, const void* q, const void* kv, const int32_t* idx, int64_t B,
                                    int64_t M, int64_t H, int64_t N, int64_t K, const float* sinks, float sm_scale,
@@ -68,7 +67,7 @@ constexpr int64_t dsa_kSrc2Limit = 0x40000000;
 
 extern "C" {
 
-int dsa_abi_version(void) { return 104; }
+int dsa_abi_version(void) { return 105; }
 
 const char* dsa_last_error_message(void) { return g_msg; }
 
@@ -359,7 +358,7 @@ static int64_t v4_cap(int64_t ori_win_left, int64_t cmp_slots) { return ori_win_
 
 size_t dsa_sparse_flash_mla_workspace_size(int64_t T, int64_t H, int64_t ori_win_left, int64_t cmp_slots) {
   if (T <= 0 || H <= 0 || ori_win_left < 0 || cmp_slots < 0) return 0;
-  return dsa::v4_workspace_bytes(T, H, v4_cap(ori_win_left, cmp_slots));
+  return dsa::v4_workspace_bytes(T, H, v4_cap(ori_win_left, cmp_slots), false);
 }
 
 int dsa_sparse_flash_mla(int kind, const void* q, int64_t T, int64_t H, int64_t D, int64_t B, const int32_t* q_start,

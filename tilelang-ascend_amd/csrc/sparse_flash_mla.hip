@@ -26,8 +26,9 @@ namespace dsa {
 
 hipError_t launch_sparse_mla_rows(int is_fp16, const void* q, const void* kv, const void* kv2, const int32_t* rows,
                                   const int32_t* count, int64_t T, int64_t H, int64_t cap, const float* sinks,
-                                  float sm_scale, void* out, float* lse, void* workspace, hipStream_t stream);
-size_t mla_workspace_bytes(int64_t tokens, int64_t H, int64_t topk);
+                                  float sm_scale, void* out, float* lse, void* workspace, hipStream_t stream,
+                                  int out_f32);
+size_t mla_workspace_bytes(int64_t tokens, int64_t H, int64_t topk, bool f32);
 
 constexpr int32_t kCmpTag = 0x40000000;  // the gather kernel's second-source bit
 
@@ -193,6 +194,7 @@ struct DecArgs {
   const int32_t* count;   // [T]; -1: padded row
   const float* sinks;     // [H] or null
   uint16_t* out;          // [T, H, 512]
+  float* out32;           // [T, H, 512] fp32 instead of out, or null
   float* lse;             // [T, H]
   int T, H, cap;
   int chunk, nsplit;      // slots per workgroup, workgroups per (row, 16 heads)
@@ -378,8 +380,15 @@ __global__ __launch_bounds__(256) void v4_decode_rows_kernel(DecArgs a) {
       if (blockIdx.z == 0 && tid < 16) a.part[((int64_t)t * a.H + h0 + tid) * a.nsplit * kDecPart + 513] = -1.f;
       return;
     }
-    for (int e = tid; e < 16 * 64; e += 256)
-      *reinterpret_cast<u32x4*>(a.out + ((int64_t)t * a.H + h0 + e / 64) * 512 + 8 * (e % 64)) = u32x4{0, 0, 0, 0};
+    for (int e = tid; e < 16 * 64; e += 256) {
+      const int64_t at = ((int64_t)t * a.H + h0 + e / 64) * 512 + 8 * (e % 64);
+      if (a.out32) {
+        *reinterpret_cast<f32x4*>(a.out32 + at) = f32x4{0.f, 0.f, 0.f, 0.f};
+        *reinterpret_cast<f32x4*>(a.out32 + at + 4) = f32x4{0.f, 0.f, 0.f, 0.f};
+      } else {
+        *reinterpret_cast<u32x4*>(a.out + at) = u32x4{0, 0, 0, 0};
+      }
+    }
     if (tid < 16) a.lse[(int64_t)t * a.H + h0 + tid] = 0.f;
     return;
   }
@@ -675,6 +684,10 @@ __global__ __launch_bounds__(256) void v4_decode_rows_kernel(DecArgs a) {
   for (int j = 0; j < 8; ++j) {
     const int item = tid + 256 * j;
     const f32x4 acc = merged(j) * inv;
+    if (a.out32) {
+      *reinterpret_cast<f32x4*>(a.out32 + th * 512 + 4 * (item >> 4)) = acc;
+      continue;
+    }
     uint32_t pk[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
@@ -697,14 +710,20 @@ template <bool kF16>
 __global__ __launch_bounds__(256) void v4_decode_combine_kernel(const float* __restrict__ part,
                                                                 const float* __restrict__ sinks, int TH, int H,
                                                                 int nsplit, uint16_t* __restrict__ out,
-                                                                float* __restrict__ lse) {
+                                                                float* __restrict__ out32, float* __restrict__ lse) {
   const int hh = blockIdx.x * 4 + (int)(threadIdx.x / 64);  // row * H + head
   if (hh >= TH) return;
   const int c8 = 8 * (threadIdx.x % 64);
   const float* base = part + (int64_t)hh * nsplit * kDecPart;
   uint16_t* op = out + (int64_t)hh * 512 + c8;
+  float* op32 = out32 ? out32 + (int64_t)hh * 512 + c8 : nullptr;
   if (base[513] < 0.f) {
-    *reinterpret_cast<u32x4*>(op) = u32x4{0, 0, 0, 0};
+    if (op32) {
+      *reinterpret_cast<f32x4*>(op32) = f32x4{0.f, 0.f, 0.f, 0.f};
+      *reinterpret_cast<f32x4*>(op32 + 4) = f32x4{0.f, 0.f, 0.f, 0.f};
+    } else {
+      *reinterpret_cast<u32x4*>(op) = u32x4{0, 0, 0, 0};
+    }
     if (c8 == 0) lse[hh] = 0.f;
     return;
   }
@@ -746,6 +765,12 @@ __global__ __launch_bounds__(256) void v4_decode_combine_kernel(const float* __r
   den += es;
   den_r += es;
   const float inv = den_r > 0.f ? 1.f / den_r : 0.f;
+  if (c8 == 0) lse[hh] = den > 0.f ? (mm + fast_log2(den)) * 0.69314718055994531f : -__builtin_huge_valf();
+  if (op32) {
+    *reinterpret_cast<f32x4*>(op32) = f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+    *reinterpret_cast<f32x4*>(op32 + 4) = f32x4{acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv};
+    return;
+  }
   uint32_t pk[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -758,7 +783,6 @@ __global__ __launch_bounds__(256) void v4_decode_combine_kernel(const float* __r
     }
   }
   *reinterpret_cast<u32x4*>(op) = u32x4{pk[0], pk[1], pk[2], pk[3]};
-  if (c8 == 0) lse[hh] = den > 0.f ? (mm + fast_log2(den)) * 0.69314718055994531f : -__builtin_huge_valf();
 }
 
 template <bool kF16, int kMode, int kD = 512>
@@ -794,14 +818,16 @@ static size_t dec_part_bytes(int64_t T, int64_t H, int64_t cap) {
 // holds dec_part_bytes(T, H, cap).
 // The decode kernel (and, past kDecSingle slots, its combine) for kernel mode
 // `mode`; `a` holds the mode's own arguments.
+// out_f32: out is fp32 (else q's dtype).
 static hipError_t dec_run(int is_fp16, int mode, DecArgs& a, const void* q, const void* kv, const void* kv2,
                           int64_t T, int64_t H, int64_t cap, const float* sinks, float sm_scale, void* out, float* lse,
-                          void* part, hipStream_t stream) {
+                          void* part, hipStream_t stream, int out_f32 = 0) {
   a.q = static_cast<const uint16_t*>(q);
   a.kv = static_cast<const uint8_t*>(kv);
   a.kv2 = static_cast<const uint8_t*>(kv2);
   a.sinks = sinks;
-  a.out = static_cast<uint16_t*>(out);
+  a.out = out_f32 ? nullptr : static_cast<uint16_t*>(out);
+  a.out32 = out_f32 ? static_cast<float*>(out) : nullptr;
   a.lse = lse;
   a.T = (int)T;
   a.H = (int)H;
@@ -818,10 +844,10 @@ static hipError_t dec_run(int is_fp16, int mode, DecArgs& a, const void* q, cons
   if (a.nsplit > 1) {
     if (is_fp16)
       hipLaunchKernelGGL(v4_decode_combine_kernel<true>, cgrid, dim3(256), 0, stream, a.part, sinks, TH, (int)H,
-                         a.nsplit, a.out, lse);
+                         a.nsplit, a.out, a.out32, lse);
     else
       hipLaunchKernelGGL(v4_decode_combine_kernel<false>, cgrid, dim3(256), 0, stream, a.part, sinks, TH, (int)H,
-                         a.nsplit, a.out, lse);
+                         a.nsplit, a.out, a.out32, lse);
   }
   return hipGetLastError();
 }
@@ -829,12 +855,13 @@ static hipError_t dec_run(int is_fp16, int mode, DecArgs& a, const void* q, cons
 static hipError_t launch_v4_decode_rows(int is_fp16, const void* q, const void* kv, const void* kv2,
                                         const int32_t* rows, const int32_t* count, int64_t T, int64_t H, int64_t cap,
                                         const float* sinks, float sm_scale, void* out, float* lse, void* part,
-                                        hipStream_t stream, const V4Args* v4 = nullptr) {
+                                        hipStream_t stream, const V4Args* v4 = nullptr, int out_f32 = 0) {
   DecArgs a = {};
   a.v4 = v4 ? *v4 : V4Args{};
   a.rows = rows;
   a.count = count;
-  return dec_run(is_fp16, v4 ? v4->mode : 0, a, q, kv, kv2, T, H, cap, sinks, sm_scale, out, lse, part, stream);
+  return dec_run(is_fp16, v4 ? v4->mode : 0, a, q, kv, kv2, T, H, cap, sinks, sm_scale, out, lse, part, stream,
+                 out_f32);
 }
 
 // Sparse MLA (576-wide rows, V = the first 512) decode rows through the decode
@@ -876,8 +903,8 @@ static size_t v4_lists_bytes(int64_t T, int64_t cap) {
 }
 
 // Row lists, then the split partials of the gather kernel or of the decode kernel.
-size_t v4_workspace_bytes(int64_t T, int64_t H, int64_t cap) {
-  const size_t a = mla_workspace_bytes(T, H, cap), b = dec_part_bytes(T, H, cap);
+size_t v4_workspace_bytes(int64_t T, int64_t H, int64_t cap, bool out_f32) {
+  const size_t a = mla_workspace_bytes(T, H, cap, out_f32), b = dec_part_bytes(T, H, cap);
   return v4_lists_bytes(T, cap) + (a > b ? a : b);
 }
 
@@ -924,10 +951,11 @@ hipError_t launch_sparse_flash_mla(int is_fp16, const void* q, int64_t T, int64_
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   return launch_sparse_mla_rows(is_fp16, q, ori_kv, cmp_kv, a.rows, a.count, T, H, cap, sinks, sm_scale, out, lse,
-                                part, stream);
+                                part, stream, 0);
 }
 
-size_t sparse_attn_sink_workspace_bytes(int64_t T, int64_t H, int64_t K) { return v4_workspace_bytes(T, H, K); }
+// The output is fp32 (as the reference kernel's), so are the split partials.
+size_t sparse_attn_sink_workspace_bytes(int64_t T, int64_t H, int64_t K) { return v4_workspace_bytes(T, H, K, true); }
 
 // Caller validated: D = 512, H % 16 == 0, B * N < 2^30, T = B * M < 2^31 / (K + 1).
 hipError_t launch_sparse_attn_sink(int is_fp16, const void* q, const void* kv, const int32_t* idx, int64_t B,
@@ -945,9 +973,9 @@ hipError_t launch_sparse_attn_sink(int is_fp16, const void* q, const void* kv, c
   void* mla_ws = static_cast<uint8_t*>(workspace) + v4_lists_bytes(T, K);
   if (T <= kDecodeRows && K <= kDecodeMaxSlots)
     return launch_v4_decode_rows(is_fp16, q, kv, nullptr, rows, count, T, H, K, sinks, sm_scale, out, lse, mla_ws,
-                                 stream);
+                                 stream, nullptr, 1);
   return launch_sparse_mla_rows(is_fp16, q, kv, nullptr, rows, count, T, H, K, sinks, sm_scale, out, lse, mla_ws,
-                                stream);
+                                stream, 1);
 }
 
 }  // namespace dsa

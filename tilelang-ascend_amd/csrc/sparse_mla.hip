@@ -97,6 +97,10 @@ struct MlaArgs {
   float* lse;                 // [B, S, H]
   uint16_t* part_o;           // [splits, B*S, H, 512] (splits > 1)
   float* part_lse;            // [splits, B*S, H]
+  // Row lists only: when set, out is written here in fp32 instead (and the
+  // split partials go to part_o32 in fp32), so no 16-bit rounding is applied.
+  float* out32;               // [B, S, H, 512] or null
+  float* part_o32;            // [splits, B*S, H, 512] (splits > 1, out32 set)
   int B, S, H, Skv, topk;
   int block_size, max_blocks;
   int causal;
@@ -507,7 +511,8 @@ __device__ __forceinline__ const uint16_t* mla_row(const uint8_t* kvb, const uin
 
 template <bool kF16, int kD>
 __device__ __attribute__((noinline)) void mla_exact_fallback(const uint16_t* q, const uint8_t* kvb, const uint8_t* kvb2,
-                                                             const float* sinks, uint16_t* obase, float* lbase, int H,
+                                                             const float* sinks, uint16_t* obase, float* obase32,
+                                                             float* lbase, int H,
                                                              float scale_log2, const int32_t* rows, int nslots,
                                                              int token, int head_begin, int nheads, float* sc,
                                                              int threads) {
@@ -561,7 +566,8 @@ __device__ __attribute__((noinline)) void mla_exact_fallback(const uint16_t* q, 
         const uint16_t v = mla_row<kF16, kD>(kvb, kvb2, row)[c];
         acc = fmaf(fast_exp2(sc[j] - m_use), unpack_lo<kF16>(v), acc);
       }
-      obase[((int64_t)token * H + h) * kMlaDV + c] = cvt1<kF16>(acc * inv);
+      if (obase32) obase32[((int64_t)token * H + h) * kMlaDV + c] = acc * inv;
+      else obase[((int64_t)token * H + h) * kMlaDV + c] = cvt1<kF16>(acc * inv);
     }
     if (tid == 0) lbase[(int64_t)token * H + h] = l > 0.f ? (mx + fast_log2(l)) * 0.69314718055994531f : -__builtin_huge_valf();
     __syncthreads();
@@ -896,12 +902,17 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   __syncthreads();
   const bool final_out = (a.splits == 1);
   uint16_t* obase = final_out ? a.out : a.part_o + (int64_t)split * T * a.H * kMlaDV;
+  float* obase32 = nullptr;  // fp32 output (row lists only)
+  if constexpr (Geo::kRowLists) {
+    if (a.out32) obase32 = final_out ? a.out32 : a.part_o32 + (int64_t)split * T * a.H * kMlaDV;
+  }
   float* lbase = final_out ? a.lse : a.part_lse + (int64_t)split * T * a.H;
   // Sinks join the softmax once: here when this workgroup writes the final
   // output, in the combine kernel otherwise.
   const float* sinks = Geo::kRowLists && final_out ? a.sinks : nullptr;
   if (*overflow_flag) {
-    mla_exact_fallback<kF16, kD>(a.q, kvb, kvb2, sinks, obase, lbase, a.H, a.scale_log2, rows, nslots_all, token,
+    mla_exact_fallback<kF16, kD>(a.q, kvb, kvb2, sinks, obase, obase32, lbase, a.H, a.scale_log2, rows, nslots_all,
+                                 token,
                                  blockIdx.y * (kNW * kHeadsPerWave), kNW * kHeadsPerWave,
                                  reinterpret_cast<float*>(lds), kNW * kWave);
     return;
@@ -942,7 +953,14 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
       l_tot = 1.f;
       m_out = 0.f;
     }
-    if (hb_on[hb]) {
+    if (Geo::kRowLists && hb_on[hb] && obase32) {
+      float* orow = obase32 + ((int64_t)token * a.H + h) * kMlaDV + 8 * g;
+#pragma unroll
+      for (int p2 = 0; p2 < kMlaDV / 32; ++p2) {
+        *reinterpret_cast<f32x4*>(orow + 32 * p2) = o[hb][2 * p2] * inv;
+        *reinterpret_cast<f32x4*>(orow + 32 * p2 + 4) = o[hb][2 * p2 + 1] * inv;
+      }
+    } else if (hb_on[hb]) {
       uint16_t* orow = obase + ((int64_t)token * a.H + h) * kMlaDV + 8 * g;
 #pragma unroll
       for (int p2 = 0; p2 < kMlaDV / 32; ++p2) {
@@ -952,36 +970,67 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
                          pack2<kF16>(y[0] * inv, y[1] * inv), pack2<kF16>(y[2] * inv, y[3] * inv)};
         *reinterpret_cast<u32x4*>(orow + 32 * p2) = v;
       }
-      if (g == 0) {
-        lbase[(int64_t)token * a.H + h] =
-            l_tot > 0.f ? (m_out + fast_log2(l_tot)) * 0.69314718055994531f : -__builtin_huge_valf();
-      }
     }
+    if (hb_on[hb] && g == 0)
+      lbase[(int64_t)token * a.H + h] =
+          l_tot > 0.f ? (m_out + fast_log2(l_tot)) * 0.69314718055994531f : -__builtin_huge_valf();
   }
 }
 
 // Merge split partials: lse = log(sum_i exp(lse_i) [+ exp(sink)]),
-// out = sum_i exp(lse_i - lse) * o_i.
-template <bool kF16>
-__global__ __launch_bounds__(256) void sparse_mla_combine_kernel(const uint16_t* __restrict__ part_o,
+// out = sum_i exp(lse_i - lse) * o_i.  kF32: partials and out are fp32 (row
+// lists with an fp32 output), else 16-bit.
+template <bool kF16, bool kF32>
+__global__ __launch_bounds__(256) void sparse_mla_combine_kernel(const void* __restrict__ part_o,
                                                                  const float* __restrict__ part_lse, int splits,
                                                                  int64_t rows, const float* __restrict__ sinks,
                                                                  const int32_t* __restrict__ slot_count, int H,
-                                                                 uint16_t* __restrict__ out, float* __restrict__ lse) {
+                                                                 void* __restrict__ out, float* __restrict__ lse) {
   // One thread per (row = token*H + head, 8 columns).
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t row = gid >> 6;
   const int c = (int)(gid & 63) * 8;
   if (row >= rows) return;
+  // 8 columns of partial i as 8 floats.
+  auto load8 = [&](int64_t i, float (&x)[8]) {
+    if constexpr (kF32) {
+      const float* p = static_cast<const float*>(part_o) + (i * rows + row) * kMlaDV + c;
+      const f32x4 lo = *reinterpret_cast<const f32x4*>(p), hi = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        x[j] = lo[j];
+        x[4 + j] = hi[j];
+      }
+    } else {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(part_o) + (i * rows + row) * kMlaDV + c);
+      const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        x[2 * j] = unpack_lo<kF16>(vv[j]);
+        x[2 * j + 1] = unpack_hi<kF16>(vv[j]);
+      }
+    }
+  };
+  auto store8 = [&](const float (&x)[8]) {
+    if constexpr (kF32) {
+      float* p = static_cast<float*>(out) + row * kMlaDV + c;
+      *reinterpret_cast<f32x4*>(p) = f32x4{x[0], x[1], x[2], x[3]};
+      *reinterpret_cast<f32x4*>(p + 4) = f32x4{x[4], x[5], x[6], x[7]};
+    } else {
+      *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(out) + row * kMlaDV + c) =
+          u32x4{pack2<kF16>(x[0], x[1]), pack2<kF16>(x[2], x[3]), pack2<kF16>(x[4], x[5]), pack2<kF16>(x[6], x[7])};
+    }
+  };
   if (slot_count && slot_count[row / H] < 0) {  // padded query row of a row-list call
-    *reinterpret_cast<u32x4*>(out + row * kMlaDV + c) = u32x4{0, 0, 0, 0};
+    const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    store8(z);
     if (c == 0) lse[row] = 0.f;
     return;
   }
   // Splits are visited kU at a time, every load of a group issued before any is
   // used (a split-serial loop is a chain of load latencies); the sums keep the
   // split order.
-  constexpr int kU = 8;
+  constexpr int kU = kF32 ? 4 : 8;
   const float sink = sinks ? sinks[row % H] : -__builtin_huge_valf();
   float mx = sink;
   for (int i0 = 0; i0 < splits; i0 += kU) {
@@ -997,34 +1046,27 @@ __global__ __launch_bounds__(256) void sparse_mla_combine_kernel(const uint16_t*
   if (mx != -__builtin_huge_valf()) {
     for (int i0 = 0; i0 < splits; i0 += kU) {
       float li[kU];
-      u32x4 v[kU];
+      float v[kU][8];
 #pragma unroll
       for (int u = 0; u < kU; ++u) {
         const int i = min(i0 + u, splits - 1);  // clamped: a real partial, unused past splits
         li[u] = i0 + u < splits ? part_lse[(int64_t)i * rows + row] : -__builtin_huge_valf();
-        v[u] = *reinterpret_cast<const u32x4*>(part_o + ((int64_t)i * rows + row) * kMlaDV + c);
+        load8(i, v[u]);
       }
 #pragma unroll
       for (int u = 0; u < kU; ++u) {
         if (li[u] == -__builtin_huge_valf()) continue;
         const float w = __expf(li[u] - mx);
         wsum += w;
-        const uint32_t vv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          acc[2 * j] += w * unpack_lo<kF16>(vv[j]);
-          acc[2 * j + 1] += w * unpack_hi<kF16>(vv[j]);
-        }
+        for (int j = 0; j < 8; ++j) acc[j] += w * v[u][j];
       }
     }
   }
   const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
-  u32x4 o;
-  o.x = pack2<kF16>(acc[0] * inv, acc[1] * inv);
-  o.y = pack2<kF16>(acc[2] * inv, acc[3] * inv);
-  o.z = pack2<kF16>(acc[4] * inv, acc[5] * inv);
-  o.w = pack2<kF16>(acc[6] * inv, acc[7] * inv);
-  *reinterpret_cast<u32x4*>(out + row * kMlaDV + c) = o;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] *= inv;
+  store8(acc);
   if (c == 0) lse[row] = wsum > 0.f ? mx + __logf(wsum) : -__builtin_huge_valf();
 }
 
@@ -1047,11 +1089,12 @@ static int64_t mla_keys_per_split(int64_t topk, int splits) {
   return ((per + kMlaTile - 1) / kMlaTile) * kMlaTile;
 }
 
-size_t mla_workspace_bytes(int64_t tokens, int64_t H, int64_t topk) {
+// Split partials: O (16-bit, or fp32 for an fp32 output) and the LSE per (split, token, head).
+size_t mla_workspace_bytes(int64_t tokens, int64_t H, int64_t topk, bool f32) {
   const int64_t hg = (H + 127) / 128;
   const int splits = mla_choose_splits(tokens, hg, topk);
   if (splits == 1) return 0;
-  return (size_t)splits * tokens * H * (kMlaDV * 2 + 4) + 256;
+  return (size_t)splits * tokens * H * (kMlaDV * (f32 ? 4 : 2) + 4) + 256;
 }
 
 bool mla_decode_applies(int64_t T, int64_t H, int64_t topk);
@@ -1065,7 +1108,7 @@ hipError_t launch_mla_decode_rows(int is_fp16, const void* q, const void* kv, co
 // Workspace of launch_sparse_mla: decode rows take the decode kernel's partials.
 size_t sparse_mla_workspace_bytes(int64_t tokens, int64_t H, int64_t topk) {
   return mla_decode_applies(tokens, H, topk) ? mla_decode_part_bytes(tokens, H, topk)
-                                             : mla_workspace_bytes(tokens, H, topk);
+                                             : mla_workspace_bytes(tokens, H, topk, false);
 }
 
 // Split partials of the allocation-free entry (dsa_sparse_mla_fwd_noalloc): one
@@ -1125,20 +1168,29 @@ static hipError_t launch_mla_dtype(const MlaArgs& a, int head_groups, int hpg, h
   if (e != hipSuccess || a.splits == 1) return e;
   const int64_t rows = (int64_t)a.B * a.S * a.H;
   const int64_t threads = rows * (kMlaDV / 8);
-  hipLaunchKernelGGL((sparse_mla_combine_kernel<kF16>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
-                     a.part_o, a.part_lse, a.splits, rows, a.sinks, a.slot_count, a.H, a.out, a.lse);
+  const dim3 grid((unsigned)((threads + 255) / 256));
+  if (a.out32)
+    hipLaunchKernelGGL((sparse_mla_combine_kernel<kF16, true>), grid, dim3(256), 0, stream, a.part_o32, a.part_lse,
+                       a.splits, rows, a.sinks, a.slot_count, a.H, a.out32, a.lse);
+  else
+    hipLaunchKernelGGL((sparse_mla_combine_kernel<kF16, false>), grid, dim3(256), 0, stream, a.part_o, a.part_lse,
+                       a.splits, rows, a.sinks, a.slot_count, a.H, a.out, a.lse);
   return hipGetLastError();
 }
 
+// a.out32 must be set first: the partials' width follows the output's.
 static void mla_set_splits(MlaArgs& a, int64_t T, int64_t H, int64_t topk, void* workspace) {
   const int head_groups = (int)((H + 127) / 128);
   a.splits = mla_choose_splits(T, head_groups, topk);
   a.keys_per_split = (int)mla_keys_per_split(topk, a.splits);
   a.part_o = nullptr;
+  a.part_o32 = nullptr;
   a.part_lse = nullptr;
   if (a.splits > 1) {
+    const size_t ebytes = a.out32 ? 4 : 2;
     a.part_o = static_cast<uint16_t*>(workspace);
-    a.part_lse = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + (size_t)a.splits * T * H * kMlaDV * 2);
+    a.part_o32 = a.out32 ? static_cast<float*>(workspace) : nullptr;
+    a.part_lse = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + (size_t)a.splits * T * H * kMlaDV * ebytes);
   }
 }
 
@@ -1165,6 +1217,7 @@ hipError_t launch_sparse_mla(int is_fp16, const void* q, const void* kv, const i
   a.q_len = q_len;
   a.kv_len = kv_len;
   a.out = static_cast<uint16_t*>(out);
+  a.out32 = nullptr;
   a.lse = lse;
   a.B = (int)B;
   a.S = (int)S;
@@ -1186,10 +1239,11 @@ hipError_t launch_sparse_mla(int is_fp16, const void* q, const void* kv, const i
 // K = V): rows[t][0 .. count[t]) index kv, or kv2 when tagged kSrc2Bit, -1 =
 // empty; sinks [H] (natural log units) or null.  The V4 sparse_flash_mla
 // kernel below builds the lists.  Caller validated: H % 16 == 0, H <= 1024,
-// cap <= 2^31 / T, workspace >= mla_workspace_bytes(T, H, cap).
+// cap <= 2^31 / T, workspace >= mla_workspace_bytes(T, H, cap, out_f32).  out_f32: out is fp32.
 hipError_t launch_sparse_mla_rows(int is_fp16, const void* q, const void* kv, const void* kv2, const int32_t* rows,
                                   const int32_t* count, int64_t T, int64_t H, int64_t cap, const float* sinks,
-                                  float sm_scale, void* out, float* lse, void* workspace, hipStream_t stream) {
+                                  float sm_scale, void* out, float* lse, void* workspace, hipStream_t stream,
+                                  int out_f32) {
   if (T == 0 || H == 0) return hipSuccess;
   MlaArgs a;
   a.q = static_cast<const uint16_t*>(q);
@@ -1201,7 +1255,8 @@ hipError_t launch_sparse_mla_rows(int is_fp16, const void* q, const void* kv, co
   a.block_table = nullptr;
   a.q_len = nullptr;
   a.kv_len = nullptr;
-  a.out = static_cast<uint16_t*>(out);
+  a.out = out_f32 ? nullptr : static_cast<uint16_t*>(out);
+  a.out32 = out_f32 ? static_cast<float*>(out) : nullptr;
   a.lse = lse;
   a.B = 1;
   a.S = (int)T;

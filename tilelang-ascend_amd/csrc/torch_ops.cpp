@@ -353,8 +353,8 @@ std::tuple<at::Tensor, at::Tensor> act_quant_meta(const at::Tensor& x, bool, c10
 }
 
 // V4 gathered-index attention with sinks (examples/deepseek_v4/sparse_attention.py:171-198):
-// q [b, m, h, 512], kv [b, n, 512], attn_sink [h] fp32, topk_idxs [b, m, topk] -> (out fp32, lse fp32).
-// The kernel writes out in q's dtype; it is returned widened to fp32.
+// q [b, m, h, 512], kv [b, n, 512], attn_sink [h] fp32, topk_idxs [b, m, topk] -> (out fp32, lse fp32);
+// the kernel writes its fp32 accumulator, as the reference's does.
 std::tuple<at::Tensor, at::Tensor> sparse_attn(const at::Tensor& q, const at::Tensor& kv,
                                                const c10::optional<at::Tensor>& attn_sink, const at::Tensor& topk_idxs,
                                                double softmax_scale) {
@@ -372,7 +372,7 @@ std::tuple<at::Tensor, at::Tensor> sparse_attn(const at::Tensor& q, const at::Te
               ", ", M, ", topk] (got ", topk_idxs.sizes(), ")");
   auto idx = aux_i32(topk_idxs, q, -1, "topk_idxs");
   auto sk = aux_f32(attn_sink, q, H, "attn_sink");
-  auto out = at::empty({B, M, H, D}, q.options());
+  auto out = at::empty({B, M, H, D}, q.options().dtype(at::kFloat));
   auto lse = at::empty({B, M, H}, q.options().dtype(at::kFloat));
   if (B * M > 0) {
     const size_t ws_bytes = dsa_sparse_attn_sink_workspace_size(B, M, H, K);
@@ -382,7 +382,7 @@ std::tuple<at::Tensor, at::Tensor> sparse_attn(const at::Tensor& q, const at::Te
                                   static_cast<float*>(ptr(lse)), ptr(ws), ws_bytes, stream_of(q)),
              "sparse_attn");
   }
-  return {out.to(at::kFloat), lse};
+  return {out, lse};
 }
 
 std::tuple<at::Tensor, at::Tensor> sparse_attn_meta(const at::Tensor& q, const at::Tensor&,

@@ -178,9 +178,8 @@ def sparse_attn(query_states: torch.Tensor, kv_states: torch.Tensor, attn_sink: 
                 topk_idxs: torch.Tensor, softmax_scale: float) -> torch.Tensor:
     """V4 gathered-index attention with sinks (examples/deepseek_v4/sparse_attention.py:171-198):
     q [b, m, h, 512], kv [b, n, 512], attn_sink [h] fp32, topk_idxs [b, m, topk] int32 (-1 =
-    empty slot; duplicates count twice) -> fp32 [b, m, h, 512].  The reference kernel writes its
-    fp32 accumulator; this kernel accumulates in fp32 and rounds the normalised output to q's dtype
-    (bf16 / fp16: a relative rounding of at most 2^-9 / 2^-12), then widens it to fp32."""
+    empty slot; duplicates count twice) -> fp32 [b, m, h, 512].  As the reference kernel
+    (sparse_attention.py:56), the fp32 accumulator is written as it is: no 16-bit rounding."""
     if query_states.dtype not in _KINDS or kv_states.dtype != query_states.dtype:
         raise ValueError("query_states / kv_states must share a bfloat16 or float16 dtype")
     dev = _lib.require_device(query_states)
@@ -202,7 +201,7 @@ def sparse_attn(query_states: torch.Tensor, kv_states: torch.Tensor, attn_sink: 
     sk = None if attn_sink is None else attn_sink.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
     if sk is not None and sk.numel() != h:
         raise ValueError(f"attn_sink must hold one value per head ({h}), got {sk.numel()}")
-    out = torch.empty((b, m, h, D), dtype=query_states.dtype, device=dev)
+    out = torch.empty((b, m, h, D), dtype=torch.float32, device=dev)
     lse = torch.empty((b, m, h), dtype=torch.float32, device=dev)
     if b * m > 0:
         lib = _lib.load_library()
@@ -212,7 +211,7 @@ def sparse_attn(query_states: torch.Tensor, kv_states: torch.Tensor, attn_sink: 
                                       _lib.ptr(idx), b, m, h, n, D, topk, _lib.ptr(sk), float(softmax_scale),
                                       _lib.ptr(out), _lib.ptr(lse), _lib.ptr(ws), ws_bytes, _lib.stream_handle(dev))
         _lib.check(rc, "dsa_sparse_attn_sink")
-    return out.float()
+    return out
 
 
 def sparse_attn_kernel(h: int, d: int, scale: Optional[float] = None):
