@@ -375,6 +375,59 @@ def test_v4_golden_mode_matches_exact_without_rounding():
     assert 0 < d < 2e-2
 
 
+def _scatter_to_pool(contig, bs, g):
+    """Lay per-batch contiguous caches [B, L, D] out as a pool of blocks [B * L / bs, bs, 1, D] under
+    a random permutation: block e of batch b goes to pool block table[b, e]."""
+    B, L, D = contig.shape
+    nb = L // bs
+    perm = torch.randperm(B * nb, generator=g)
+    table = perm.view(B, nb).to(torch.int32)
+    pool = torch.empty(B * nb, bs, 1, D, dtype=contig.dtype)
+    for b in range(B):
+        for e in range(nb):
+            pool[int(table[b, e])] = contig[b, e * bs:(e + 1) * bs].view(bs, 1, D)
+    return pool, table
+
+
+def test_unpack_paged_permuted_table_equals_contiguous_cache():
+    g = torch.Generator().manual_seed(12)
+    B, L, D, bs = 3, 96, 8, 16
+    contig = torch.randn(B, L, D, generator=g)
+    pool, table = _scatter_to_pool(contig, bs, g)
+    assert not torch.equal(table.view(-1), torch.arange(B * L // bs, dtype=torch.int32))
+    for b in range(B):
+        for length in (L, 50, 16, 1):  # whole blocks and a partial last block
+            assert torch.equal(ref.unpack_paged(pool, table, length, b), contig[b, :length])
+
+
+def test_v4_paged_permuted_table_equals_contiguous_layout():
+    # The whole V4 oracle on a permuted pool gives what it gives on the identity layout of the
+    # same per-batch caches (original and compressed rows both paged).
+    g = torch.Generator().manual_seed(13)
+    B, L, D, bs, H, ratio = 2, 128, 16, 16, 4, 4
+    ori = torch.randn(B, L, D, generator=g)
+    cmp = torch.randn(B, L // ratio, D, generator=g)
+    q = torch.randn(6, H, D, generator=g)
+    sinks = torch.randn(H, generator=g)
+    cu, kv_len = [0, 2, 6], [100, 128]
+    pool_o, tab_o = _scatter_to_pool(ori, bs, g)
+    pool_c, tab_c = _scatter_to_pool(cmp, bs // ratio, g)
+    ident_o = torch.arange(B * L // bs, dtype=torch.int32).view(B, -1)
+    ident_c = torch.arange(B * L // bs, dtype=torch.int32).view(B, -1)
+    lin_o = ori.reshape(B * L // bs, bs, 1, D)
+    lin_c = cmp.reshape(B * L // bs, bs // ratio, 1, D)
+    a = ref.sparse_flash_mla(q, cu, kv_len, pool_o, tab_o, sinks, 0.3, cmp_kv=pool_c, cmp_block_table=tab_c,
+                             cmp_ratio=ratio, ori_win_left=31)
+    b = ref.sparse_flash_mla(q, cu, kv_len, lin_o, ident_o, sinks, 0.3, cmp_kv=lin_c, cmp_block_table=ident_c,
+                             cmp_ratio=ratio, ori_win_left=31)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    # And a wrong table (the permutation's inverse) changes the result.
+    inv = torch.argsort(tab_o.view(-1).long()).to(torch.int32).view(B, -1)
+    c = ref.sparse_flash_mla(q, cu, kv_len, pool_o, inv, sinks, 0.3, cmp_kv=pool_c, cmp_block_table=tab_c,
+                             cmp_ratio=ratio, ori_win_left=31)
+    assert not torch.equal(a[0], c[0])
+
+
 # ----------------------------------------------------- V4 sparse_attn with sinks
 def test_sparse_attn_sink_one_key_closed_form():
     # Every slot on one key j: p is uniform over the K slots, so
