@@ -245,7 +245,9 @@ int dsa_sparse_mla_fwd(int kind, const void* q, const void* kv, const int32_t* i
  * process ends.  A shape whose dsa_sparse_mla_workspace_size() exceeds it is
  * rejected (hipErrorInvalidValue).  The call allocates nothing.  Calls that
  * overlap on one GPU (concurrent streams, or host threads) share that array
- * and race: serialise them.
+ * and race: serialise them.  The first call on a GPU looks the array's address
+ * up (once); it may run inside HIP-graph capture once any entry of this
+ * library has run eagerly on that GPU (the usual graph warm-up).
  */
 size_t dsa_sparse_mla_noalloc_max_workspace(void);
 

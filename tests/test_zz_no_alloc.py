@@ -1,7 +1,12 @@
 """dsa_sparse_mla_fwd_noalloc (the allocation-free sparse MLA entry, split partials in a
 library-owned per-GPU scratch array) against dsa_sparse_mla_fwd with a caller workspace,
 through the C ABI: bit-equal outputs on two calls in a row (the second smaller), a call with
-no split (no scratch used), and the rejection of a shape whose partials exceed the scratch."""
+no split (no scratch used), the rejection of a shape whose partials exceed the scratch, and a
+process's first noalloc call (the scratch lookup) made inside HIP-graph capture."""
+import subprocess
+import sys
+from pathlib import Path
+
 import pytest
 import torch
 
@@ -68,3 +73,12 @@ def test_noalloc_rejects_partials_beyond_the_scratch(dsa, dev):
     rc = lib.dsa_sparse_mla_fwd_noalloc(1, x.data_ptr(), x.data_ptr(), x.data_ptr(), None, None, None, 1, 1000, 128,
                                         576, 512, 4096, 0, 0, 4096, 0.04, 1, x.data_ptr(), x.data_ptr(), None)
     assert rc == 1 and b"scratch" in lib.dsa_last_error_message()
+
+
+def test_noalloc_first_call_inside_graph_capture():
+    """A fresh process warms up through the workspace entry, then makes its first noalloc call
+    (the per-device scratch lookup included) inside torch.cuda.graph capture; three replays equal
+    the workspace entry bit for bit (tests/noalloc_capture_child.py)."""
+    child = Path(__file__).resolve().parent / "noalloc_capture_child.py"
+    res = subprocess.run([sys.executable, str(child)], capture_output=True, text=True, timeout=240)
+    assert res.returncode == 0 and res.stdout.strip().endswith("ok"), res.stdout[-2000:] + res.stderr[-2000:]
