@@ -374,6 +374,23 @@ __device__ __forceinline__ void pv_only(f32x4 (&o)[2][kMlaDV / 16], const u32x4 
 // spread over the half-steps.
 constexpr int kQkAhead = 6;
 
+// One Q K^T MFMA with its accumulator in VGPRs, as inline asm.  The compiler
+// writes every MFMA result of this kernel to AGPRs, where the O accumulators
+// already take all 256: it then parked O columns in VGPRs around each tile's
+// Q K^T (about 100 v_accvgpr moves a tile).  The accumulator chains are eight
+// MFMAs apart (no back-to-back dependence); qk_phase waits out the last
+// results before any VALU instruction reads them.  kZero: start the chain (C = 0).
+template <bool kF16, bool kZero>
+__device__ __forceinline__ void mfma_qk(f32x4& c, const u32x4& a, const u32x4& b) {
+  if constexpr (kZero) {
+    if constexpr (kF16) __asm__ __volatile__("v_mfma_f32_16x16x32_f16 %0, %1, %2, 0" : "=v"(c) : "v"(a), "v"(b));
+    else __asm__ __volatile__("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=v"(c) : "v"(a), "v"(b));
+  } else {
+    if constexpr (kF16) __asm__ __volatile__("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+    else __asm__ __volatile__("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+  }
+}
+
 template <bool kF16, int kNW, int kD, bool kDma, int J>
 __device__ __forceinline__ void qk_half(f32x4 (&c)[2][2][2], const u32x4 (&qb)[2][kD / 32],
                                         const uint32_t (&qa)[2], u32x4 (&k)[kQkAhead + 1], TileDma<kNW, kD>& dma) {
@@ -387,8 +404,9 @@ __device__ __forceinline__ void qk_half(f32x4 (&c)[2][2][2], const u32x4 (&qb)[2
   constexpr int kSlot = J % (kQkAhead + 1);
   lgkm_wait_k<kWait>(k[kSlot]);
   constexpr int kSet = (J / 2) % 2, kKb = J % 2, kSt = J / 2;
-  c[kSet][0][kKb] = mfma16<kF16>(k[kSlot], qb[0][kSt], c[kSet][0][kKb]);
-  c[kSet][1][kKb] = mfma16<kF16>(k[kSlot], qb[1][kSt], c[kSet][1][kKb]);
+  // Half-steps 0..3 start the four chains of each head block.
+  mfma_qk<kF16, (J < 4)>(c[kSet][0][kKb], k[kSlot], qb[0][kSt]);
+  mfma_qk<kF16, (J < 4)>(c[kSet][1][kKb], k[kSlot], qb[1][kSt]);
   if constexpr (J + 1 < kQkHalf) qk_half<kF16, kNW, kD, kDma, J + 1>(c, qb, qa, k, dma);
 }
 
@@ -404,13 +422,17 @@ template <bool kF16, int kNW, int kD, bool kDma>
 __device__ __forceinline__ void qk_phase(f32x4 (&s)[2][2], const u32x4 (&qb)[2][kD / 32],
                                          const uint32_t (&qa)[2], TileDma<kNW, kD>& dma) {
   f32x4 c[2][2][2];
-#pragma unroll
-  for (int st = 0; st < 2; ++st)
-#pragma unroll
-    for (int hb = 0; hb < 2; ++hb) c[st][hb][0] = c[st][hb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
   u32x4 k[kQkAhead + 1];
   qk_prologue<0>(k, qa);
   qk_half<kF16, kNW, kD, kDma, 0>(c, qb, qa, k, dma);
+  static_assert(kQkAhead + 1 == 7, "the wait below names every K operand register");
+  // The asm MFMAs are opaque to the compiler's hazard checks: 24 wait states
+  // (a 16-pass MFMA needs 19) before a VALU instruction reads a result, and
+  // before the K operand registers may be reused.
+  __asm__ __volatile__("s_nop 7\n\ts_nop 7\n\ts_nop 7"
+                       : "+v"(c[0][0][0]), "+v"(c[0][0][1]), "+v"(c[0][1][0]), "+v"(c[0][1][1]), "+v"(c[1][0][0]),
+                         "+v"(c[1][0][1]), "+v"(c[1][1][0]), "+v"(c[1][1][1]), "+v"(k[0]), "+v"(k[1]), "+v"(k[2]),
+                         "+v"(k[3]), "+v"(k[4]), "+v"(k[5]), "+v"(k[6]));
 #pragma unroll
   for (int hb = 0; hb < 2; ++hb)
 #pragma unroll
