@@ -86,22 +86,29 @@ def test_python_layer_validation_messages(dsa):
 def test_fused_indexer_host_logic(dsa):
     """When the fused indexer applies, its workspace, and its argument checks (host only)."""
     lib = dsa.load_library()
-    # C2 and C5 rows apply; short rows, k > 4096 and S2 < 8k do not.
+    # C2 and C5 rows apply, up to the reference's largest sparse_count (8192, a multiple of
+    # 1024: lightning_indexer.py:1238-1239); short rows and S2 < 8k do not.
     assert lib.dsa_lightning_indexer_fused_applies(1, 4096, 32768, 2048) == 1
     assert lib.dsa_lightning_indexer_fused_applies(1, 4096, 131072, 2048) == 1
     assert lib.dsa_lightning_indexer_fused_applies(32, 1, 131072, 2048) == 1
+    for k in (6144, 8192):
+        assert lib.dsa_lightning_indexer_fused_applies(1, 4096, 131072, k) == 1
+    assert lib.dsa_lightning_indexer_fused_applies(1, 4096, 32768, 8192) == 0
     assert lib.dsa_lightning_indexer_fused_applies(1, 4096, 8192, 2048) == 0
-    assert lib.dsa_lightning_indexer_fused_applies(1, 4096, 131072, 8192) == 0
     assert lib.dsa_lightning_indexer_fused_applies(1, 64, 20000, 4096) == 0
-    # The fused workspace holds the dense logits too; where the fused path does not apply the
-    # entry runs the dense path and asks for exactly its workspace.
+    # The fused workspace holds no dense logits: flagged rows are recomputed in rounds in a
+    # bounded buffer.  At C5 (4096 x 131072, k = 2048) it is well under half the dense path's,
+    # whose logits alone take 2 GiB; at k = 8192 it stays under the dense path's too.
     dense = lib.dsa_lightning_indexer_workspace_size(1, 4096, 131072, 2048)
     fused = lib.dsa_lightning_indexer_fused_workspace_size(1, 4096, 131072, 2048)
-    assert fused >= 4096 * 131072 * 4 and fused > 0 and dense > 0
+    assert dense >= 4096 * 131072 * 4 and 0 < fused < dense // 2
+    assert (lib.dsa_lightning_indexer_fused_workspace_size(1, 4096, 131072, 8192)
+            < lib.dsa_lightning_indexer_workspace_size(1, 4096, 131072, 8192))
+    # Where the fused path does not apply the entry runs the dense path and asks for exactly
+    # its workspace.
     assert (lib.dsa_lightning_indexer_fused_workspace_size(1, 16, 4096, 2048)
             == lib.dsa_lightning_indexer_workspace_size(1, 16, 4096, 2048))
-    assert (lib.dsa_lightning_indexer_tnd_fused_workspace_size(2, 100, 80, 40000, 2048)
-            >= lib.dsa_lightning_indexer_tnd_workspace_size(100, 40000, 2048))
+    assert lib.dsa_lightning_indexer_tnd_fused_workspace_size(2, 100, 80, 40000, 2048) > 0
     # Argument checks, before any launch.
     assert lib.dsa_lightning_indexer_fused(0, 8, 8, None, 8, 1, 16, 32768, 64, 128, None, None, None, 0, 0, 3,
                                            0, 8, None, 8, 1 << 40, None) == 1

@@ -138,8 +138,8 @@ def test_fused_threshold_too_high_falls_back(dsa, dev):
 
 
 def test_fused_chunk_overflow_falls_back(dsa, dev):
-    """k = 256: each key chunk keeps at most 1024 keys; the first chunk's unsampled keys scaled
-    up 50x overflow it."""
+    """k = 256: each key chunk keeps at most 2 k + 1024 = 1536 keys; the first chunk's unsampled
+    keys scaled up 50x (3840 of them) overflow it."""
     B, S1, S2, H, D, K = 1, 64, 32768, 64, 128, 256
     print("fused indexer forced fallback (overflow)", flush=True)
     q, k, w, ks = _inputs(B, S1, S2, H, D, torch.float8_e4m3fn, 35)
@@ -149,6 +149,48 @@ def test_fused_chunk_overflow_falls_back(dsa, dev):
     assert torch.equal(fi, di) and torch.equal(fv, dv)
     ci, cv, nfb = _fused_c(dsa, dev, q, k, w, ks, K)
     assert nfb > 0 and torch.equal(ci, di) and torch.equal(cv, dv)
+
+
+def test_fused_fallback_in_several_rounds(dsa, dev):
+    """Rows sent back to the dense logits (sampled keys scaled up 50x), more of them than the
+    bounded fallback buffer holds: 600 rows of 65536 keys go back in three rounds of 256."""
+    B, S1, S2, H, D, K = 1, 600, 65536, 64, 128, 512
+    print("fused indexer fallback rounds", flush=True)
+    assert _applies(dsa, B, S1, S2, K)
+    q, k, w, ks = _inputs(B, S1, S2, H, D, torch.float8_e4m3fn, 38)
+    pos = torch.arange(S2)
+    ks = torch.where((pos % 1024) < 64, ks * 50, ks)  # covers every sampled tile (64 of each 2048)
+    ci, cv, nfb = _fused_c(dsa, dev, q, k, w, ks, K)
+    (fi, fv), (di, dv) = _both(dsa, dev, q, k.unsqueeze(2), w, ks, K, return_value=True)
+    assert nfb >= S1 * 9 // 10  # rows in every round
+    assert torch.equal(fi, di) and torch.equal(fv, dv)
+    assert torch.equal(ci, di) and torch.equal(cv, dv)
+
+
+@pytest.mark.parametrize("K", [8192, 6144])
+def test_fused_large_k_radix_path(dsa, dev, K):
+    """sparse_count 6144 and 8192 (the reference's largest): the candidates of every row are
+    packed and ranked by the exact radix kernel; equal to the dense path bit for bit."""
+    B, S1, S2, H, D = 1, 192, 65536, 64, 128
+    print(f"fused indexer k={K}", flush=True)
+    assert _applies(dsa, B, S1, S2, K)
+    q, k, w, ks = _inputs(B, S1, S2, H, D, torch.float8_e4m3fn, 39)
+    ci, cv, nfb = _fused_c(dsa, dev, q, k, w, ks, K)
+    di, dv = dsa.lightning_indexer(q.to(dev), k.unsqueeze(2).to(dev), w.to(dev), key_scale=ks.to(dev),
+                                   sparse_count=K, return_value=True, fuse_topk=False)
+    torch.cuda.synchronize()
+    assert nfb == 0
+    assert torch.equal(ci, di) and torch.equal(cv, dv)
+    # And with every row forced back to the dense logits.
+    pos = torch.arange(S2)
+    ks2 = torch.where((pos % 1024) < 64, ks * 50, ks)
+    ci2, cv2, nfb2 = _fused_c(dsa, dev, q, k, w, ks2, K)
+    di2, dv2 = dsa.lightning_indexer(q.to(dev), k.unsqueeze(2).to(dev), w.to(dev), key_scale=ks2.to(dev),
+                                     sparse_count=K, return_value=True, fuse_topk=False)
+    torch.cuda.synchronize()
+    # Most rows go back (a row whose scaled samples are mostly negative gets a low threshold
+    # and keeps its top k in the stream).
+    assert nfb2 >= S1 * 9 // 10 and torch.equal(ci2, di2) and torch.equal(cv2, dv2)
 
 
 def test_fused_heavy_ties(dsa, dev):

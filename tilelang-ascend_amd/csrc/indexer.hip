@@ -250,6 +250,9 @@ struct IdxArgs {
   int cand_cap;
   const int32_t* flag_idx;  // dense pass: only workgroups with a row whose flag_idx[row * flag_ld] is kFallbackFlag
   int64_t flag_ld;
+  // With flag_idx: only rows row_lo .. row_hi - 1 count, and only they are stored, at
+  // logits + (row - row_lo) * ld (the fused path's bounded fallback buffer, one round).
+  int64_t row_lo, row_hi;
 };
 
 enum IdxMode : int { kModeDense = 0, kModeSample = 1, kModeFilter = 2 };
@@ -339,15 +342,19 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
                         : (a.ak_len ? min(max(a.ak_len[b], 0), a.S2) : a.S2);
   const int t_rows = a.cu_q ? aq : a.S1;  // rows of this batch that exist in the output
   constexpr int nhb = kNhb;
-  if (kMode == kModeDense && a.flag_idx) {  // block-uniform: every thread reads the same flags
+  // Rows this call stores: every row, or (fallback rounds) row_lo .. row_hi - 1 only.
+  const bool ranged = kMode == kModeDense && a.flag_idx;
+  auto stored = [&](int t) { return !ranged || (q_base + t >= a.row_lo && q_base + t < a.row_hi); };
+  if (ranged) {  // block-uniform: every thread reads the same flags
     bool any = false;
 #pragma unroll
     for (int j = 0; j < kTok; ++j) {
       const int t = t_base + j;
-      if (t < t_rows) any |= a.flag_idx[(q_base + t) * a.flag_ld] == kFallbackFlag;
+      if (t < t_rows && stored(t)) any |= a.flag_idx[(q_base + t) * a.flag_ld] == kFallbackFlag;
     }
     if (!any) return;
   }
+  float* const logits0 = ranged ? a.logits - a.row_lo * a.ld : a.logits;  // row r at logits0 + r * ld
   const int tstride = kMode == kModeSample ? a.tile_stride : kIdxKeyTile;
 
   // Valid key count per token of this wave (0 for padded rows).
@@ -609,7 +616,8 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
       const int t = t_base + tw + j;
       const float v = (s < nvalid[j]) ? res[j] * (sc * post[j]) : -__builtin_huge_valf();
       if constexpr (kMode == kModeDense) {
-        if (storer && t < t_rows && s < key1) __builtin_nontemporal_store(v, &a.logits[(q_base + t) * a.ld + s]);
+        if (storer && t < t_rows && s < key1 && stored(t))
+          __builtin_nontemporal_store(v, &logits0[(q_base + t) * a.ld + s]);
       } else if constexpr (kMode == kModeSample) {
         if (t < t_rows && s < key1)
           a.sample[(q_base + t) * a.sample_ld + (int64_t)(key0 / tstride + tile) * kIdxKeyTile + lane] = v;
@@ -641,8 +649,8 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
 #pragma unroll
     for (int j = 0; j < kTokPW; ++j) {
       const int t = t_base + tw + j;
-      if (t < t_rows) {
-        float* row = a.logits + (q_base + t) * a.ld;
+      if (t < t_rows && stored(t)) {
+        float* row = logits0 + (q_base + t) * a.ld;
         for (int s = masked0 + (kSplit ? tid : lane); s < key1; s += kSplit ? kIdxThreads : kWave)
           __builtin_nontemporal_store(-__builtin_huge_valf(), &row[s]);
       }
@@ -808,19 +816,25 @@ hipError_t launch_indexer_logits(int kind, const void* q, const void* k, const f
 //      mu = k * sampled / valid the expected number of sampled keys in the
 //      row's top k (thr = -inf when the row has at most k valid keys);
 //   3. filter pass: the indexer again, keeping (logit, key) for logit >= thr,
-//      per (row, key chunk) in key order;
+//      per (row, key chunk) in key order (at most four chunks a row);
 //   4. per row, the kept keys of all chunks read in key order as one packed
-//      row, in place (no copy); the row is flagged when a chunk overflowed or
-//      when thr is finite and fewer than k keys reached it -- otherwise every
-//      key outside the kept set is below thr, which is at most the k-th largest
-//      logit, so the top k (ties to the lower index included) lie in the kept set;
-//   5. the register top-k over those rows (positions map back to keys), and the
-//      exact radix top-k over packed copies of the rows it could not bound (ties);
-//   6. rows flagged in step 4 only: their dense logits and the exact radix top-k.
-// Steps 5-6 give the same output as the dense path bit for bit; step 6 costs an
-// early exit per workgroup when nothing is flagged.
+//      row; the row is flagged when a chunk overflowed, when more keys were kept
+//      than a packed row holds, or when thr is finite and fewer than k keys
+//      reached it -- otherwise every key outside the kept set is below thr,
+//      which is at most the k-th largest logit, so the top k (ties to the
+//      lower index included) lie in the kept set;
+//   5. k <= 4096: the register top-k over those rows where the filter left
+//      them (positions map back to keys), and the exact radix top-k over packed
+//      copies of the rows it could not bound (ties); k > 4096: every row packed,
+//      then the exact radix top-k over the packed rows;
+//   6. rows flagged in step 4 only, in rounds of consecutive rows: their dense
+//      logits into a bounded buffer (the candidate slots, dead by then) and the
+//      exact radix top-k -- an early exit per workgroup when nothing is flagged.
+// Steps 5-6 give the same output as the dense path bit for bit.
 hipError_t launch_topk_candidates(const CandSegments& cs, int64_t rows, int64_t k, int32_t* out_idx,
                                   float* out_val, hipStream_t stream);
+hipError_t launch_topk_packed(const CandSegments& cs, int64_t rows, int64_t k, int32_t* out_idx, float* out_val,
+                              hipStream_t stream);
 hipError_t launch_topk_flagged(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k, int32_t* out_idx,
                                float* out_val, hipStream_t stream);
 
@@ -831,15 +845,25 @@ hipError_t launch_topk_flagged(const float* x, int64_t ld, int64_t rows, int64_t
 // sample half as many keys as long ones (C2: the sample pass at 1/32 of the keys, not 1/16).
 constexpr int kFusedSampleTilesMin = 16;
 constexpr int kFusedSampleTilesMax = 32;
-constexpr int kFusedMaxSeg = kCandMaxSeg;
+// Key chunks (candidate slots) per row: four keep the filter pass's grid at thousands
+// of workgroups for long rows (two cost C5 10%: 3.50 -> 3.84 ms); past the register
+// top-k's k, whose slots are twice as large, two.
+constexpr int kFusedMaxSeg = 4;
+constexpr int kFusedMaxSegLargeK = 2;
+static_assert(kFusedMaxSeg <= kCandMaxSeg, "the register top-k walks at most kCandMaxSeg chunks");
 constexpr int kFusedSampleChunkTiles = 8;  // sampled tiles per workgroup of the sample pass
+constexpr int kFusedMaxK = 8192;
+constexpr int kFusedRegK = 4096;           // largest k the register top-k takes (beyond: radix)
+constexpr size_t kFusedMinFallback = size_t(64) << 20;  // dense-fallback rows per round: at least 64 MB
 
 struct FusedPlan {
   bool fused;
   int64_t rows, ld, sample_ld, ldc;
   int64_t key_chunk, tile_stride;
   int nseg, cap;
-  size_t dense, sample, thr, valid, cval, ccnt, pval, pidx, plen, total;
+  int64_t fb_rows;  // rows per dense-fallback round
+  int rounds;
+  size_t cval, sample, thr, valid, ccnt, pval, pidx, plen, total;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
@@ -849,8 +873,8 @@ static FusedPlan fused_plan(int64_t rows, int64_t B, int64_t S1, int64_t S2, int
   FusedPlan p = {};
   p.rows = rows;
   p.ld = (S2 + 3) & ~int64_t(3);
-  // At most kFusedMaxSeg key chunks (candidate slots) per row.
-  const int64_t min_chunk = ((S2 + kFusedMaxSeg - 1) / kFusedMaxSeg + kIdxKeyTile - 1) / kIdxKeyTile * kIdxKeyTile;
+  const int max_seg = k <= kFusedRegK ? kFusedMaxSeg : kFusedMaxSegLargeK;
+  const int64_t min_chunk = ((S2 + max_seg - 1) / max_seg + kIdxKeyTile - 1) / kIdxKeyTile * kIdxKeyTile;
   p.key_chunk = indexer_key_chunk(B, S1, S2);
   if (p.key_chunk < min_chunk) p.key_chunk = min_chunk;
   p.nseg = (int)((S2 + p.key_chunk - 1) / p.key_chunk);
@@ -860,24 +884,33 @@ static FusedPlan fused_plan(int64_t rows, int64_t B, int64_t S1, int64_t S2, int
   const int64_t F = tiles / sample_tiles > 1 ? tiles / sample_tiles : 1;
   p.tile_stride = F * kIdxKeyTile;
   p.sample_ld = (S2 + p.tile_stride - 1) / p.tile_stride * kIdxKeyTile;  // <= 4096: F >= tiles / 64
-  const int64_t cap4k = (4 * k + 63) & ~int64_t(63);
-  p.cap = (int)(p.key_chunk < cap4k ? p.key_chunk : cap4k);
-  p.ldc = ((4 * k + 4095) / 4096) * 4096;
-  p.fused = k <= 4096 && S2 >= 16384 && S2 >= 8 * k &&
-            p.nseg <= kFusedMaxSeg && p.ldc <= 32768 && p.sample_ld <= 4096 && p.rows > 0;
-  size_t off = align256((size_t)p.rows * p.ld * sizeof(float));
-  p.dense = 0;
-  if (p.fused) {
-    const size_t R = (size_t)p.rows;
-    p.sample = off; off = align256(off + R * p.sample_ld * 4);
-    p.thr = off; off = align256(off + R * 4);
-    p.valid = off; off = align256(off + R * 4);
-    p.cval = off; off = align256(off + R * p.nseg * p.cap * 8);
-    p.ccnt = off; off = align256(off + R * p.nseg * 4);
-    p.pval = off; off = align256(off + R * p.ldc * 4);
-    p.pidx = off; off = align256(off + R * p.ldc * 4);
-    p.plen = off; off = align256(off + R * 4);
-  }
+  // Packed-row capacity: 4 k for the register top-k, 2 k + 2048 past it (radix top-k).
+  // A chunk's slot holds 2 k + 1024 (resp. a whole packed row) -- more than the kept
+  // count of a whole row (about 1.8 k at C5, 1.4 k at k = 8192), so only a row whose
+  // kept keys crowd into one chunk past that overflows (and goes back to its dense logits).
+  const int64_t cap_k = k <= kFusedRegK ? (2 * k + 1024 + 63) & ~int64_t(63) : (2 * k + 2048 + 63) & ~int64_t(63);
+  p.ldc = k <= kFusedRegK ? ((4 * k + 4095) / 4096) * 4096 : cap_k;
+  p.cap = (int)std::min<int64_t>(p.key_chunk, cap_k);
+  p.fused = k <= kFusedMaxK && S2 >= 16384 && S2 >= 8 * k && p.nseg <= max_seg &&
+            (k > kFusedRegK || p.ldc <= 32768) && p.sample_ld <= 4096 && p.rows > 0;
+  if (!p.fused) return p;
+  const size_t R = (size_t)p.rows;
+  // The candidate slots, which the dense-fallback rounds reuse once the top-k has read them.
+  const size_t slots = R * p.nseg * p.cap * 8;
+  const size_t row_bytes = (size_t)p.ld * 4;
+  p.fb_rows = (int64_t)(std::max(slots, kFusedMinFallback) / row_bytes);
+  if (p.fb_rows < 1) p.fb_rows = 1;
+  if (p.fb_rows > p.rows) p.fb_rows = p.rows;
+  p.rounds = (int)((p.rows + p.fb_rows - 1) / p.fb_rows);
+  size_t off = 0;
+  p.cval = off; off = align256(off + std::max(slots, (size_t)p.fb_rows * row_bytes));
+  p.sample = off; off = align256(off + R * p.sample_ld * 4);
+  p.thr = off; off = align256(off + R * 4);
+  p.valid = off; off = align256(off + R * 4);
+  p.ccnt = off; off = align256(off + R * p.nseg * 4);
+  p.pval = off; off = align256(off + R * p.ldc * 4);
+  p.pidx = off; off = align256(off + R * p.ldc * 4);
+  p.plen = off; off = align256(off + R * 4);
   p.total = off;
   return p;
 }
@@ -954,24 +987,34 @@ hipError_t launch_indexer_topk_fused(int kind, const void* q, const void* k, con
   hipLaunchKernelGGL(fused_threshold_kernel, dim3((unsigned)((p.rows + 3) / 4)), dim3(256), 0, stream, a.sample,
                      p.sample_ld, a.row_valid, p.rows, (int)topk, a.thr);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  // 3. Filter pass over the usual key chunks (one candidate slot per chunk).
+  // 3. Filter pass over the key chunks (one candidate slot per chunk).
   a.tile_stride = kIdxKeyTile;
   a.key_chunk = (int)p.key_chunk;
   if ((e = launch_indexer_mode<kModeFilter>(kind, D, a, B, stream)) != hipSuccess) return e;
-  // 4-5. Top-k over the candidates where the filter left them.
+  // 4-5. Top-k over the candidates.
   const CandSegments cs = {a.cand, a.cand_cnt, a.thr, p.nseg, p.cap, (int)p.ldc,
                            reinterpret_cast<float*>(ws + p.pval), reinterpret_cast<int32_t*>(ws + p.pidx),
                            reinterpret_cast<int32_t*>(ws + p.plen)};
-  if ((e = launch_topk_candidates(cs, p.rows, topk, out_idx, out_val, stream)) != hipSuccess) return e;
-  // 6. Rows still flagged: dense logits, then the exact radix top-k.
-  float* dense = reinterpret_cast<float*>(ws);
-  a.logits = dense;
+  e = topk <= kFusedRegK ? launch_topk_candidates(cs, p.rows, topk, out_idx, out_val, stream)
+                         : launch_topk_packed(cs, p.rows, topk, out_idx, out_val, stream);
+  if (e != hipSuccess) return e;
+  // 6. Rows still flagged, fb_rows consecutive rows a round: dense logits into the
+  // candidate slots (read by now), then the exact radix top-k of those rows.
+  float* fb = reinterpret_cast<float*>(ws + p.cval);
+  a.logits = fb;
   a.ld = p.ld;
   a.flag_idx = out_idx;
   a.flag_ld = topk;
   a.key_chunk = (int)p.key_chunk;
-  if ((e = launch_indexer_mode<kModeDense>(kind, D, a, B, stream)) != hipSuccess) return e;
-  return launch_topk_flagged(dense, p.ld, p.rows, S2, topk, out_idx, out_val, stream);
+  for (int rd = 0; rd < p.rounds; ++rd) {
+    a.row_lo = (int64_t)rd * p.fb_rows;
+    a.row_hi = std::min<int64_t>(p.rows, a.row_lo + p.fb_rows);
+    if ((e = launch_indexer_mode<kModeDense>(kind, D, a, B, stream)) != hipSuccess) return e;
+    if ((e = launch_topk_flagged(fb, p.ld, a.row_hi - a.row_lo, S2, topk, out_idx + a.row_lo * topk,
+                                 out_val ? out_val + a.row_lo * topk : nullptr, stream)) != hipSuccess)
+      return e;
+  }
+  return hipSuccess;
 }
 
 }  // namespace dsa

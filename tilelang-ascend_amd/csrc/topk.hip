@@ -911,6 +911,55 @@ hipError_t launch_topk_candidates(const CandSegments& cs, int64_t rows, int64_t 
   return launch_rows(cs.pval, cs.ldc, rows, cs.ldc, k, cs.plen, 1, out_idx, out_val, 1, cs.pidx, stream);
 }
 
+// Every candidate row packed in key order into cs.pval / cs.pidx (one 256-thread
+// workgroup per row), for k beyond the register top-k.  A row whose candidates
+// cannot hold its top k -- a chunk overflowed, more kept keys than a packed row
+// holds, or a finite threshold that fewer than k keys reached -- gets packed
+// length -1 and out_idx[row][0] = kFallbackFlag: its dense logits decide.
+__global__ __launch_bounds__(256) void cand_pack_kernel(const CandSegments cs, int k, int32_t* __restrict__ out_idx) {
+  const int row = blockIdx.x;
+  const u32x2* crow = cs.cand + (int64_t)row * cs.nseg * cs.cap;
+  int soff[kCandMaxSeg];
+  int tot = 0;
+  bool over = false;
+#pragma unroll
+  for (int z = 0; z < kCandMaxSeg; ++z) {
+    soff[z] = z < cs.nseg ? tot : (1 << 30);
+    if (z < cs.nseg) {
+      const int c = cs.count[(int64_t)row * cs.nseg + z];
+      over |= c > cs.cap;
+      tot += min(c, cs.cap);
+    }
+  }
+  const bool back = over || tot > cs.ldc || (tot < k && cs.thr[row] != -__builtin_huge_valf());
+  if (threadIdx.x == 0) {
+    cs.plen[row] = back ? -1 : tot;
+    if (back) out_idx[(int64_t)row * k] = kFallbackFlag;
+  }
+  if (back) return;  // block-uniform
+  float* pv = cs.pval + (int64_t)row * cs.ldc;
+  int32_t* pi = cs.pidx + (int64_t)row * cs.ldc;
+  for (int p = threadIdx.x; p < tot; p += 256) {
+    const u32x2 e = crow[cand_slot(soff, cs.cap, p)];
+    pv[p] = __uint_as_float(e.x);
+    pi[p] = (int32_t)e.y;
+  }
+}
+
+// Top-k over the fused indexer's candidate rows for any k up to 8192: every row
+// packed, then the exact radix kernel over the packed rows (positions map back
+// through cs.pidx; packed position order is key order, which breaks the ties).
+// Rows that go back to the dense path come out flagged in out_idx[row][0].
+hipError_t launch_topk_packed(const CandSegments& cs, int64_t rows, int64_t k, int32_t* out_idx, float* out_val,
+                              hipStream_t stream) {
+  if (rows == 0) return hipSuccess;
+  if (cs.nseg < 1 || cs.nseg > kCandMaxSeg) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(cand_pack_kernel, dim3((unsigned)rows), dim3(256), 0, stream, cs, (int)k, out_idx);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return launch_rows(cs.pval, cs.ldc, rows, cs.ldc, k, cs.plen, 1, out_idx, out_val, 0, cs.pidx, stream);
+}
+
 // The exact radix kernel for the rows whose out_idx[row][0] is kFallbackFlag (sorted output).
 hipError_t launch_topk_flagged(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k, int32_t* out_idx,
                                float* out_val, hipStream_t stream) {
