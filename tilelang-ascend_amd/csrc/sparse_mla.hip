@@ -943,13 +943,25 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   // Epilogue: normalise, write out (or the split partial) and the LSE.  Lane
   // (g, r) holds, for head 16*hb + r, columns 32p + 8g .. 32p + 8g + 7 in
   // blocks 2p and 2p + 1: normalised, they go out as one 16-byte store each.
+  //
+  // Vector-memory stores and loads share one in-order counter, so a register
+  // reload from scratch placed between the stores would wait for every store
+  // before it to be acknowledged.  Hence: the lane's coordinates are taken
+  // afresh from the hardware (nothing address-like is carried across the tile
+  // loop to be spilled), every value is normalised and packed first, and the
+  // stores follow behind a compiler barrier.
+  uint32_t lane_e;
+  __asm__ volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane_e));
+  const int r_e = (int)(lane_e & 15);
+  const int g_e = (int)(lane_e >> 4);
+  float inv_h[2], ltot_h[2], mout_h[2];
 #pragma unroll
   for (int hb = 0; hb < 2; ++hb) {
     float l_tot = lsum[hb];
     l_tot += __shfl_xor(l_tot, 16, kWave);
     l_tot += __shfl_xor(l_tot, 32, kWave);
     float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    const int h = head0 + 16 * hb + r;
+    const int h = head0 + 16 * hb + r_e;
     float m_out = m_ref[hb];
     if constexpr (Geo::kRowLists) {
       // O is normalised by the rounded weights (see SoftmaxSlices), the LSE by
@@ -975,28 +987,53 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
       l_tot = 1.f;
       m_out = 0.f;
     }
-    if (Geo::kRowLists && hb_on[hb] && obase32) {
-      float* orow = obase32 + ((int64_t)token * a.H + h) * kMlaDV + 8 * g;
+    inv_h[hb] = inv;
+    ltot_h[hb] = l_tot;
+    mout_h[hb] = m_out;
+  }
+  if (Geo::kRowLists && obase32) {
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+      if (!hb_on[hb]) continue;
+      float* orow = obase32 + ((int64_t)token * a.H + head0 + 16 * hb + r_e) * kMlaDV + 8 * g_e;
 #pragma unroll
       for (int p2 = 0; p2 < kMlaDV / 32; ++p2) {
-        *reinterpret_cast<f32x4*>(orow + 32 * p2) = o[hb][2 * p2] * inv;
-        *reinterpret_cast<f32x4*>(orow + 32 * p2 + 4) = o[hb][2 * p2 + 1] * inv;
+        *reinterpret_cast<f32x4*>(orow + 32 * p2) = o[hb][2 * p2] * inv_h[hb];
+        *reinterpret_cast<f32x4*>(orow + 32 * p2 + 4) = o[hb][2 * p2 + 1] * inv_h[hb];
       }
-    } else if (hb_on[hb]) {
-      uint16_t* orow = obase + ((int64_t)token * a.H + h) * kMlaDV + 8 * g;
+    }
+  } else {
+    u32x4 pk[2][kMlaDV / 32];
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb)
 #pragma unroll
       for (int p2 = 0; p2 < kMlaDV / 32; ++p2) {
         const f32x4& x = o[hb][2 * p2];
         const f32x4& y = o[hb][2 * p2 + 1];
-        const u32x4 v = {pack2<kF16>(x[0] * inv, x[1] * inv), pack2<kF16>(x[2] * inv, x[3] * inv),
-                         pack2<kF16>(y[0] * inv, y[1] * inv), pack2<kF16>(y[2] * inv, y[3] * inv)};
-        *reinterpret_cast<u32x4*>(orow + 32 * p2) = v;
+        const float inv = inv_h[hb];
+        pk[hb][p2] = u32x4{pack2<kF16>(x[0] * inv, x[1] * inv), pack2<kF16>(x[2] * inv, x[3] * inv),
+                           pack2<kF16>(y[0] * inv, y[1] * inv), pack2<kF16>(y[2] * inv, y[3] * inv)};
       }
+    // Every packed value exists before the first store (none is sunk into a
+    // store's branch, where it would need the reloads the order avoids).
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+      for (int p2 = 0; p2 < kMlaDV / 32; ++p2) __asm__ __volatile__("" : "+v"(pk[hb][p2]));
+    __asm__ __volatile__("" ::: "memory");
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+      if (!hb_on[hb]) continue;
+      uint16_t* orow = obase + ((int64_t)token * a.H + head0 + 16 * hb + r_e) * kMlaDV + 8 * g_e;
+#pragma unroll
+      for (int p2 = 0; p2 < kMlaDV / 32; ++p2) *reinterpret_cast<u32x4*>(orow + 32 * p2) = pk[hb][p2];
     }
-    if (hb_on[hb] && g == 0)
-      lbase[(int64_t)token * a.H + h] =
-          l_tot > 0.f ? (m_out + fast_log2(l_tot)) * 0.69314718055994531f : -__builtin_huge_valf();
   }
+#pragma unroll
+  for (int hb = 0; hb < 2; ++hb)
+    if (hb_on[hb] && g_e == 0)
+      lbase[(int64_t)token * a.H + head0 + 16 * hb + r_e] =
+          ltot_h[hb] > 0.f ? (mout_h[hb] + fast_log2(ltot_h[hb])) * 0.69314718055994531f : -__builtin_huge_valf();
 }
 
 // Merge split partials: lse = log(sum_i exp(lse_i) [+ exp(sink)]),
