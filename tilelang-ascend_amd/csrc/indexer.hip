@@ -255,7 +255,10 @@ struct IdxArgs {
   int64_t row_lo, row_hi;
 };
 
-enum IdxMode : int { kModeDense = 0, kModeSample = 1, kModeFilter = 2 };
+enum IdxMode : int { kModeDense = 0, kModeSample = 1, kModeFilter = 2, kModeFallback = 3 };
+// kModeFallback exists at launch level only: the fused path's bounded dense
+// rounds (flag_idx set), run as indexer_fallback_kernel -- the dense body under
+// a name of its own, so that kernel traces tell them from the plain dense pass.
 
 // kNhb = H / 16 head blocks, a compile-time count: no branch between the MFMAs.
 // kPaged: keys (and their scales) through the block table; otherwise one
@@ -697,6 +700,14 @@ void indexer_filter_fp8_kernel(IdxArgs a) {
   indexer_body<kFp8, kD, kTokPW, kNhb, kPaged, kModeFilter>(a);
 }
 
+// The fused path's fallback rounds: the dense pass under its own kernel name.
+template <int kKind, int kD, int kTokPW, int kNhb, bool kPaged>
+__global__ __launch_bounds__(kIdxThreads)
+__attribute__((amdgpu_waves_per_eu(kKind == kFp8 && kD == 128 ? 3 : 1, kKind == kFp8 && kD == 128 ? 3 : 8)))
+void indexer_fallback_kernel(IdxArgs a) {
+  indexer_body<kKind, kD, kTokPW, kNhb, kPaged, kModeDense>(a);
+}
+
 // Query rows per batch up to which dense logits split each key tile over the
 // waves (one token per workgroup) instead of giving each wave its own tokens.
 constexpr int kIdxSplitRows = 4;
@@ -721,7 +732,7 @@ static hipError_t launch_indexer_split(const IdxArgs& a, int B, hipStream_t stre
 
 template <int kKind, int kD, int kMode = kModeDense>
 static hipError_t launch_indexer_kind(const IdxArgs& a, int B, hipStream_t stream) {
-  if constexpr (kMode == kModeDense)
+  if constexpr (kMode == kModeDense || kMode == kModeFallback)
     if (a.S1 <= kIdxSplitRows) return launch_indexer_split<kKind, kD>(a, B, stream);
   constexpr int kTokPW = 2;
   constexpr int kTok = kTokPW * kIdxWaves;
@@ -729,6 +740,8 @@ static hipError_t launch_indexer_kind(const IdxArgs& a, int B, hipStream_t strea
 #define DSA_IDX(N, P)                                                                                           \
   if constexpr (kKind == kFp8 && kMode == kModeFilter)                                                          \
     hipLaunchKernelGGL((indexer_filter_fp8_kernel<kD, kTokPW, N, P>), grid, dim3(kIdxThreads), 0, stream, a);   \
+  else if constexpr (kMode == kModeFallback)                                                                    \
+    hipLaunchKernelGGL((indexer_fallback_kernel<kKind, kD, kTokPW, N, P>), grid, dim3(kIdxThreads), 0, stream, a); \
   else                                                                                                          \
     hipLaunchKernelGGL((indexer_logits_kernel<kKind, kD, kTokPW, N, P, kMode>), grid, dim3(kIdxThreads), 0, stream, a)
 #define DSA_IDX2(N) \
@@ -1009,7 +1022,7 @@ hipError_t launch_indexer_topk_fused(int kind, const void* q, const void* k, con
   for (int rd = 0; rd < p.rounds; ++rd) {
     a.row_lo = (int64_t)rd * p.fb_rows;
     a.row_hi = std::min<int64_t>(p.rows, a.row_lo + p.fb_rows);
-    if ((e = launch_indexer_mode<kModeDense>(kind, D, a, B, stream)) != hipSuccess) return e;
+    if ((e = launch_indexer_mode<kModeFallback>(kind, D, a, B, stream)) != hipSuccess) return e;
     if ((e = launch_topk_flagged(fb, p.ld, a.row_hi - a.row_lo, S2, topk, out_idx + a.row_lo * topk,
                                  out_val ? out_val + a.row_lo * topk : nullptr, stream)) != hipSuccess)
       return e;
