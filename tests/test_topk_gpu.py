@@ -176,3 +176,33 @@ def test_structured_rows_crowd_waves(dsa, dev):
     runs = torch.stack([torch.cat([torch.sort(torch.randn(2048, generator=g), descending=True).values
                                    for _ in range(4)]) for _ in range(6)])
     _check(dsa, dev, runs, 2048)                                # n = 8192: four sorted runs of 2048
+
+
+def test_candidates_across_zero(dsa, dev):
+    # Rows whose candidates straddle zero: the binning then collapses magnitudes
+    # far below the largest one (the plain order key would crowd them into a few
+    # bins).  Shifted Gaussians (k-th score negative), a huge outlier on either
+    # side, signed zeros and denormals around zero, and a row whose largest
+    # magnitude is itself a denormal (no collapse).
+    g = torch.Generator().manual_seed(123)
+    n = 32768
+    rows = [torch.randn(n, generator=g) - s for s in (1.2, 1.6, 2.5)]
+    r = torch.randn(n, generator=g) - 1.5
+    r[77] = 1.0e30
+    rows.append(r)
+    r = torch.randn(n, generator=g) - 1.5
+    r[5] = -3.0e38
+    r[9] = 2.0e-3
+    rows.append(r)
+    r = torch.randn(n, generator=g) * 1e-3
+    r[::7] = 0.0
+    r[3::7] = -0.0
+    r[1::11] = 1e-42
+    r[2::13] = -1e-42
+    rows.append(r)
+    r = (torch.randn(n, generator=g).sign() * 1e-40).float()
+    rows.append(r)
+    x = torch.stack(rows)
+    _check(dsa, dev, x, 2048)
+    _check(dsa, dev, x, 333)
+    _check(dsa, dev, x[:, :9000], 2048)

@@ -290,7 +290,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(
 // once it holds at least k scores (or t admits every present score) it holds
 // the whole top-k; otherwise t moves by bisection over the sample ranks and
 // the pass repeats.  The candidates alone are then bucketed into 4096 bins of
-// their order keys (key - key(min)) >> shift, a descending scan finds the bin
+// their binning positions (pos - pos(min)) >> shift (cand_pos: the order key
+// with magnitudes far below the largest collapsed), a descending scan finds the bin
 // b* holding the k-th largest, the candidates of bins >= b* are regrouped by
 // bin, and each counts the entries of its own bin that beat it (bins rarely
 // hold more than one): bin start + that rank is its sorted position, exact
@@ -392,6 +393,22 @@ __device__ __forceinline__ uint32_t lane_prefix(uint64_t m, uint32_t add) {  // 
 __device__ __forceinline__ uint32_t cand_key(float x) {
   const uint32_t u = __float_as_uint(x + 0.0f);
   return u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
+}
+
+// Binning position of a candidate: the order key with every magnitude below
+// `floor_bits` collapsed onto zero.  Monotone non-decreasing in the value, so
+// bins stay ordered and the in-bin ranking stays exact.  The plain key spreads
+// the binades near zero over ~2^31 of its range: candidates on both sides of
+// zero then crowded a few bins, and ranking a bin costs its size squared (up to
+// 60 us for one C2 row).  Such rows collapse the magnitudes more than
+// kBinBinades binades under the largest candidate magnitude; rows of one sign
+// keep the plain key (floor_bits = 0).
+constexpr uint32_t kBinBinades = 12;
+__device__ __forceinline__ uint32_t cand_pos(float x, uint32_t floor_bits) {
+  const uint32_t u = __float_as_uint(x + 0.0f);
+  const uint32_t mag = u & 0x7fffffffu;
+  const uint32_t cm = mag > floor_bits ? mag - floor_bits : 0u;
+  return (u >> 31) ? 0x80000000u - cm : 0x80000000u + cm;
 }
 
 // Ballot compaction of the scores >= t among a thread's registers into
@@ -718,13 +735,20 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
   const uint32_t kmax = row0_max(wl ? red[kRedMax + lane] : 0u);
 
   if (kk > 0) {
-    // 4. Bucket the candidates by order key: bin = (key - kmin) >> sh < 4096.
-    const uint32_t range = kmax - kmin;
+    // 4. Bucket the candidates by binning position: bin = (pos - pos(min)) >> sh
+    // < 4096.  The extreme candidates (keys kmin, kmax) carry the extreme
+    // magnitudes, which fix the collapse floor of rows across zero.
+    const float vlo = key_to_float(kmin), vhi = key_to_float(kmax);
+    const uint32_t mhi = max(__float_as_uint(vlo) & 0x7fffffffu, __float_as_uint(vhi) & 0x7fffffffu);
+    const bool across = vlo < 0.f && vhi > 0.f;
+    const uint32_t floor_bits = across && (mhi >> 23) > kBinBinades ? ((mhi >> 23) - kBinBinades) << 23 : 0u;
+    const uint32_t plo = cand_pos(vlo, floor_bits);
+    const uint32_t range = cand_pos(vhi, floor_bits) - plo;
     const int sh = max(0, (range ? 32 - __builtin_clz(range) : 0) - kCandBinBits);
     uint32_t eb[kLaneEntries];
 #pragma unroll
     for (int q = 0; q < kLaneEntries; ++q) {
-      eb[q] = (cand_key(ev[q]) - kmin) >> sh;
+      eb[q] = (cand_pos(ev[q], floor_bits) - plo) >> sh;
       if (ev[q] != -__builtin_huge_valf()) atomicAdd(&cnt[eb[q]], 1u);
       else eb[q] = 0xffffffffu;
     }
