@@ -85,6 +85,11 @@ struct CandSegments {
   float* pval;
   int32_t* pidx;
   int32_t* plen;
+  // Counters (zeroed by an earlier launch on the stream, or null): rows handed
+  // to the radix kernel on their packed candidates, and rows sent back to their
+  // dense logits.  The passes behind read them and skip their work at zero.
+  int32_t* nspill;
+  int32_t* nback;
 };
 
 __device__ __forceinline__ float wave_max(float v) {

@@ -253,6 +253,8 @@ struct IdxArgs {
   // With flag_idx: only rows row_lo .. row_hi - 1 count, and only they are stored, at
   // logits + (row - row_lo) * ld (the fused path's bounded fallback buffer, one round).
   int64_t row_lo, row_hi;
+  // With flag_idx, or null: the count of flagged rows (zero: every workgroup ends at once).
+  const int32_t* flag_count;
 };
 
 enum IdxMode : int { kModeDense = 0, kModeSample = 1, kModeFilter = 2, kModeFallback = 3 };
@@ -349,6 +351,8 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
   const bool ranged = kMode == kModeDense && a.flag_idx;
   auto stored = [&](int t) { return !ranged || (q_base + t >= a.row_lo && q_base + t < a.row_hi); };
   if (ranged) {  // block-uniform: every thread reads the same flags
+    typedef const __attribute__((address_space(4))) int32_t const_i32;
+    if (a.flag_count && *(const_i32*)a.flag_count == 0) return;
     bool any = false;
 #pragma unroll
     for (int j = 0; j < kTok; ++j) {
@@ -849,7 +853,7 @@ hipError_t launch_topk_candidates(const CandSegments& cs, int64_t rows, int64_t 
 hipError_t launch_topk_packed(const CandSegments& cs, int64_t rows, int64_t k, int32_t* out_idx, float* out_val,
                               hipStream_t stream);
 hipError_t launch_topk_flagged(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k, int32_t* out_idx,
-                               float* out_val, hipStream_t stream);
+                               float* out_val, hipStream_t stream, const int32_t* gate);
 
 // Sampled tiles per row: S2 / (2 k) clamped to [16, 32], so that mu = k * sampled / S2 stays
 // at least 32 where the row allows it (a smaller mu widens the spread of the kept count
@@ -876,7 +880,7 @@ struct FusedPlan {
   int nseg, cap;
   int64_t fb_rows;  // rows per dense-fallback round
   int rounds;
-  size_t cval, sample, thr, valid, ccnt, pval, pidx, plen, total;
+  size_t cval, sample, thr, valid, ccnt, pval, pidx, plen, counts, total;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
@@ -924,6 +928,7 @@ static FusedPlan fused_plan(int64_t rows, int64_t B, int64_t S1, int64_t S2, int
   p.pval = off; off = align256(off + R * p.ldc * 4);
   p.pidx = off; off = align256(off + R * p.ldc * 4);
   p.plen = off; off = align256(off + R * 4);
+  p.counts = off; off = align256(off + 2 * 4);  // rows spilled to the radix kernel, rows sent back
   p.total = off;
   return p;
 }
@@ -935,10 +940,13 @@ size_t indexer_topk_fused_bytes(int64_t rows, int64_t B, int64_t S1, int64_t S2,
 }
 
 // Thresholds after a sample pass of several key chunks: one wave per row.
+// It also clears the two row counters of the top-k passes behind it (no memset: graph capture).
 __global__ __launch_bounds__(256) void fused_threshold_kernel(const float* __restrict__ sample, int64_t sld,
                                                               const int32_t* __restrict__ row_valid, int64_t rows,
-                                                              int k, float* __restrict__ thr) {
+                                                              int k, float* __restrict__ thr,
+                                                              int32_t* __restrict__ counts) {
   const int lane = threadIdx.x & (kWave - 1);
+  if (blockIdx.x == 0 && threadIdx.x < 2) counts[threadIdx.x] = 0;
   const int64_t row = (int64_t)blockIdx.x * (256 / kWave) + threadIdx.x / kWave;
   if (row >= rows) return;
   const float* sr = sample + row * sld;
@@ -997,8 +1005,9 @@ hipError_t launch_indexer_topk_fused(int kind, const void* q, const void* k, con
   a.key_chunk = (int)(p.tile_stride * kFusedSampleChunkTiles);
   hipError_t e = launch_indexer_mode<kModeSample>(kind, D, a, B, stream);
   if (e != hipSuccess) return e;
+  int32_t* counts = reinterpret_cast<int32_t*>(ws + p.counts);
   hipLaunchKernelGGL(fused_threshold_kernel, dim3((unsigned)((p.rows + 3) / 4)), dim3(256), 0, stream, a.sample,
-                     p.sample_ld, a.row_valid, p.rows, (int)topk, a.thr);
+                     p.sample_ld, a.row_valid, p.rows, (int)topk, a.thr, counts);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   // 3. Filter pass over the key chunks (one candidate slot per chunk).
   a.tile_stride = kIdxKeyTile;
@@ -1007,7 +1016,7 @@ hipError_t launch_indexer_topk_fused(int kind, const void* q, const void* k, con
   // 4-5. Top-k over the candidates.
   const CandSegments cs = {a.cand, a.cand_cnt, a.thr, p.nseg, p.cap, (int)p.ldc,
                            reinterpret_cast<float*>(ws + p.pval), reinterpret_cast<int32_t*>(ws + p.pidx),
-                           reinterpret_cast<int32_t*>(ws + p.plen)};
+                           reinterpret_cast<int32_t*>(ws + p.plen), counts, counts + 1};
   e = topk <= kFusedRegK ? launch_topk_candidates(cs, p.rows, topk, out_idx, out_val, stream)
                          : launch_topk_packed(cs, p.rows, topk, out_idx, out_val, stream);
   if (e != hipSuccess) return e;
@@ -1018,13 +1027,14 @@ hipError_t launch_indexer_topk_fused(int kind, const void* q, const void* k, con
   a.ld = p.ld;
   a.flag_idx = out_idx;
   a.flag_ld = topk;
+  a.flag_count = counts + 1;
   a.key_chunk = (int)p.key_chunk;
   for (int rd = 0; rd < p.rounds; ++rd) {
     a.row_lo = (int64_t)rd * p.fb_rows;
     a.row_hi = std::min<int64_t>(p.rows, a.row_lo + p.fb_rows);
     if ((e = launch_indexer_mode<kModeFallback>(kind, D, a, B, stream)) != hipSuccess) return e;
     if ((e = launch_topk_flagged(fb, p.ld, a.row_hi - a.row_lo, S2, topk, out_idx + a.row_lo * topk,
-                                 out_val ? out_val + a.row_lo * topk : nullptr, stream)) != hipSuccess)
+                                 out_val ? out_val + a.row_lo * topk : nullptr, stream, counts + 1)) != hipSuccess)
       return e;
   }
   return hipSuccess;

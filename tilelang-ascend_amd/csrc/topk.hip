@@ -242,11 +242,16 @@ __device__ __forceinline__ void radix_row(const int row, const float* __restrict
 // gridDim.x), reads 1024 of their flags at once and runs the flagged ones, so a
 // launch with nothing flagged costs one flag load per thread instead of a
 // workgroup (and its LDS allocation) per row.
+//
+// gate (flagged walk only, may be null): a count of flagged rows written by an
+// earlier launch; at zero the launch ends after one scalar load per workgroup.
 template <bool kCached>
 __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(
     const float* __restrict__ x, int64_t ld, int n, int k, const int32_t* __restrict__ row_len,
     int sorted, int kpad, int32_t* __restrict__ out_idx, float* __restrict__ out_val, int only_flagged,
-    const int32_t* __restrict__ idx_map, int rows) {
+    const int32_t* __restrict__ idx_map, int rows, const int32_t* __restrict__ gate) {
+  typedef const __attribute__((address_space(4))) int32_t const_i32;
+  if (only_flagged && gate && *(const_i32*)gate == 0) return;  // block-uniform
   if (!only_flagged) {
     radix_row<kCached>(blockIdx.x, x, ld, n, k, row_len, sorted, kpad, out_idx, out_val, 0, idx_map);
     return;
@@ -476,9 +481,10 @@ __device__ __forceinline__ int cand_slot(const int (&soff)[kCandMaxSeg], int cap
 }
 
 // A candidate row the register path hands to the radix kernel: its pairs
-// packed in position order into pval / pidx.
+// packed in position order into pval / pidx, and counted.
 __device__ void cand_spill(const CandSegments& cs, const u32x2* crow, const int (&soff)[kCandMaxSeg], int row,
                            int nv) {
+  if (threadIdx.x == 0 && cs.nspill) atomicAdd(cs.nspill, 1);
   float* pv = cs.pval + (int64_t)row * cs.ldc;
   int32_t* pi = cs.pidx + (int64_t)row * cs.ldc;
   for (int p = threadIdx.x; p < nv; p += kTopkThreads) {
@@ -537,8 +543,11 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
     const bool back = over || tot > cs.ldc || (tot < k && cs.thr[row] != -__builtin_huge_valf());
     if (tid == 0) cs.plen[row] = back ? -1 : tot;
     if (back) {
-      if (tid == 0) oi[0] = kFallbackFlag;  // the radix kernel leaves it for the dense path
-      return;                               // block-uniform
+      if (tid == 0) {
+        oi[0] = kFallbackFlag;  // the radix kernel leaves it for the dense path
+        if (cs.nback) atomicAdd(cs.nback, 1);
+      }
+      return;  // block-uniform
     }
     nv = tot;
   }
@@ -882,7 +891,8 @@ size_t topk_workspace_bytes(int64_t rows, int64_t n, int64_t k) {
 // and long rows take the radix kernel alone).
 static hipError_t launch_rows(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k,
                               const int32_t* row_len, int sorted, int32_t* out_idx, float* out_val,
-                              int only_flagged, const int32_t* idx_map, hipStream_t stream);
+                              int only_flagged, const int32_t* idx_map, hipStream_t stream,
+                              const int32_t* gate = nullptr);
 
 hipError_t launch_topk(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k,
                        const int32_t* row_len, int sorted, int32_t* out_idx, float* out_val,
@@ -932,7 +942,7 @@ hipError_t launch_topk_candidates(const CandSegments& cs, int64_t rows, int64_t 
 #undef DSA_CAND
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  return launch_rows(cs.pval, cs.ldc, rows, cs.ldc, k, cs.plen, 1, out_idx, out_val, 1, cs.pidx, stream);
+  return launch_rows(cs.pval, cs.ldc, rows, cs.ldc, k, cs.plen, 1, out_idx, out_val, 1, cs.pidx, stream, cs.nspill);
 }
 
 // Every candidate row packed in key order into cs.pval / cs.pidx (one 256-thread
@@ -958,7 +968,10 @@ __global__ __launch_bounds__(256) void cand_pack_kernel(const CandSegments cs, i
   const bool back = over || tot > cs.ldc || (tot < k && cs.thr[row] != -__builtin_huge_valf());
   if (threadIdx.x == 0) {
     cs.plen[row] = back ? -1 : tot;
-    if (back) out_idx[(int64_t)row * k] = kFallbackFlag;
+    if (back) {
+      out_idx[(int64_t)row * k] = kFallbackFlag;
+      if (cs.nback) atomicAdd(cs.nback, 1);
+    }
   }
   if (back) return;  // block-uniform
   float* pv = cs.pval + (int64_t)row * cs.ldc;
@@ -984,16 +997,18 @@ hipError_t launch_topk_packed(const CandSegments& cs, int64_t rows, int64_t k, i
   return launch_rows(cs.pval, cs.ldc, rows, cs.ldc, k, cs.plen, 1, out_idx, out_val, 0, cs.pidx, stream);
 }
 
-// The exact radix kernel for the rows whose out_idx[row][0] is kFallbackFlag (sorted output).
+// The exact radix kernel for the rows whose out_idx[row][0] is kFallbackFlag (sorted output);
+// gate (or null): a count of those rows, written by an earlier launch (zero: nothing to do).
 hipError_t launch_topk_flagged(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k, int32_t* out_idx,
-                               float* out_val, hipStream_t stream) {
+                               float* out_val, hipStream_t stream, const int32_t* gate) {
   if (rows == 0) return hipSuccess;
-  return launch_rows(x, ld, rows, n, k, nullptr, 1, out_idx, out_val, 1, nullptr, stream);
+  return launch_rows(x, ld, rows, n, k, nullptr, 1, out_idx, out_val, 1, nullptr, stream, gate);
 }
 
 static hipError_t launch_rows(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k,
                               const int32_t* row_len, int sorted, int32_t* out_idx, float* out_val,
-                              int only_flagged, const int32_t* idx_map, hipStream_t stream) {
+                              int only_flagged, const int32_t* idx_map, hipStream_t stream,
+                              const int32_t* gate) {
   const int kpad = sorted ? next_pow2((int)(k < 2 ? 2 : k)) : 0;
   const size_t base = (size_t)(kHistBins + kRedWords) * 4 + (size_t)kpad * 8;
   const size_t cached = base + (size_t)n * 4;
@@ -1006,12 +1021,12 @@ static hipError_t launch_rows(const float* x, int64_t ld, int64_t rows, int64_t 
     const hipError_t ea = set_dynamic_lds_once<topk_rows_kernel<true>>(kLdsBytes - kRowsStaticLds);
     if (ea != hipSuccess) return ea;
     hipLaunchKernelGGL(topk_rows_kernel<true>, grid, block, lds, stream, x, ld, (int)n, (int)k, row_len,
-                       sorted, kpad, out_idx, out_val, only_flagged, idx_map, (int)rows);
+                       sorted, kpad, out_idx, out_val, only_flagged, idx_map, (int)rows, gate);
   } else {
     const hipError_t ea = set_dynamic_lds_once<topk_rows_kernel<false>>(kLdsBytes - kRowsStaticLds);
     if (ea != hipSuccess) return ea;
     hipLaunchKernelGGL(topk_rows_kernel<false>, grid, block, lds, stream, x, ld, (int)n, (int)k, row_len,
-                       sorted, kpad, out_idx, out_val, only_flagged, idx_map, (int)rows);
+                       sorted, kpad, out_idx, out_val, only_flagged, idx_map, (int)rows, gate);
   }
   return hipGetLastError();
 }
