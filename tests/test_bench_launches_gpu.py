@@ -3,8 +3,7 @@
 * C2 (indexer + top-k alone: 4096 query rows x 32768 keys, 64 fp8 heads x 128, per-key scale,
   causal, top-2048): the whole logits launch runs once; 16 rows spread over it (both ends
   included) are compared with the oracle's logits; the dense and the streamed (fused) top-k of
-  the launch agree bit for bit on every row, and on the 16 rows equal topk_stable of the GPU
-  logits.
+  the launch both equal topk_stable of the GPU logits on every one of the 4096 rows.
 * C3 (paged decode: 64 sequences x 65536 keys in 64-token blocks under a random block table,
   128 heads, top-2048): the whole launch runs once through the C ABI with the block table, as
   bench.py calls it; 8 sequences are compared with the oracle on a compact copy of each
@@ -43,8 +42,8 @@ def test_c2_launch_logits_and_topk(dsa, dev):
     _log("C2 logits launch")
     logits = dsa.indexer_logits(q, k, w, ks, sparse_mode=3)
     rows = sorted({int(round(i * (S1 - 1) / 15)) for i in range(16)})
-    sel = torch.tensor(rows, device=dev)
-    lg = logits[0, sel].cpu()
+    lg_all = logits[0].cpu()
+    lg = lg_all[rows]
     del logits
     _log("C2 oracle logits")
     kc, ksc = k.cpu(), ks.cpu()
@@ -58,9 +57,13 @@ def test_c2_launch_logits_and_topk(dsa, dev):
     fi, fv = dsa.lightning_indexer(q, k, w, key_scale=ks, sparse_count=K, sparse_mode=3, return_value=True,
                                    fuse_topk=True)
     torch.cuda.synchronize()
-    assert torch.equal(fi, di) and torch.equal(fv, dv)
-    ri, rv = ref.topk_stable(lg, K)
-    assert torch.equal(di[0, sel, 0].cpu(), ri) and torch.equal(dv[0, sel, 0].cpu(), rv)
+    _log("C2 oracle top-k of the GPU logits, every row")
+    ri, rv = ref.topk_stable(lg_all, K)
+    for name, (i, v) in (("dense", (di, dv)), ("fused", (fi, fv))):
+        i, v = i[0, :, 0].cpu(), v[0, :, 0].cpu()
+        bad = (i != ri).any(1)
+        assert not bad.any(), f"{name}: {int(bad.sum())} rows differ, first {int(bad.nonzero()[0])}"
+        assert torch.equal(v, rv), name
 
 
 def test_c3_decode_launch(dsa, dev):
