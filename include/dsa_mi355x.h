@@ -257,6 +257,35 @@ int dsa_sparse_mla_fwd_noalloc(int kind, const void* q, const void* kv, const in
                                int64_t block_size, int64_t max_blocks, int64_t topk, float sm_scale, int is_causal,
                                void* out, float* lse, void* stream);
 
+/* Workspace bytes dsa_sparse_attention_fwd needs (0 for d_qk 128, and when no split is used). */
+size_t dsa_sparse_attention_workspace_size(int64_t B, int64_t S, int64_t H, int64_t kv_group, int64_t d_qk,
+                                           int64_t topk);
+
+/*
+ * Sparse attention over kv_group KV heads, with LSE.
+ * Replaces the `sparse_attention_fwd` builders with their `kv_group` argument
+ * (examples/sparse_flash_attention/example_sparse_flash_attn.py:19-29, kv
+ * [B, Skv, kv_group, dim + tail_dim], indices [B, S, kv_group, topk]; paged:
+ * example_sparse_flash_attn_mask_pa.py:14-46) and the grouped 128-wide kernel of
+ * examples/sparse_flash_attention/example_sparse_flash_attn_gqa.py:13-238.
+ * Query heads g * Hg .. (g + 1) * Hg - 1 (Hg = H / kv_group) read KV head g
+ * through indices[b, s, g, :] (the goldens' q.view(b, s, g, Hg, d)).
+ *
+ *  q        [B, S, H, d_qk]
+ *  kv       [B, Skv, kv_group, d_qk], or (d_qk 576 only) with block_table a
+ *           paged pool [num_blocks, block_size, kv_group, d_qk]; V = kv[..., :d_v]
+ *  indices  [B, S, kv_group, topk] int32, -1 = empty slot
+ *  out      [B, S, H, d_v] of `kind`;  lse [B, S, H] fp32 (natural log)
+ * (d_qk, d_v) = (576, 512): Hg a multiple of 16 (the 576-wide kernels of
+ * dsa_sparse_mla_fwd); (128, 128): any Hg <= 1024, topk <= 8192, no block
+ * table.  Slot validity, causality and lengths as dsa_sparse_mla_fwd.
+ */
+int dsa_sparse_attention_fwd(int kind, const void* q, const void* kv, const int32_t* indices,
+                             const int32_t* block_table, const int32_t* actual_q_len, const int32_t* actual_kv_len,
+                             int64_t B, int64_t S, int64_t H, int64_t kv_group, int64_t d_qk, int64_t d_v, int64_t Skv,
+                             int64_t block_size, int64_t max_blocks, int64_t topk, float sm_scale, int is_causal,
+                             void* out, float* lse, void* workspace, size_t workspace_bytes, void* stream);
+
 /*
  * DeepSeek V4 sparse flash MLA (D = 512, K = V, paged caches, attention sinks).
  * Replaces `sparse_flash_mla(...)` (examples/deepseek_v4/sparse_flash_mla/

@@ -38,6 +38,12 @@ How each function is pinned (see ``tests/test_oracle.py``):
   (out = V row, lse = scale.q.k), equal scores (mean of V), permutation
   invariance, ``-1`` padding equal to dropping the slot, LSE against
   ``torch.logsumexp``.
+* ``sparse_attention_grouped`` (KV groups, ``examples/sparse_flash_attention/example_sparse_flash_attn_gqa.py``):
+  the dense restatement of that example's golden (``sparse_gqa_dense_ref``, which
+  maps heads to groups by the golden's view / repeat_interleave rather than by
+  slicing), equality with ``sparse_mla_fwd`` at one group, a permutation of the
+  groups permuting the outputs, and a single valid index per group (out = that
+  group's V row).
 * ``fp8_quantize_per_token``: absmax maps to 448, representable values round
   trip exactly.
 * ``act_quant`` (``examples/deepseek_v4/act_quant.py:118-142``, int8, extended
@@ -417,6 +423,78 @@ def sparse_mla_dense_ref(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tenso
     p = score.softmax(dim=-1)
     p = torch.nan_to_num(p, nan=0.0)
     return torch.einsum("bshn,bnd->bshd", p, kvf[..., :d_v]).to(torch.float32)
+
+
+def sparse_attention_grouped(
+    q: torch.Tensor,
+    kv: torch.Tensor,
+    indices: torch.Tensor,
+    sm_scale: Optional[float] = None,
+    *,
+    d_v: int,
+    block_table: Optional[torch.Tensor] = None,
+    actual_seq_lengths_query: Optional[Sequence[int]] = None,
+    actual_seq_lengths_kv: Optional[Sequence[int]] = None,
+    is_causal: bool = True,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Sparse attention over G KV heads: (out fp32 [B, S, H, d_v], lse fp32 [B, S, H]).
+
+    kv [B, Skv, G, Dqk] (or, with ``block_table``, a pool [num_blocks, block_size, G, Dqk]);
+    indices [B, S, G, topk].  Query heads g*Hg .. (g+1)*Hg - 1 (Hg = H / G) read KV head g
+    through indices[:, :, g] (example_sparse_flash_attn.py:41-46 shapes; the goldens'
+    q.view(b, sq, g, h, d), example_sparse_flash_attn_gqa.py:276-283).  Groups do not
+    interact: each is ``sparse_mla_fwd`` on its own slices, with the default scale
+    Dqk^-0.5 of the whole row (example_sparse_flash_attn_gqa.py:30).
+    """
+    B, S, H, Dqk = q.shape
+    G = kv.shape[2]
+    assert H % G == 0, "H must be a multiple of the KV groups"
+    Hg = H // G
+    if sm_scale is None:
+        sm_scale = Dqk ** -0.5
+    idx = indices.reshape(B, S, G, -1)
+    out = torch.zeros((B, S, H, d_v), dtype=torch.float32)
+    lse = torch.full((B, S, H), NEG_INF, dtype=torch.float32)
+    for g in range(G):
+        o, l = sparse_mla_fwd(q[:, :, g * Hg:(g + 1) * Hg], kv[:, :, g:g + 1], idx[:, :, g:g + 1], sm_scale,
+                              d_v=d_v, block_table=block_table, actual_seq_lengths_query=actual_seq_lengths_query,
+                              actual_seq_lengths_kv=actual_seq_lengths_kv, is_causal=is_causal)
+        out[:, :, g * Hg:(g + 1) * Hg] = o
+        lse[:, :, g * Hg:(g + 1) * Hg] = l
+    return out, lse
+
+
+def sparse_gqa_dense_ref(q: torch.Tensor, kv: torch.Tensor, indices: torch.Tensor,
+                         q_start_index_s: Optional[int] = None, sm_scale: Optional[float] = None,
+                         d_v: Optional[int] = None) -> torch.Tensor:
+    """Dense scatter-mask restatement of the grouped golden
+    ``ref_sparse_attention_fwd_interface_gqa`` (example_sparse_flash_attn_gqa.py:241-283,
+    kv_stride 1): a [B, G, S, Skv] mask per KV head from its index rows (-1 slots dropped)
+    AND the causal mask q_start + t >= j, scores of q viewed as [B, S, G, Hg, D], and the
+    probabilities of query head h applied to KV head h // Hg (the golden's
+    ``repeat_interleave``).  d_v defaults to the whole row (K = V).  Tiny shapes only:
+    an independent check of ``sparse_attention_grouped``.
+    """
+    qf = q.to(torch.float64)
+    kvf = kv.to(torch.float64)
+    B, S, H, D = q.shape
+    Skv, G = kv.shape[1], kv.shape[2]
+    Hg = H // G
+    d_v = D if d_v is None else d_v
+    if q_start_index_s is None:
+        q_start_index_s = Skv - S
+    if sm_scale is None:
+        sm_scale = D ** -0.5
+    idx = indices.reshape(B, S, G, -1).long().transpose(1, 2)  # [B, G, S, topk]
+    safe = torch.where(idx < 0, torch.full_like(idx, Skv), idx)
+    mask = torch.zeros(B, G, S, Skv + 1, dtype=torch.bool).scatter(3, safe, True)[..., :Skv]
+    causal = torch.arange(q_start_index_s, q_start_index_s + S).view(-1, 1) >= torch.arange(Skv).view(1, -1)
+    mask &= causal.view(1, 1, S, Skv)
+    score = torch.einsum("bqghd,bkgd->bghqk", qf.view(B, S, G, Hg, D), kvf)
+    score = score.masked_fill(~mask.view(B, G, 1, S, Skv), float("-inf")) * sm_scale
+    p = torch.nan_to_num(score.softmax(dim=-1), nan=0.0).reshape(B, H, S, Skv)
+    v = kvf[..., :d_v].repeat_interleave(Hg, dim=2)  # [B, Skv, H, d_v]
+    return torch.einsum("bhqs,bshd->bqhd", p, v).to(torch.float32)
 
 
 # ----------------------------------------------------------------------------

@@ -40,7 +40,7 @@ def test_binding_signatures_cover_the_header(dsa):
 
 def test_abi_rejects_bad_arguments_without_launching(dsa):
     lib = dsa.load_library()
-    assert lib.dsa_abi_version() == 105
+    assert lib.dsa_abi_version() == 106
     # k out of range
     assert lib.dsa_topk_select(None, 8, 1, 8, 0, None, 1, None, None, None) == 1
     assert b"k must be" in lib.dsa_last_error_message()
@@ -69,6 +69,32 @@ def test_python_layer_refuses_cpu_tensors(dsa):
     idx = torch.zeros(1, 2, 1, 4, dtype=torch.int32)
     with pytest.raises(ValueError, match="HIP"):
         dsa.sparse_mla_fwd(q, kv, idx)
+
+
+def test_grouped_sparse_attention_host_logic(dsa):
+    """dsa_sparse_attention_fwd: workspace sizes and argument checks (host only)."""
+    lib = dsa.load_library()
+    # kv_group 1 asks for what dsa_sparse_mla_fwd asks for; G groups of H / G heads for the
+    # split partials of B * S * G rows; the 128-wide kernel needs none.
+    for B, S, H, k in ((1, 1, 128, 2048), (2, 64, 128, 2048), (1, 4, 16, 512)):
+        assert (lib.dsa_sparse_attention_workspace_size(B, S, H, 1, 576, k)
+                == lib.dsa_sparse_mla_workspace_size(B, S, H, k))
+    assert (lib.dsa_sparse_attention_workspace_size(1, 1, 128, 2, 576, 2048)
+            == lib.dsa_sparse_mla_workspace_size(1, 2, 64, 2048))
+    assert lib.dsa_sparse_attention_workspace_size(2, 273, 64, 4, 128, 2048) == 0
+    assert lib.dsa_sparse_attention_workspace_size(1, 1, 100, 3, 576, 2048) == 0  # H % G != 0
+
+    def call(H, G, d_qk, d_v, topk=2048, bt=None, Skv=4096, kind=1):
+        return lib.dsa_sparse_attention_fwd(kind, 8, 8, 8, bt, None, None, 1, 1, H, G, d_qk, d_v, Skv, 64, 4, topk,
+                                            1.0, 1, 8, 8, None, 0, None)
+
+    assert call(64, 3, 128, 128) == 1 and b"multiple of kv_group" in lib.dsa_last_error_message()
+    assert call(96, 4, 576, 512) == 1 and b"multiple of 16" in lib.dsa_last_error_message()
+    assert call(64, 4, 128, 128, topk=8193) == 1 and b"8192" in lib.dsa_last_error_message()
+    assert call(64, 4, 128, 128, bt=8) == 1 and b"block table" in lib.dsa_last_error_message()
+    assert call(64, 4, 256, 256) == 1 and b"(576, 512) or (128, 128)" in lib.dsa_last_error_message()
+    assert call(64, 4, 128, 128, Skv=1 << 29) == 1 and b"2^31" in lib.dsa_last_error_message()
+    assert call(64, 4, 128, 128, kind=3) == 1 and b"kind" in lib.dsa_last_error_message()
 
 
 def test_python_layer_validation_messages(dsa):

@@ -521,3 +521,62 @@ def test_act_quant_fp8_grid():
     # 1.1875 is the midpoint of 1.125 and 1.25 (001 / 010): even -> 1.25;
     # 2^-9 is the smallest subnormal; 1.5 * 2^-9 is a midpoint -> 2 * 2^-9 (even).
     assert got == [448.0, 1.0, 1.125, 1.0, 1.25, -3.5, 0.001953125, 0.00390625]
+
+
+# --------------------------------------------------------------------------- KV groups
+def _gqa_inputs(B=2, S=5, Skv=23, G=3, Hg=2, D=16, topk=7, seed=11):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, S, G * Hg, D, generator=g)
+    kv = torch.randn(B, Skv, G, D, generator=g)
+    idx = torch.full((B, S, G, topk), -1, dtype=torch.int32)
+    for b in range(B):
+        for t in range(S):
+            for k in range(G):
+                # Some slots past the causal bound (Skv - S + t) and some -1 padding.
+                n = int(torch.randint(1, topk + 1, (1,), generator=g))
+                sel = torch.randperm(Skv, generator=g)[:n]
+                idx[b, t, k, :n] = sel.to(torch.int32)
+    return q, kv, idx
+
+
+@pytest.mark.parametrize("D,d_v", [(16, 16), (24, 16)])
+def test_grouped_gather_equals_dense_gqa_golden(D, d_v):
+    q, kv, idx = _gqa_inputs(D=D)
+    out, _ = ref.sparse_attention_grouped(q, kv, idx, d_v=d_v)
+    dense = ref.sparse_gqa_dense_ref(q, kv, idx, d_v=d_v)
+    torch.testing.assert_close(out, dense, rtol=1e-5, atol=1e-5)
+    # A head-to-group map by interleaving (h % G) instead of blocks would differ.
+    perm = torch.arange(q.shape[2]).view(2, 3).t().reshape(-1)
+    wrong, _ = ref.sparse_attention_grouped(q[:, :, perm], kv, idx, d_v=d_v)
+    assert (wrong[:, :, perm.argsort()] - dense).abs().max() > 1e-2
+
+
+def test_grouped_one_group_equals_sparse_mla_fwd():
+    q, kv, idx = _mla_inputs()
+    out_g, lse_g = ref.sparse_attention_grouped(q, kv, idx, d_v=512)
+    out, lse = ref.sparse_mla_fwd(q, kv, idx)
+    torch.testing.assert_close(out_g, out, rtol=0, atol=0)
+    torch.testing.assert_close(lse_g, lse, rtol=0, atol=0)
+
+
+def test_grouped_permuting_groups_permutes_outputs():
+    q, kv, idx = _gqa_inputs()
+    out, lse = ref.sparse_attention_grouped(q, kv, idx, d_v=16)
+    gp = torch.tensor([2, 0, 1])
+    hp = torch.cat([torch.arange(2) + 2 * int(k) for k in gp])
+    out_p, lse_p = ref.sparse_attention_grouped(q[:, :, hp], kv[:, :, gp], idx[:, :, gp], d_v=16)
+    torch.testing.assert_close(out_p, out[:, :, hp], rtol=0, atol=0)
+    torch.testing.assert_close(lse_p, lse[:, :, hp], rtol=0, atol=0)
+
+
+def test_grouped_single_index_per_group_closed_form():
+    q, kv, _ = _gqa_inputs(B=1, S=1)
+    idx = torch.full((1, 1, 3, 7), -1, dtype=torch.int32)
+    picks = [4, 9, 17]
+    for k, j in enumerate(picks):
+        idx[0, 0, k, 5] = j
+    out, lse = ref.sparse_attention_grouped(q, kv, idx, d_v=16)
+    for k, j in enumerate(picks):
+        torch.testing.assert_close(out[0, 0, 2 * k:2 * k + 2], kv[0, j, k].expand(2, 16), rtol=1e-6, atol=1e-6)
+        want = (q[0, 0, 2 * k:2 * k + 2].double() @ kv[0, j, k].double()) / 4.0
+        torch.testing.assert_close(lse[0, 0, 2 * k:2 * k + 2].double(), want, rtol=1e-6, atol=1e-6)

@@ -10,7 +10,7 @@ from ._lib import DSAError, library_path, load_library, load_torch_ops
 from .act_quant import act_quant
 from .lightning_indexer import indexer, indexer_logits, lightning_indexer
 from .sparse_flash_mla import sparse_attn, sparse_attn_kernel, sparse_flash_mla
-from .sparse_mla import sparse_attention_fwd, sparse_attn_tilelang, sparse_mla_fwd
+from .sparse_mla import sparse_attention_fwd, sparse_attn_tilelang, sparse_gqa_fwd, sparse_mla_fwd
 from .topk_selector import simple_topk_selector, topk_selector
 
 __all__ = [
@@ -28,6 +28,7 @@ __all__ = [
     "sparse_attn_kernel",
     "sparse_attn_tilelang",
     "sparse_flash_mla",
+    "sparse_gqa_fwd",
     "sparse_mla_fwd",
     "topk_selector",
 ]

@@ -75,6 +75,10 @@ SIGNATURES = {
     "dsa_sparse_mla_fwd_noalloc": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
                                             _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_float, _c_int, _c_vp,
                                             _c_vp, _c_vp]),
+    "dsa_sparse_attention_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
+    "dsa_sparse_attention_fwd": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
+                                          _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_float, _c_int,
+                                          _c_vp, _c_vp, _c_vp, _c_size, _c_vp]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

@@ -24,9 +24,14 @@ hipError_t launch_indexer_logits(int kind, const void* q, const void* k, const f
                                  const int32_t* block_table, int64_t block_size, int64_t max_blocks, int sparse_mode,
                                  float* logits, int64_t ld, hipStream_t stream);
 hipError_t launch_sparse_mla(int is_fp16, const void* q, const void* kv, const int32_t* indices, const int32_t* block_table,
-                             const int32_t* q_len, const int32_t* kv_len, int64_t B, int64_t S, int64_t H,
+                             const int32_t* q_len, const int32_t* kv_len, int64_t B, int64_t S, int64_t G, int64_t H,
                              int64_t Skv, int64_t block_size, int64_t max_blocks, int64_t topk, float sm_scale,
                              int causal, void* out, float* lse, void* workspace, hipStream_t stream);
+int64_t sparse_gqa_max_topk();
+hipError_t launch_sparse_gqa(int is_fp16, const void* q, const void* kv, const int32_t* indices,
+                             const int32_t* q_len, const int32_t* kv_len, int64_t B, int64_t S, int64_t G, int64_t Hg,
+                             int64_t Skv, int64_t topk, float sm_scale, int causal, void* out, float* lse,
+                             hipStream_t stream);
 size_t sparse_mla_workspace_bytes(int64_t tokens, int64_t H, int64_t topk);
 size_t mla_scratch_bytes();
 hipError_t mla_scratch_ptr(void** out);
@@ -67,7 +72,7 @@ constexpr int64_t dsa_kSrc2Limit = 0x40000000;
 
 extern "C" {
 
-int dsa_abi_version(void) { return 105; }
+int dsa_abi_version(void) { return 106; }
 
 const char* dsa_last_error_message(void) { return g_msg; }
 
@@ -328,9 +333,61 @@ int dsa_sparse_mla_fwd(int kind, const void* q, const void* kv, const int32_t* i
   if (workspace_bytes < dsa_sparse_mla_workspace_size(B, S, H, topk)) return reject("sparse_mla: workspace too small");
   if (B * S > 0 && (!q || !kv || !indices || !out || !lse)) return reject("sparse_mla: null pointer");
   const int64_t skv_eff = block_table ? block_size * max_blocks : Skv;
-  return ok(dsa::launch_sparse_mla(kind == DSA_KIND_FP16, q, kv, indices, block_table, actual_q_len, actual_kv_len, B, S, H, skv_eff,
-                                   block_size, max_blocks, topk, sm_scale, is_causal ? 1 : 0, out, lse, workspace,
-                                   static_cast<hipStream_t>(stream)));
+  return ok(dsa::launch_sparse_mla(kind == DSA_KIND_FP16, q, kv, indices, block_table, actual_q_len, actual_kv_len, B, S, 1, H,
+                                   skv_eff, block_size, max_blocks, topk, sm_scale, is_causal ? 1 : 0, out, lse,
+                                   workspace, static_cast<hipStream_t>(stream)));
+}
+
+size_t dsa_sparse_attention_workspace_size(int64_t B, int64_t S, int64_t H, int64_t kv_group, int64_t d_qk,
+                                           int64_t topk) {
+  if (B <= 0 || S <= 0 || H <= 0 || topk <= 0 || kv_group <= 0 || H % kv_group != 0) return 0;
+  if (d_qk != 576) return 0;  // the 128-wide kernel needs no workspace
+  return dsa::sparse_mla_workspace_bytes(B * S * kv_group, H / kv_group, topk);
+}
+
+int dsa_sparse_attention_fwd(int kind, const void* q, const void* kv, const int32_t* indices,
+                             const int32_t* block_table, const int32_t* actual_q_len, const int32_t* actual_kv_len,
+                             int64_t B, int64_t S, int64_t H, int64_t kv_group, int64_t d_qk, int64_t d_v, int64_t Skv,
+                             int64_t block_size, int64_t max_blocks, int64_t topk, float sm_scale, int is_causal,
+                             void* out, float* lse, void* workspace, size_t workspace_bytes, void* stream) {
+  if (kind != DSA_KIND_BF16 && kind != DSA_KIND_FP16) return reject("sparse_attention: kind must be bf16 or fp16");
+  if (kv_group < 1 || H < 1 || H % kv_group != 0)
+    return reject("sparse_attention: H must be a positive multiple of kv_group >= 1");
+  const int64_t Hg = H / kv_group;
+  if (B < 0 || S < 0 || topk < 1 || B * S > kMaxInt / kv_group || topk > kMaxInt)
+    return reject("sparse_attention: bad sizes");
+  if (!(sm_scale > 0.f) || !(sm_scale < 3.0e38f))
+    return reject("sparse_attention: sm_scale must be positive and finite");
+  const bool mla = d_qk == 576 && d_v == 512;
+  if (mla) {
+    if (Hg % 16 != 0 || Hg > 1024)
+      return reject("sparse_attention: heads per KV group must be a multiple of 16 in [16, 1024] (d_qk 576)");
+    if (block_table) {
+      if (block_size <= 0 || max_blocks <= 0 || block_size * max_blocks > kMaxInt)
+        return reject("sparse_attention: paged kv needs block_size > 0 and max_blocks > 0");
+    } else if (Skv < 0 || B * Skv > kMaxInt / kv_group) {
+      return reject("sparse_attention: B x Skv x kv_group must stay below 2^31");
+    }
+  } else if (d_qk == 128 && d_v == 128) {
+    if (block_table) return reject("sparse_attention: d_qk 128 takes a contiguous kv (no block table)");
+    if (Hg > 1024) return reject("sparse_attention: at most 1024 heads per KV group");
+    if (topk > dsa::sparse_gqa_max_topk()) return reject("sparse_attention: topk must be <= 8192 (d_qk 128)");
+    if (Skv < 0 || B * Skv > kMaxInt / kv_group) return reject("sparse_attention: B x Skv x kv_group must stay below 2^31");
+  } else {
+    return reject("sparse_attention: (d_qk, d_v) must be (576, 512) or (128, 128)");
+  }
+  if (workspace_bytes < dsa_sparse_attention_workspace_size(B, S, H, kv_group, d_qk, topk))
+    return reject("sparse_attention: workspace too small");
+  if (B * S > 0 && (!q || !kv || !indices || !out || !lse)) return reject("sparse_attention: null pointer");
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (mla) {
+    const int64_t skv_eff = block_table ? block_size * max_blocks : Skv;
+    return ok(dsa::launch_sparse_mla(kind == DSA_KIND_FP16, q, kv, indices, block_table, actual_q_len, actual_kv_len, B,
+                                     S, kv_group, Hg, skv_eff, block_size, max_blocks, topk, sm_scale,
+                                     is_causal ? 1 : 0, out, lse, workspace, st));
+  }
+  return ok(dsa::launch_sparse_gqa(kind == DSA_KIND_FP16, q, kv, indices, actual_q_len, actual_kv_len, B, S, kv_group,
+                                   Hg, Skv, topk, sm_scale, is_causal ? 1 : 0, out, lse, st));
 }
 
 size_t dsa_sparse_mla_noalloc_max_workspace(void) { return dsa::mla_scratch_bytes(); }

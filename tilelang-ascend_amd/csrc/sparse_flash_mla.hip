@@ -210,7 +210,9 @@ struct DecArgs {
     const int32_t* block_table;  // [B, max_blocks] or null
     const int32_t* q_len;        // [B] or null (S)
     const int32_t* kv_len;       // [B] or null (Skv)
-    int S, Skv, block_size, max_blocks, causal;
+    // KV groups: row t = (b * S + s) * G + g reads KV column g, physical row
+    // (pool row) * G + g.
+    int S, G, Skv, block_size, max_blocks, causal;
   } mla;
 };
 
@@ -326,13 +328,15 @@ __global__ __launch_bounds__(256) void v4_decode_rows_kernel(DecArgs a) {
   for (int st = 0; st < kSteps; ++st) qb[st] = *reinterpret_cast<const u32x4*>(qp + 32 * st);
   int cnt_raw, vb = 0, vnw = 0, vw0 = 0, thr = 0, nread = 0;
   const V4Args& v = a.v4;
-  int mb = 0, mkl = 0, mlim = 0;  // kMode 4: batch, kv length, causal bound of the row
+  int mb = 0, mg = 0, mkl = 0, mlim = 0;  // kMode 4: batch, KV group, kv length, causal bound of the row
   if constexpr (kMode == 4) {
     // A row past its batch's query length has no valid slot (out 0, lse -inf, as
     // the gather kernel gives it); a slot is valid iff 0 <= idx < kv_len and, when
     // causal, idx <= kv_len - q_len + s.
-    mb = t / a.mla.S;
-    const int sq = t - mb * a.mla.S;
+    const int bs_row = t / a.mla.G;
+    mg = t - bs_row * a.mla.G;
+    mb = bs_row / a.mla.S;
+    const int sq = bs_row - mb * a.mla.S;
     const int ql = min(max(a.mla.q_len ? a.mla.q_len[mb] : a.mla.S, 0), a.mla.S);
     mkl = min(max(a.mla.kv_len ? a.mla.kv_len[mb] : a.mla.Skv, 0), a.mla.Skv);
     mlim = a.mla.causal ? mkl - ql + sq : 0x7fffffff;
@@ -403,9 +407,9 @@ __global__ __launch_bounds__(256) void v4_decode_rows_kernel(DecArgs a) {
       const bool ok = idx >= 0 && idx < mkl && idx <= mlim;
       if (a.mla.block_table) {
         const int blk = a.mla.block_table[(int64_t)mb * a.mla.max_blocks + (ok ? idx / a.mla.block_size : 0)];
-        return ok ? blk * a.mla.block_size + idx % a.mla.block_size : -1;
+        return ok ? (blk * a.mla.block_size + idx % a.mla.block_size) * a.mla.G + mg : -1;
       }
-      return ok ? mb * a.mla.Skv + idx : -1;
+      return ok ? (mb * a.mla.Skv + idx) * a.mla.G + mg : -1;
     } else {
       // Window position vw0 + i, then compressed entry i - vnw: the lookups of both
       // go out (from clamped entries) and the slot picks one.
@@ -879,23 +883,25 @@ size_t mla_decode_part_bytes(int64_t T, int64_t H, int64_t topk) {
   return (size_t)T * H * dec_splits(topk) * kDecPart * sizeof(float);
 }
 
-// Caller: mla_decode_applies(B * S, H, topk), H % 16 == 0, workspace >= mla_decode_part_bytes.
+// Caller: mla_decode_applies(B * S * G, H, topk), H (heads per KV group) % 16 == 0,
+// workspace >= mla_decode_part_bytes.
 hipError_t launch_mla_decode_rows(int is_fp16, const void* q, const void* kv, const int32_t* indices,
                                   const int32_t* block_table, const int32_t* q_len, const int32_t* kv_len, int64_t B,
-                                  int64_t S, int64_t H, int64_t Skv, int64_t block_size, int64_t max_blocks,
-                                  int64_t topk, float sm_scale, int causal, void* out, float* lse, void* workspace,
-                                  hipStream_t stream) {
+                                  int64_t S, int64_t G, int64_t H, int64_t Skv, int64_t block_size,
+                                  int64_t max_blocks, int64_t topk, float sm_scale, int causal, void* out, float* lse,
+                                  void* workspace, hipStream_t stream) {
   DecArgs a = {};
   a.mla.idx = indices;
   a.mla.block_table = block_table;
   a.mla.q_len = q_len;
   a.mla.kv_len = kv_len;
   a.mla.S = (int)S;
+  a.mla.G = (int)G;
   a.mla.Skv = (int)Skv;
   a.mla.block_size = (int)block_size;
   a.mla.max_blocks = (int)max_blocks;
   a.mla.causal = causal;
-  return dec_run(is_fp16, 4, a, q, kv, nullptr, B * S, H, topk, nullptr, sm_scale, out, lse, workspace, stream);
+  return dec_run(is_fp16, 4, a, q, kv, nullptr, B * S * G, H, topk, nullptr, sm_scale, out, lse, workspace, stream);
 }
 
 static size_t v4_lists_bytes(int64_t T, int64_t cap) {

@@ -102,6 +102,10 @@ struct MlaArgs {
   float* out32;               // [B, S, H, 512] or null
   float* part_o32;            // [splits, B*S, H, 512] (splits > 1, out32 set)
   int B, S, H, Skv, topk;
+  // KV groups (kv_group): query row t = (b * S + s) * G + g reads KV column g
+  // through its own index row, heads g * H .. (g + 1) * H - 1 of the caller's q
+  // (H here is the heads per group); its physical rows are (pool row) * G + g.
+  int G;
   int block_size, max_blocks;
   int causal;
   int splits, keys_per_split;
@@ -609,11 +613,13 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   const int r = lane & 15;
   const int g = lane >> 4;
 
-  const int T = a.B * a.S;
+  const int T = a.B * a.S * a.G;
   const int token = blockIdx.x % T;
   const int split = blockIdx.x / T;
-  const int b = token / a.S;
-  const int s = token % a.S;
+  const int bs_row = token / a.G;  // b * S + s
+  const int kvg = token - bs_row * a.G;
+  const int b = bs_row / a.S;
+  const int s = bs_row % a.S;
   // A wave owns two 16-head blocks: heads head0 + 16*hb + r.
   const int head0 = blockIdx.y * (kNW * kHeadsPerWave) + wave * kHeadsPerWave;
   bool hb_on[2];
@@ -693,10 +699,11 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
     __asm__ __volatile__("" ::: "memory");
     load_q();
 #pragma unroll
-    for (int j = 0; j < kIdxPerLane; ++j) row_of[j] = ok[j] ? blk[j] * a.block_size + idx_raw[j] % a.block_size : -1;
+    for (int j = 0; j < kIdxPerLane; ++j)
+      row_of[j] = ok[j] ? (blk[j] * a.block_size + idx_raw[j] % a.block_size) * a.G + kvg : -1;
   } else {
 #pragma unroll
-    for (int j = 0; j < kIdxPerLane; ++j) row_of[j] = ok[j] ? b * a.Skv + idx_raw[j] : -1;
+    for (int j = 0; j < kIdxPerLane; ++j) row_of[j] = ok[j] ? (b * a.Skv + idx_raw[j]) * a.G + kvg : -1;
   }
 #pragma unroll
   for (int j = 0; j < kIdxPerLane; ++j) __asm__ __volatile__("" : "+v"(row_of[j]));
@@ -1160,9 +1167,9 @@ bool mla_decode_applies(int64_t T, int64_t H, int64_t topk);
 size_t mla_decode_part_bytes(int64_t T, int64_t H, int64_t topk);
 hipError_t launch_mla_decode_rows(int is_fp16, const void* q, const void* kv, const int32_t* indices,
                                   const int32_t* block_table, const int32_t* q_len, const int32_t* kv_len, int64_t B,
-                                  int64_t S, int64_t H, int64_t Skv, int64_t block_size, int64_t max_blocks,
-                                  int64_t topk, float sm_scale, int causal, void* out, float* lse, void* workspace,
-                                  hipStream_t stream);
+                                  int64_t S, int64_t G, int64_t H, int64_t Skv, int64_t block_size,
+                                  int64_t max_blocks, int64_t topk, float sm_scale, int causal, void* out, float* lse,
+                                  void* workspace, hipStream_t stream);
 
 // Workspace of launch_sparse_mla: decode rows take the decode kernel's partials.
 size_t sparse_mla_workspace_bytes(int64_t tokens, int64_t H, int64_t topk) {
@@ -1204,7 +1211,7 @@ static hipError_t launch_mla_kernel(const MlaArgs& a, int head_groups, hipStream
   constexpr int kLds = MlaGeom<kD>::kLds;
   const hipError_t ea = set_dynamic_lds_once<sparse_mla_kernel<kNW, kF16, kD, kPaged>>(kLds);
   if (ea != hipSuccess) return ea;
-  const dim3 grid((unsigned)((int64_t)a.B * a.S * a.splits), (unsigned)head_groups);
+  const dim3 grid((unsigned)((int64_t)a.B * a.S * a.G * a.splits), (unsigned)head_groups);
   hipLaunchKernelGGL((sparse_mla_kernel<kNW, kF16, kD, kPaged>), grid, dim3(kNW * kWave), kLds, stream, a);
   return hipGetLastError();
 }
@@ -1225,7 +1232,7 @@ static hipError_t launch_mla_dtype(const MlaArgs& a, int head_groups, int hpg, h
   else if (hpg > 32) e = launch_mla_nw<2, kF16, kD>(a, head_groups, stream);
   else e = launch_mla_nw<1, kF16, kD>(a, head_groups, stream);
   if (e != hipSuccess || a.splits == 1) return e;
-  const int64_t rows = (int64_t)a.B * a.S * a.H;
+  const int64_t rows = (int64_t)a.B * a.S * a.G * a.H;
   const int64_t threads = rows * (kMlaDV / 8);
   const dim3 grid((unsigned)((threads + 255) / 256));
   if (a.out32)
@@ -1253,17 +1260,18 @@ static void mla_set_splits(MlaArgs& a, int64_t T, int64_t H, int64_t topk, void*
   }
 }
 
-// Caller validated: d_qk 576, d_v 512, H % 16 == 0, 16-bit inputs, workspace >= sparse_mla_workspace_bytes,
-// physical KV rows < 2^31.
+// Caller validated: d_qk 576, d_v 512, H (heads per KV group) % 16 == 0, 16-bit inputs,
+// workspace >= sparse_mla_workspace_bytes(B * S * G, H, topk), physical KV rows times G < 2^31.
 hipError_t launch_sparse_mla(int is_fp16, const void* q, const void* kv, const int32_t* indices,
                              const int32_t* block_table, const int32_t* q_len, const int32_t* kv_len, int64_t B,
-                             int64_t S, int64_t H, int64_t Skv, int64_t block_size, int64_t max_blocks, int64_t topk,
-                             float sm_scale, int causal, void* out, float* lse, void* workspace, hipStream_t stream) {
-  const int64_t T = B * S;
+                             int64_t S, int64_t G, int64_t H, int64_t Skv, int64_t block_size, int64_t max_blocks,
+                             int64_t topk, float sm_scale, int causal, void* out, float* lse, void* workspace,
+                             hipStream_t stream) {
+  const int64_t T = B * S * G;
   if (T == 0 || H == 0) return hipSuccess;
   // Few query rows (decode): the decode kernel, slots across waves and chunks.
   if (mla_decode_applies(T, H, topk))
-    return launch_mla_decode_rows(is_fp16, q, kv, indices, block_table, q_len, kv_len, B, S, H, Skv, block_size,
+    return launch_mla_decode_rows(is_fp16, q, kv, indices, block_table, q_len, kv_len, B, S, G, H, Skv, block_size,
                                   max_blocks, topk, sm_scale, causal, out, lse, workspace, stream);
   MlaArgs a;
   a.q = static_cast<const uint16_t*>(q);
@@ -1283,6 +1291,7 @@ hipError_t launch_sparse_mla(int is_fp16, const void* q, const void* kv, const i
   a.H = (int)H;
   a.Skv = (int)Skv;
   a.topk = (int)topk;
+  a.G = (int)G;
   a.block_size = (int)block_size;
   a.max_blocks = (int)max_blocks;
   a.causal = causal;
@@ -1322,6 +1331,7 @@ hipError_t launch_sparse_mla_rows(int is_fp16, const void* q, const void* kv, co
   a.H = (int)H;
   a.Skv = 0x7fffffff;
   a.topk = (int)cap;
+  a.G = 1;
   a.block_size = 0;
   a.max_blocks = 0;
   a.causal = 0;
