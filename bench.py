@@ -573,6 +573,48 @@ def run_v4(torch, pkg, dev, args, flush, H=64, D=512, bs=128, K=512, win=127):
 SFA_REFERENCE_US = {2560: (109.760, 98.0), 6400: (109.100, 99.0), 48000: (108.980, 100.0)}
 
 
+def run_gqa(torch, pkg, dev, args, flush):
+    """The grouped 128-wide sparse attention at the shape of the reference's GQA example
+    (examples/sparse_flash_attention/example_sparse_flash_attn_gqa.py:266-318): B=2, S=273,
+    SKV=44444, 64 query heads over 4 KV heads, D=128 (K = V), topk 2048, fp16; every row draws
+    2048 distinct positions below q_start = 28672.  No published figure: reported for its own
+    bounds (the gathered rows, the unique HBM bytes, the MFMA work)."""
+    from tilelang_ascend_amd import _lib as L
+    lib = pkg.load_library()
+    B, S, SKV, H, G, D, K, q_start = 2, 273, 44444, 64, 4, 128, 2048, 4096 * 7
+    g = torch.Generator(device=dev).manual_seed(20261207)
+    q = torch.randn((B, S, H, D), device=dev, generator=g).to(torch.float16)
+    kv = torch.randn((B, SKV, G, D), device=dev, generator=g).to(torch.float16)
+    idx = torch.rand((B * S * G, q_start), device=dev, generator=g).argsort(dim=1)[:, :K]
+    idx = idx.to(torch.int32).view(B, S, G, K).contiguous()
+    out = torch.empty((B, S, H, D), dtype=torch.float16, device=dev)
+    lse = torch.empty((B, S, H), dtype=torch.float32, device=dev)
+    stream = L.stream_handle(dev)
+
+    def call():
+        rc = lib.dsa_sparse_attention_fwd(L.KIND_FP16, q.data_ptr(), kv.data_ptr(), idx.data_ptr(), None, None, None,
+                                          B, S, H, G, D, D, SKV, 0, 0, K, D ** -0.5, 1, out.data_ptr(),
+                                          lse.data_ptr(), None, 0, stream)
+        L.check(rc, "grouped sparse attention")
+
+    call()
+    torch.cuda.synchronize()
+    t = _median(_timed(torch, call, args.reps, flush))
+    gathered = B * S * G * K * D * 2
+    unique = kv.numel() * 2 + q.numel() * 2 + out.numel() * 2 + lse.numel() * 4 + idx.numel() * 4
+    flops = 4.0 * B * S * H * K * D
+    res = {"workload": "GQA example shape: B=2, S=273, SKV=44444, H=64 over kv_group=4, D=128, topk=2048, fp16",
+           "us": round(t * 1e3, 1),
+           "gathered_bytes": gathered,
+           "gather_gbs": round(gathered / (t * 1e-3) / 1e9, 1),
+           "unique_hbm_bytes": unique,
+           "hbm_floor_us": round(unique / (PEAK_HBM_GBS * 1e9) * 1e6, 1),
+           "tflops": round(flops / (t * 1e-3) / 1e12, 1)}
+    _log(f"GQA example shape: {t * 1e3:.1f} us, gathered rows {res['gather_gbs']:.0f} GB/s")
+    del q, kv, idx, out, lse
+    return res
+
+
 def run_sfa_reference_shapes(torch, pkg, dev):
     """The reference's SFA decode benchmark (bench_sfa.py:9-70, :104-140): T=1, B=1, 128 heads,
     D=512 + 64 rope (one 576-wide latent row, V = its first 512), 2048 distinct indices drawn from
@@ -737,7 +779,7 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--reps", type=int, default=20, help="repetitions of the secondary (flushed) benchmarks")
-    ap.add_argument("--skip", default="", help="comma list of parts to skip: step,indexer,decode,c5,v4,sfa,cpu")
+    ap.add_argument("--skip", default="", help="comma list of parts to skip: step,indexer,decode,c5,v4,gqa,sfa,cpu")
     ap.add_argument("--only", default="", help="comma list of the only parts to run (the complement of --skip)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy (HBM byte-counter calibration for rocprof)")
@@ -747,7 +789,7 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     skip = set(filter(None, args.skip.split(",")))
-    parts = {"step", "indexer", "decode", "c5", "v4", "sfa", "cpu"}
+    parts = {"step", "indexer", "decode", "c5", "v4", "gqa", "sfa", "cpu"}
     if args.only:
         skip |= parts - set(filter(None, args.only.split(",")))
 
@@ -905,6 +947,10 @@ def main():
     # ---------------- V4 sparse flash MLA at the reference benchmark's shapes ----------------
     if "v4" not in skip:
         result["v4_sparse_flash_mla"] = run_v4(torch, pkg, dev, args, flush)
+
+    # ---------------- the grouped 128-wide kernel at the reference's GQA example shape ----------------
+    if "gqa" not in skip:
+        result["gqa_example_shape"] = run_gqa(torch, pkg, dev, args, flush)
 
     # ---------------- the reference's own SFA decode benchmark shapes ----------------
     if "sfa" not in skip:

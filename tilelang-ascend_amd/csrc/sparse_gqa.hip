@@ -31,8 +31,6 @@
 
 namespace dsa {
 
-namespace {
-
 constexpr int kGqaD = 128;
 constexpr int kGqaRowBytes = kGqaD * 2;                 // 256
 constexpr int kGqaTile = 32;                            // slots per tile
@@ -425,7 +423,7 @@ __global__ __launch_bounds__(kGqaThreads, 2) void sparse_gqa_kernel(GqaArgs a) {
 }
 
 template <bool kF16, int kHB, int kStg>
-hipError_t gqa_launch(const GqaArgs& a, hipStream_t stream) {
+static hipError_t gqa_launch(const GqaArgs& a, hipStream_t stream) {
   constexpr int kMaxLds = gqa_lds_bytes(kStg, kHB, kGqaMaxTiles);
   static_assert(kMaxLds <= 160 * 1024, "LDS");
   const hipError_t e = set_dynamic_lds_once<sparse_gqa_kernel<kF16, kHB, kStg>>(kMaxLds);
@@ -436,8 +434,6 @@ hipError_t gqa_launch(const GqaArgs& a, hipStream_t stream) {
                      gqa_lds_bytes(kStg, kHB, ntiles), stream, a);
   return hipGetLastError();
 }
-
-}  // namespace
 
 int64_t sparse_gqa_max_topk() { return kGqaMaxTopk; }
 
