@@ -1,7 +1,7 @@
 """Static check: every explicit LDS wait in the gather and decode kernels covers the reads it guards.
 
-csrc/sparse_mla.hip and csrc/sparse_flash_mla.hip issue their LDS operand reads as inline asm and
-wait for them with counted ``s_waitcnt lgkmcnt(N)``.  This test compiles both files to gfx950
+csrc/sparse_mla.hip, csrc/sparse_flash_mla.hip and csrc/sparse_gqa.hip issue their LDS operand reads
+as inline asm and wait for them with counted ``s_waitcnt lgkmcnt(N)``.  This test compiles the files to gfx950
 assembly with the library's own flags and replays the LDS counter through each kernel's control
 flow (tests/asm_lds.py): no instruction may touch a register whose LDS load may still be in
 flight.  The planted case below shows the check sees an off-by-eight count.
@@ -35,10 +35,10 @@ def _asm(tmp_path_factory, name: str) -> str:
     return out.read_text()
 
 
-@pytest.mark.parametrize("name", ["sparse_flash_mla.hip", "sparse_mla.hip"])
-def test_lds_waits_cover_their_reads(tmp_path_factory, name):
+@pytest.mark.parametrize("name,nkernels", [("sparse_flash_mla.hip", 6), ("sparse_mla.hip", 6), ("sparse_gqa.hip", 4)])
+def test_lds_waits_cover_their_reads(tmp_path_factory, name, nkernels):
     kernels, findings = asm_lds.check_asm(_asm(tmp_path_factory, name))
-    assert len(kernels) >= 6, kernels
+    assert len(kernels) >= nkernels, kernels
     assert not findings, "\n".join(map(str, findings[:20]))
 
 
