@@ -177,3 +177,16 @@ def test_mla_kv_groups_paged_and_builder(dsa, dev):
     kern = dsa.sparse_attention_fwd(heads=G * Hg, dim=512, tail_dim=64, topk=topk, kv_stride=1, kv_group=G)
     out = kern(q.to(dev), kv.to(dev), idx.to(dev))
     torch.testing.assert_close(out.float().cpu(), ro, atol=2e-2, rtol=2e-2)
+
+
+def test_mla_kv_groups_split_combine(dsa, dev):
+    """kv_group 2 on 8 decode rows: 16 (row, group) pairs of 64 heads over topk 2048 take the gather
+    kernel with split index lists and the combine (a workspace is needed), against the oracle."""
+    B, S, Skv, G, Hg, topk = 8, 1, 8192, 2, 64, 2048
+    lib = dsa.load_library()
+    assert lib.dsa_sparse_attention_workspace_size(B, S, G * Hg, G, 576, topk) > 0
+    q, kv, idx = _mla_group_inputs(B, S, Skv, G, Hg, topk, seed=91)
+    _log("MLA kv_group=2 split + combine")
+    out, lse = dsa.sparse_mla_fwd(q.to(dev), kv.to(dev), idx.to(dev))
+    ro, rl = ref.sparse_attention_grouped(q, kv, idx, d_v=512)
+    _check(out, lse, ro, rl, torch.bfloat16)
