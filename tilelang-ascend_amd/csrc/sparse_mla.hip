@@ -760,16 +760,6 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   constexpr int kStageBytes = Geo::kStageBytes;
   constexpr int kDepth = Cfg::kDepth;
   constexpr int kL = Cfg::kMaxPerWave;
-  // The first min(kDepth, ntiles) tiles go out now; iteration t sends tile
-  // t + kDepth while it exists (no DMA past the last tile).
-#pragma unroll
-  for (int t = 0; t < kDepth; ++t) {
-    if (t < ntiles) {
-      TileDma<kNW, kD> dma;
-      dma.prepare(kvb, kvb2, trows, safe_row, t, lds + (t % kStages) * kStageBytes, wave, lane);
-      il_dma_all(dma);
-    }
-  }
 
   f32x4 o[2][kMlaDV / 16];
 #pragma unroll
@@ -848,9 +838,20 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   // publishes tile t+1 and certifies that every wave is done with tile t-1,
   // whose stage the DMA of tile t + kDepth then refills.
   if (ntiles > 0) {
+    // The first kDepth stages are filled now (a row of fewer tiles re-loads its
+    // last tile into the stages it does not use), unconditionally, so that the
+    // compiler sees a fixed count of loads behind Q: the wait for tile 0 then
+    // also covers Q, and no wait for every load in flight is added before the
+    // first MFMA.  Iteration t sends tile t + kDepth while it exists.
+#pragma unroll
+    for (int t = 0; t < kDepth; ++t) {
+      TileDma<kNW, kD> dma;
+      dma.prepare(kvb, kvb2, trows, safe_row, min(t, ntiles - 1), lds + (t % kStages) * kStageBytes, wave, lane);
+      il_dma_all(dma);
+    }
     u32x4 pa[2];
     {
-      wait_tiles<kL>(min(kDepth, ntiles) - 1);
+      wait_vmcnt<(kDepth - 1) * kL>();
       raw_barrier();
       f32x4 c[2][2];
       uint32_t qa[2];
