@@ -258,6 +258,10 @@ struct IdxArgs {
 };
 
 enum IdxMode : int { kModeDense = 0, kModeSample = 1, kModeFilter = 2, kModeFallback = 3 };
+
+// Scale of every key when the call has none (loaded like a real scale, so the
+// load is unconditional).
+__device__ float kIdxUnitScale[1] = {1.f};
 // kModeFallback exists at launch level only: the fused path's bounded dense
 // rounds (flag_idx set), run as indexer_fallback_kernel -- the dense body under
 // a name of its own, so that kernel traces tell them from the plain dense pass.
@@ -529,6 +533,28 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
       }
     }
   };
+  // Contiguous keys, tokens split over the waves (kUL): every load is issued
+  // whatever the tile -- rows past the valid keys re-load the last valid row
+  // (their logits are masked) and a fetch past the last tile re-loads it -- so
+  // the compiler knows how many loads follow each one and waits for exactly the
+  // data it needs.  Keys go out two tiles ahead, each tile's key scale one tile
+  // ahead (scale slot tile & 1).
+  constexpr bool kUL = !kPaged && !kSplit;
+  auto fetch_ul = [&](auto slot_c, int tile) {
+    constexpr int slot = decltype(slot_c)::value;
+    const int rl = max(tile_end - key0 - tile * tstride, 1);
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int kr = min(kr0 + i * kRowsPerLoad, rl - 1);
+      stage[slot][i] = *reinterpret_cast<const u32x4*>(a.k + (k_base + key0 + (int64_t)tile * tstride + kr) * kRB +
+                                                        (tid % (kRB / 16)) * 16);
+    }
+  };
+  auto scale_ul = [&](auto slot_c, int tile) {
+    constexpr int slot = decltype(slot_c)::value;
+    const int ss = min(key0 + tile * tstride + sc_off, tile_end - 1);
+    scl[slot] = *(a.k_scale ? a.k_scale + k_base + ss : kIdxUnitScale);
+  };
   auto commit = [&](auto slot_c, int buf) {
     constexpr int slot = decltype(slot_c)::value;
 #pragma unroll
@@ -546,14 +572,25 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
   // arrived -- after the first key tile was requested, so the two latencies
   // overlap, and before the second, which keeps fewer registers live.
   uint32_t qscale[kTokPW];
-  if (ntiles > 0) fetch(Slot0{}, 0);
+  if constexpr (kUL) {
+    if (ntiles > 0) {
+      fetch_ul(Slot0{}, 0);
+      scale_ul(Slot0{}, 0);
+    }
+  } else {
+    if (ntiles > 0) fetch(Slot0{}, 0);
+  }
 #pragma unroll
   for (int j = 0; j < kTokPW; ++j) {
     qscale[j] = 0x7f7f7f7fu;
     if constexpr (kMfmaSum) fp8_head_scales<kD, kMode == kModeSample>(qa[j], wv[j], nhb, qscale[j], wa[j], post[j]);
   }
   if (ntiles > 0) commit(Slot0{}, 0);
-  if (ntiles > 1) fetch(Slot1{}, 1);
+  if constexpr (kUL) {
+    if (ntiles > 0) fetch_ul(Slot1{}, min(1, ntiles - 1));
+  } else {
+    if (ntiles > 1) fetch(Slot1{}, 1);
+  }
   __syncthreads();
 
   // One tile of work; kSlot = tile & 1 (the loop runs two tiles per trip, so
@@ -562,9 +599,16 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
     constexpr int slot = decltype(slot_c)::value;
     const int buf = tile % 3;
     // This tile's scale: kSplit's from its slot before the fetch below reuses it;
-    // otherwise loaded now, its latency behind the tile's MFMAs.
-    const float sc_early = kSplit ? scl[slot] : load_scale(tile, 0);
-    if (tile + 2 < ntiles) fetch(slot_c, tile + 2);
+    // kUL's from its slot at the stores (loaded a tile ago); otherwise loaded
+    // now, its latency behind the tile's MFMAs.
+    float sc_early = 1.f;
+    if constexpr (kUL) {
+      fetch_ul(slot_c, min(tile + 2, ntiles - 1));
+      scale_ul(std::integral_constant<int, slot ^ 1>{}, min(tile + 1, ntiles - 1));
+    } else {
+      sc_early = kSplit ? scl[slot] : load_scale(tile, 0);
+      if (tile + 2 < ntiles) fetch(slot_c, tile + 2);
+    }
 
     float res[kTokPW];
 #pragma unroll
@@ -613,11 +657,16 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
         }
       }
     }
+    // kUL: the next tile goes to LDS before this one's stores, so that waiting
+    // for its keys never waits for stores issued after them.
+    if constexpr (kUL) {
+      if (tile + 1 < ntiles) commit(std::integral_constant<int, slot ^ 1>{}, (tile + 1) % 3);
+    }
     // Lane l now holds key (tile * tstride + l) of the chunk for each token
     // (kSplit: lane (g, r) of wave w holds key 16 w + r, and group 0 stores it).
     const int s = key0 + tile * tstride + sc_off;
     const bool storer = !kSplit || g == 0;
-    const float sc = sc_early;
+    const float sc = kUL ? scl[slot] : sc_early;
 #pragma unroll
     for (int j = 0; j < kTokPW; ++j) {
       const int t = t_base + tw + j;
@@ -642,7 +691,9 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
       }
     }
     // Buffer (tile + 1) % 3 was last read two tiles ago, before the previous barrier.
-    if (tile + 1 < ntiles) commit(std::integral_constant<int, slot ^ 1>{}, (tile + 1) % 3);
+    if constexpr (!kUL) {
+      if (tile + 1 < ntiles) commit(std::integral_constant<int, slot ^ 1>{}, (tile + 1) % 3);
+    }
     __syncthreads();
   };
   for (int tile = 0; tile < ntiles; tile += 2) {
