@@ -482,9 +482,15 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
   // tiles in the two staging slots, loaded with their keys; with paged keys a
   // fetch also takes its block ids (of this thread's key rows and of its scale
   // key) from the previous fetch, which issues them before its own key rows, so
-  // waiting for them never waits for key rows.
+  // waiting for them never waits for key rows.  Every load of a kSplit fetch is
+  // issued whatever the tile (clamped to the last valid key, as kUL below), so
+  // that the compiler can count the loads behind each one.
   float scl[2] = {1.f, 1.f};
   int bid[kLoads], sbid = 0;
+  // Key scales without a branch per load: without scales every index maps to
+  // the one unit scale.
+  const float* const ks_base = a.k_scale ? a.k_scale : kIdxUnitScale;
+  const int64_t ks_mul = a.k_scale ? 1 : 0;
   auto block_ids = [&](int tile, int (&ids)[kLoads], int& sid) {
     const int64_t tb = (int64_t)b * a.max_blocks;
     const int base = key0 + tile * tstride;
@@ -502,15 +508,26 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
   auto fetch = [&](auto slot_c, int tile) {
     constexpr int slot = decltype(slot_c)::value;
     const int rows_left = tile_end - key0 - tile * tstride;  // block-uniform
+    if constexpr (kSplit) {
+      // The scale first: a wait for it (the compiler copies these registers
+      // across the loop's back edge) then never waits for this fetch's keys.
+      const int ss = min(key0 + tile * tstride + sc_off, tile_end - 1);
+      const int64_t si = kPaged ? (int64_t)sbid * a.block_size + ss % a.block_size : k_base + ss;
+      scl[slot] = ks_base[si * ks_mul];
+    }
     int nid[kLoads], nsid = sbid;
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) nid[i] = bid[i];
-    if constexpr (kPaged && kSplit) {
-      if (tile + 1 < ntiles) block_ids(tile + 1, nid, nsid);
-    }
+    if constexpr (kPaged && kSplit) block_ids(min(tile + 1, ntiles - 1), nid, nsid);
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
       const int kr = kr0 + i * kRowsPerLoad;    // key row in tile
+      if constexpr (kSplit) {
+        const int s = key0 + tile * tstride + min(kr, max(rows_left, 1) - 1);  // a valid key
+        const int64_t rowi = kPaged ? (int64_t)bid[i] * a.block_size + s % a.block_size : k_base + s;
+        stage[slot][i] = *reinterpret_cast<const u32x4*>(a.k + rowi * kRB + (tid % (kRB / 16)) * 16);
+        continue;
+      }
       u32x4 v = {0, 0, 0, 0};
       if (kr < rows_left) {
         if constexpr (kPaged) {
@@ -525,7 +542,6 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
       stage[slot][i] = v;
     }
     if constexpr (kSplit) {
-      scl[slot] = load_scale(tile, sbid);
       if constexpr (kPaged) {
 #pragma unroll
         for (int i = 0; i < kLoads; ++i) bid[i] = nid[i];
@@ -553,7 +569,7 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
   auto scale_ul = [&](auto slot_c, int tile) {
     constexpr int slot = decltype(slot_c)::value;
     const int ss = min(key0 + tile * tstride + sc_off, tile_end - 1);
-    scl[slot] = *(a.k_scale ? a.k_scale + k_base + ss : kIdxUnitScale);
+    scl[slot] = ks_base[(k_base + ss) * ks_mul];
   };
   auto commit = [&](auto slot_c, int buf) {
     constexpr int slot = decltype(slot_c)::value;
@@ -588,6 +604,8 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
   if (ntiles > 0) commit(Slot0{}, 0);
   if constexpr (kUL) {
     if (ntiles > 0) fetch_ul(Slot1{}, min(1, ntiles - 1));
+  } else if constexpr (kSplit) {
+    if (ntiles > 0) fetch(Slot1{}, min(1, ntiles - 1));
   } else {
     if (ntiles > 1) fetch(Slot1{}, 1);
   }
@@ -605,8 +623,11 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
     if constexpr (kUL) {
       fetch_ul(slot_c, min(tile + 2, ntiles - 1));
       scale_ul(std::integral_constant<int, slot ^ 1>{}, min(tile + 1, ntiles - 1));
+    } else if constexpr (kSplit) {
+      sc_early = scl[slot];
+      fetch(slot_c, min(tile + 2, ntiles - 1));
     } else {
-      sc_early = kSplit ? scl[slot] : load_scale(tile, 0);
+      sc_early = load_scale(tile, 0);
       if (tile + 2 < ntiles) fetch(slot_c, tile + 2);
     }
 
@@ -657,9 +678,9 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
         }
       }
     }
-    // kUL: the next tile goes to LDS before this one's stores, so that waiting
-    // for its keys never waits for stores issued after them.
-    if constexpr (kUL) {
+    // kUL, kSplit: the next tile goes to LDS before this one's stores, so that
+    // waiting for its keys never waits for stores issued after them.
+    if constexpr (kUL || kSplit) {
       if (tile + 1 < ntiles) commit(std::integral_constant<int, slot ^ 1>{}, (tile + 1) % 3);
     }
     // Lane l now holds key (tile * tstride + l) of the chunk for each token
@@ -691,7 +712,7 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
       }
     }
     // Buffer (tile + 1) % 3 was last read two tiles ago, before the previous barrier.
-    if constexpr (!kUL) {
+    if constexpr (!kUL && !kSplit) {
       if (tile + 1 < ntiles) commit(std::integral_constant<int, slot ^ 1>{}, (tile + 1) % 3);
     }
     __syncthreads();
