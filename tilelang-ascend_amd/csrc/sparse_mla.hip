@@ -1046,8 +1046,10 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
 
 // Merge split partials: lse = log(sum_i exp(lse_i) [+ exp(sink)]),
 // out = sum_i exp(lse_i - lse) * o_i.  kF32: partials and out are fp32 (row
-// lists with an fp32 output), else 16-bit.
-template <bool kF16, bool kF32>
+// lists with an fp32 output), else 16-bit.  kU: splits visited at a time; with
+// at most kU splits (the launch picks kU >= splits up to 8) every LSE and
+// partial of the row is loaded at once, in one round trip.
+template <bool kF16, bool kF32, int kU>
 __global__ __launch_bounds__(256) void sparse_mla_combine_kernel(const void* __restrict__ part_o,
                                                                  const float* __restrict__ part_lse, int splits,
                                                                  int64_t rows, const float* __restrict__ sinks,
@@ -1097,8 +1099,38 @@ __global__ __launch_bounds__(256) void sparse_mla_combine_kernel(const void* __r
   // Splits are visited kU at a time, every load of a group issued before any is
   // used (a split-serial loop is a chain of load latencies); the sums keep the
   // split order.
-  constexpr int kU = kF32 ? 4 : 8;
   const float sink = sinks ? sinks[row % H] : -__builtin_huge_valf();
+  if (splits <= kU) {
+    float li[kU];
+    float v[kU][8];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int i = min(u, splits - 1);  // clamped: a real partial, unused past splits
+      li[u] = u < splits ? part_lse[(int64_t)i * rows + row] : -__builtin_huge_valf();
+      load8(i, v[u]);
+    }
+    float m1 = sink;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) m1 = fmaxf(m1, li[u]);
+    float a1[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float ws = sinks && m1 != -__builtin_huge_valf() ? __expf(sink - m1) : 0.f;
+    if (m1 != -__builtin_huge_valf()) {
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        if (li[u] == -__builtin_huge_valf()) continue;
+        const float w = __expf(li[u] - m1);
+        ws += w;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) a1[j] += w * v[u][j];
+      }
+    }
+    const float inv1 = ws > 0.f ? 1.f / ws : 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a1[j] *= inv1;
+    store8(a1);
+    if (c == 0) lse[row] = ws > 0.f ? m1 + __logf(ws) : -__builtin_huge_valf();
+    return;
+  }
   float mx = sink;
   for (int i0 = 0; i0 < splits; i0 += kU) {
     float li[kU];
@@ -1237,10 +1269,13 @@ static hipError_t launch_mla_dtype(const MlaArgs& a, int head_groups, int hpg, h
   const int64_t threads = rows * (kMlaDV / 8);
   const dim3 grid((unsigned)((threads + 255) / 256));
   if (a.out32)
-    hipLaunchKernelGGL((sparse_mla_combine_kernel<kF16, true>), grid, dim3(256), 0, stream, a.part_o32, a.part_lse,
+    hipLaunchKernelGGL((sparse_mla_combine_kernel<kF16, true, 4>), grid, dim3(256), 0, stream, a.part_o32, a.part_lse,
                        a.splits, rows, a.sinks, a.slot_count, a.H, a.out32, a.lse);
+  else if (a.splits <= 4)
+    hipLaunchKernelGGL((sparse_mla_combine_kernel<kF16, false, 4>), grid, dim3(256), 0, stream, a.part_o, a.part_lse,
+                       a.splits, rows, a.sinks, a.slot_count, a.H, a.out, a.lse);
   else
-    hipLaunchKernelGGL((sparse_mla_combine_kernel<kF16, false>), grid, dim3(256), 0, stream, a.part_o, a.part_lse,
+    hipLaunchKernelGGL((sparse_mla_combine_kernel<kF16, false, 8>), grid, dim3(256), 0, stream, a.part_o, a.part_lse,
                        a.splits, rows, a.sinks, a.slot_count, a.H, a.out, a.lse);
   return hipGetLastError();
 }
