@@ -717,10 +717,16 @@ __device__ __forceinline__ void indexer_body(const IdxArgs& a) {
     }
     __syncthreads();
   };
-  for (int tile = 0; tile < ntiles; tile += 2) {
+  // Pairs of tiles, the odd last one after the loop: with a conditional second
+  // step the loop's back edge could follow the first step alone, and the
+  // compiler waited at the top of every trip for the loads that path leaves
+  // in flight.
+  int tile = 0;
+  for (; tile + 1 < ntiles; tile += 2) {
     step(Slot0{}, tile);
-    if (tile + 1 < ntiles) step(Slot1{}, tile + 1);
+    step(Slot1{}, tile + 1);
   }
+  if (tile < ntiles) step(Slot0{}, tile);
 
   if constexpr (kMode == kModeDense) {
     // Keys of this chunk past every token's bound: -inf.
