@@ -73,6 +73,16 @@ struct MlaGeom {
   // one cache.  Fixed per width, so neither pays for the other's features.
   static constexpr bool kRowLists = kD == 512;
 };
+// LDS of a workgroup whose ring has kSt stages: the stages, then the slot table
+// (physical rows), the flag words and one valid-slot bitmask per tile.
+template <int kD, int kSt>
+struct MlaLayout {
+  static constexpr int kRowsOffset = kSt * MlaGeom<kD>::kStageBytes;
+  static constexpr int kTileMaskOffset = kRowsOffset + kSlotsCap * 4 + 16;
+  static constexpr int kLds = kTileMaskOffset + (kSlotsCap / 32) * 4;
+};
+static_assert(MlaLayout<576, kStages>::kLds == MlaGeom<576>::kLds, "the 4-stage layout is MlaGeom's");
+
 // Reference max = first valid tile's max + kRefBias (log2); the fast path accepts
 // P up to 2^kOverflowGuard.  bf16 shares fp32's exponent range; fp16 P must stay
 // within [2^-14, 65504].
@@ -601,12 +611,20 @@ __device__ __attribute__((noinline)) void mla_exact_fallback(const uint16_t* q, 
 }
 
 // kPaged: the KV rows are addressed through a block table (a.block_table).
-template <int kNW, bool kF16, int kD, bool kPaged>
-__global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
+// kSt: ring stages.  4 (sparse_mla_kernel): the pipelined loop below.  2
+// (sparse_mla_rows2_kernel: the 512-wide row lists with one or two waves, i.e. up
+// to 64 heads): each tile is computed in turn -- Q K^T, softmax, P V -- while the
+// next tile's DMA fills the other stage; the 73 KB of LDS let two workgroups
+// share a CU, so all four SIMDs work and each workgroup's exposed DMA latency,
+// prologue and epilogue overlap the other's.
+template <int kNW, bool kF16, int kD, bool kPaged, int kSt>
+__device__ __forceinline__ void sparse_mla_body(MlaArgs a) {
+  static_assert(kSt == kStages || kSt == 2, "ring stages");
   using Cfg = MlaCfg<kNW, kD>;
   using Geo = MlaGeom<kD>;
+  using Lay = MlaLayout<kD, kSt>;
   extern __shared__ __align__(16) uint8_t lds[];
-  int32_t* rows = reinterpret_cast<int32_t*>(lds + Geo::kRowsOffset);
+  int32_t* rows = reinterpret_cast<int32_t*>(lds + Lay::kRowsOffset);
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform
@@ -716,7 +734,7 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   __syncthreads();
   // Each wave wrote 64 consecutive slots per pass; record, per tile of 32,
   // the bitmask of its valid slots.
-  uint32_t* tile_mask = reinterpret_cast<uint32_t*>(lds + Geo::kTileMaskOffset);
+  uint32_t* tile_mask = reinterpret_cast<uint32_t*>(lds + Lay::kTileMaskOffset);
   int wave_first = 0x7fffffff;  // lowest valid slot this wave saw (wave-uniform)
   int wave_last = -1;           // highest
 #pragma unroll
@@ -794,12 +812,12 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
       pv_lane[par] = 1024 * (g >> 1) + 128 * u + 16 * ((4 * par + (r & 3)) ^ lds_swizzle(u, g >> 1));
   }
   auto stage_k = [&](int tile, uint32_t (&out)[2]) {
-    const uint32_t base = lds_u32(lds + (tile % kStages) * kStageBytes);
+    const uint32_t base = lds_u32(lds + (tile % kSt) * kStageBytes);
     out[0] = base + qk_lane[0];
     out[1] = base + qk_lane[1];
   };
   auto stage_v = [&](int tile, uint32_t (&out)[2]) {
-    const uint32_t base = lds_u32(lds + (tile % kStages) * kStageBytes);
+    const uint32_t base = lds_u32(lds + (tile % kSt) * kStageBytes);
     out[0] = base + pv_lane[0];
     out[1] = base + pv_lane[1];
   };
@@ -837,7 +855,58 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
   // softmax turns S(t+1) into P(t+1) (phase B).  One barrier per tile: it
   // publishes tile t+1 and certifies that every wave is done with tile t-1,
   // whose stage the DMA of tile t + kDepth then refills.
-  if (ntiles > 0) {
+  if (kSt == 2 && ntiles > 0) {
+    // Two stages: tile t in stage t & 1; the DMA of tile t + 1 goes out spread
+    // over the Q K^T of tile t, into the stage tile t - 1 left.
+    {
+      TileDma<kNW, kD> dma;
+      dma.prepare(kvb, kvb2, trows, safe_row, 0, lds, wave, lane);
+      il_dma_all(dma);
+    }
+    u32x4 pa[2];
+    for (int tile = 0; tile < ntiles; ++tile) {
+      // Tile `tile` has arrived (vector-memory loads complete in order, so this
+      // also covers Q); the barrier publishes it and certifies that every wave
+      // is done with tile - 1.
+      wait_vmcnt<0>();
+      raw_barrier();
+      const bool more = tile + 1 < ntiles;  // workgroup-uniform
+      TileDma<kNW, kD> dma;
+      if (more) dma.prepare(kvb, kvb2, trows, safe_row, tile + 1, lds + ((tile + 1) % kSt) * kStageBytes, wave, lane);
+      f32x4 c[2][2];
+      uint32_t qa[2], va[2];
+      stage_k(tile, qa);
+      stage_v(tile, va);
+      if (more) qk_phase<kF16, kNW, kD, true>(c, qb, qa, dma);
+      else qk_phase<kF16, kNW, kD, false>(c, qb, qa, dma);
+      mask_scores(c, __builtin_amdgcn_readfirstlane(tmask[tile]));
+      if (tile == 0) {
+        // The first processed tile holds the first valid slot: it fixes m_ref.
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb) {
+          float cmax = -__builtin_huge_valf();
+#pragma unroll
+          for (int e = 0; e < 8; ++e) cmax = fmaxf(cmax, c[hb][e / 4][e % 4]);
+          cmax = fmaxf(cmax, __shfl_xor(cmax, 16, kWave));
+          cmax = fmaxf(cmax, __shfl_xor(cmax, 32, kWave));
+          m_ref[hb] = cmax * scale_log2 + PRange<kF16>::kRefBias;
+        }
+      }
+      Softmax sm{c, pa, lsum, lsum_r, overflow, {-m_ref[0], -m_ref[1]}, scale_log2, {}};
+      sm.template run<0>();
+      sm.template run<1>();
+      sm.template run<2>();
+      sm.template run<3>();
+      sm.template run<4>();
+      sm.template run<5>();
+      sm.template run<6>();
+      sm.template run<7>();
+      sm.template run<8>();
+      sm.template run<9>();
+      pv_only<kF16>(o, pa, va);
+    }
+  }
+  if (kSt == kStages && ntiles > 0) {
     // The first kDepth stages are filled now (a row of fewer tiles re-loads its
     // last tile into the stages it does not use), unconditionally, so that the
     // compiler sees a fixed count of loads behind Q: the wait for tile 0 then
@@ -1044,6 +1113,16 @@ __global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
           ltot_h[hb] > 0.f ? (mout_h[hb] + fast_log2(ltot_h[hb])) * 0.69314718055994531f : -__builtin_huge_valf();
 }
 
+template <int kNW, bool kF16, int kD, bool kPaged>
+__global__ __launch_bounds__(kNW * kWave) void sparse_mla_kernel(MlaArgs a) {
+  sparse_mla_body<kNW, kF16, kD, kPaged, kStages>(a);
+}
+
+template <int kNW, bool kF16>
+__global__ __launch_bounds__(kNW * kWave) void sparse_mla_rows2_kernel(MlaArgs a) {
+  sparse_mla_body<kNW, kF16, 512, false, 2>(a);
+}
+
 // Merge split partials: lse = log(sum_i exp(lse_i) [+ exp(sink)]),
 // out = sum_i exp(lse_i - lse) * o_i.  kF32: partials and out are fp32 (row
 // lists with an fp32 output), else 16-bit.  kU: splits visited at a time; with
@@ -1241,11 +1320,19 @@ hipError_t mla_scratch_ptr(void** out) {
 
 template <int kNW, bool kF16, int kD, bool kPaged>
 static hipError_t launch_mla_kernel(const MlaArgs& a, int head_groups, hipStream_t stream) {
-  constexpr int kLds = MlaGeom<kD>::kLds;
-  const hipError_t ea = set_dynamic_lds_once<sparse_mla_kernel<kNW, kF16, kD, kPaged>>(kLds);
-  if (ea != hipSuccess) return ea;
   const dim3 grid((unsigned)((int64_t)a.B * a.S * a.G * a.splits), (unsigned)head_groups);
-  hipLaunchKernelGGL((sparse_mla_kernel<kNW, kF16, kD, kPaged>), grid, dim3(kNW * kWave), kLds, stream, a);
+  if constexpr (kD == 512 && kNW <= 2) {
+    // Two-stage ring for the 512-wide row lists of up to 64 heads (see the kernel).
+    constexpr int kLds = MlaLayout<512, 2>::kLds;
+    const hipError_t ea = set_dynamic_lds_once<sparse_mla_rows2_kernel<kNW, kF16>>(kLds);
+    if (ea != hipSuccess) return ea;
+    hipLaunchKernelGGL((sparse_mla_rows2_kernel<kNW, kF16>), grid, dim3(kNW * kWave), kLds, stream, a);
+  } else {
+    constexpr int kLds = MlaLayout<kD, kStages>::kLds;
+    const hipError_t ea = set_dynamic_lds_once<sparse_mla_kernel<kNW, kF16, kD, kPaged>>(kLds);
+    if (ea != hipSuccess) return ea;
+    hipLaunchKernelGGL((sparse_mla_kernel<kNW, kF16, kD, kPaged>), grid, dim3(kNW * kWave), kLds, stream, a);
+  }
   return hipGetLastError();
 }
 
