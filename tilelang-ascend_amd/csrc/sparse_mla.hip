@@ -42,6 +42,11 @@
 // between them, then the PV MFMAs of tile t with the softmax of tile t+1 cut
 // into slices between them.  With more than one split a workgroup writes a
 // normalised bf16 partial and its LSE; a combine kernel merges them.
+//
+// The 512-wide row lists of up to 64 heads (one or two waves) run the same
+// body from a two-stage ring instead (sparse_mla_rows2_kernel): one tile is
+// computed at a time while the next arrives, in 73 KB of LDS, so that two
+// workgroups share a CU and every SIMD holds a wave.
 #include "common.hpp"
 
 namespace dsa {
