@@ -165,6 +165,35 @@ def test_split_path_and_no_sink(dsa, dev):
         torch.testing.assert_close(_lse(dsa, dev, q, kv, sk, idx, scale), want_lse, rtol=1e-3, atol=1e-3)
 
 
+@pytest.mark.parametrize("jump", [40.0, 200.0])  # within the fixed reference's headroom / beyond it
+def test_row_lists_large_score_jumps(dsa, dev, jump):
+    """40 rows of 64 heads (the two-stage row-list kernel) whose last four tiles score ~jump (base 2)
+    above the first four: within the bf16 headroom of the fixed reference max, and beyond it, where
+    the workgroup recomputes exactly (its scratch and flags in the two-stage LDS layout)."""
+    b, m, n, h, d, topk = 1, 40, 1024, 64, 512, 256
+    g = torch.Generator().manual_seed(21)
+    q = torch.zeros(b, m, h, d)
+    q[..., :64] = 1.0
+    q += torch.randn(b, m, h, d, generator=g) * 0.01
+    kv = torch.randn(b, n, d, generator=g) * 0.5
+    scale = 512 ** -0.5
+    # base-2 score = scale * log2(e) * q.k ~= 64 * c * scale * log2(e) for a row with c in its first 64 dims
+    kv[0, 512:, :64] = jump / (64 * scale * 1.4426950408889634)
+    idx = torch.empty(b, m, topk, dtype=torch.int32)
+    for t in range(m):
+        low = torch.randperm(512, generator=g)[:topk // 2]
+        high = 512 + torch.randperm(512, generator=g)[:topk // 2]
+        idx[0, t] = torch.cat([low, high]).to(torch.int32)  # the first four tiles all low
+    sink = torch.randn(h, generator=g)
+    q, kv = q.to(torch.bfloat16), kv.to(torch.bfloat16)
+    print(f"sparse_attn row lists b=1 m=40 h=64 topk=256 jump={jump}", flush=True)
+    out = _run(dsa, dev, q, kv, sink, idx, scale)
+    want, want_lse = ref.sparse_attn_sink(q, kv, sink, idx, scale)
+    assert torch.isfinite(out).all()
+    torch.testing.assert_close(out, want, atol=2e-2, rtol=2e-2)
+    torch.testing.assert_close(_lse(dsa, dev, q, kv, sink, idx, scale), want_lse, rtol=1e-3, atol=1e-3)
+
+
 def test_rejects_bad_shapes(dsa, dev):
     q, kv, sink, idx = _inputs(1, 2, 8, 16, 512, 4, torch.bfloat16, 46)
     with pytest.raises(ValueError):
