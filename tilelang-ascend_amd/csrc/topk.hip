@@ -575,8 +575,12 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
         v[c][j] = p < nv ? __uint_as_float(crow[cand_slot(soff, cs.cap, p)].x) : -__builtin_huge_valf();
       }
   } else if constexpr (kFull) {
+    // With 8 chunks the even ones are loaded first: the sample below reads only
+    // them, so it waits for half the loads and the rest arrive meanwhile.
 #pragma unroll
-    for (int c = 0; c < kChunks; ++c) {
+    for (int i = 0; i < kChunks; ++i) {
+      const int c = kChunks == 8 ? 2 * (i & 3) + (i >> 2) : i;
+      if (kChunks == 8 && i == 4) __builtin_amdgcn_sched_barrier(0);  // the even loads stay first
       const f32x4 t = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(xr) + tid + c * kTopkThreads);
       v[c][0] = t[0]; v[c][1] = t[1]; v[c][2] = t[2]; v[c][3] = t[3];
     }
@@ -616,15 +620,19 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
   __syncthreads();
 
   // 2. Sample: wave w takes register (c, j) = (w % kChunks, (w / kChunks) % 4),
-  // 64 positions 4 apart in each of 16 windows spread over the row.  (A
-  // separate, earlier sample load costs more than it saves: the row loads
-  // fetched its lines from HBM a second time.)
+  // 64 positions 4 apart in each of 16 windows spread over the row; with 8
+  // chunks only the even ones, (2 (w % 4), (w / 4) % 4), which still span the
+  // row: each sample then stands for the same number of positions, the odd
+  // chunk beside it taken to look alike.  (A separate, earlier sample load costs
+  // more than it saves: the row loads fetched its lines from HBM a second time.)
+  constexpr int kSampleChunks = kChunks == 8 ? 4 : kChunks;
+  constexpr int kSampleStep = kChunks / kSampleChunks;
   float s = v[0][0];
 #pragma unroll
-  for (int c = 0; c < kChunks; ++c)
+  for (int c = 0; c < kChunks; c += kSampleStep)
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      if (wave % kChunks == c && (wave / kChunks) % 4 == j) s = v[c][j];  // wave-uniform choice
+      if (wave % kSampleChunks == c / kSampleStep && (wave / kSampleChunks) % 4 == j) s = v[c][j];  // wave-uniform
   const uint32_t sk = float_key(s);
   const bool sp = sk > kKeyInvalidMax;  // present: > -1e30, not NaN
   if (sp) atomicAdd(&shc[sk >> 22], 1u);
