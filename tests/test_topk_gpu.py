@@ -138,6 +138,21 @@ def test_long_rows_row_len_and_strides(dsa, dev):
     _check(dsa, dev, x, 2048, row_len=row_len)
 
 
+def test_row_len_aligned_rows_every_tail(dsa, dev):
+    """16-byte aligned rows of 8 register chunks with row lengths: the last whole group of 4 in an
+    even and an odd chunk, a partial group after it or none, lengths below 4 (no whole group)."""
+    g = torch.Generator().manual_seed(78)
+    x = torch.randn(14, 32768, generator=g)
+    x[12, 9000:] = float("-inf")  # masked inside the length
+    row_len = torch.tensor([0, 1, 3, 5, 2049, 4097, 8195, 16386, 20001, 28673, 32767, 32768, 30000, 4096],
+                           dtype=torch.int32)
+    _check(dsa, dev, x, 2048, row_len=row_len)
+    _check(dsa, dev, x, 100, sorted=False, row_len=row_len)
+    x2 = torch.randn(6, 20000, generator=g)  # 20000 scores a row: 8 chunks, the last ones past the row
+    _check(dsa, dev, x2, 2048, row_len=torch.tensor([0, 2, 2050, 10001, 19999, 20000], dtype=torch.int32))
+    _check(dsa, dev, x2, 2048)
+
+
 def test_long_rows_ws_matches_plain_entry(dsa, dev):
     # dsa_topk_select (no workspace: radix passes) and dsa_topk_select_ws agree bit for bit.
     from tilelang_ascend_amd import _lib as L

@@ -416,9 +416,13 @@ __device__ __forceinline__ uint32_t cand_pos(float x, uint32_t floor_bits) {
   return (u >> 31) ? 0x80000000u - cm : 0x80000000u + cm;
 }
 
+// Four absent scores: what a register group past a row's last whole group of 4 reads.
+__device__ __align__(16) float kTopkAbsent4[4] = {-__builtin_huge_valf(), -__builtin_huge_valf(),
+                                                  -__builtin_huge_valf(), -__builtin_huge_valf()};
+
 // Ballot compaction of the scores >= t among a thread's registers into
-// lv/lp from index `base` on (wave-uniform), in register order; returns the
-// wave's count.  Position of register (c, j): e4 + 4096 c + j, or with
+// lv/lp from index `base` on (wave-uniform), registers in the order the row's
+// loads are issued (with 8 chunks the even ones first); returns the wave's count.  Position of register (c, j): e4 + 4096 c + j, or with
 // kLaneMajor e4 + 1024 (4 c + j).
 template <int kChunks, bool kLaneMajor = false>
 __device__ __forceinline__ uint32_t compact_scores(const float (&v)[kChunks][4], float t, uint32_t base, uint32_t e4,
@@ -428,9 +432,10 @@ __device__ __forceinline__ uint32_t compact_scores(const float (&v)[kChunks][4],
   uint32_t e4o;
   __asm__ volatile("v_mov_b32 %0, %1" : "=v"(e4o) : "v"(e4));
 #pragma unroll
-  for (int c = 0; c < kChunks; ++c)
+  for (int q = 0; q < kChunks; ++q)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      const int c = kChunks == 8 ? 2 * (q & 3) + (q >> 2) : q;
       const float val = v[c][j];
       const bool p = val >= t;
       const uint64_t m = __builtin_amdgcn_ballot_w64(p);
@@ -497,12 +502,13 @@ __device__ void cand_spill(const CandSegments& cs, const u32x2* crow, const int 
 // kCand: the rows are the fused indexer's candidates in their key chunks (cs;
 // x, row_len and idx_map unused), positions 0..ldc; thread t holds positions
 // t + 1024 (4 c + j), so a wave's loads of one register are contiguous.
-template <int kChunks, bool kFull, bool kCand = false>
+template <int kChunks, bool kFull, bool kCand = false, bool kAligned = false>
 __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8, 8))) void topk_reg_kernel(
     const float* __restrict__ x, int64_t ld, int n, int k, const int32_t* __restrict__ row_len,
     int32_t* __restrict__ out_idx, float* __restrict__ out_val, int nseg, int seg_len,
     const int32_t* __restrict__ idx_map, const CandSegments cs) {
   static_assert(!(kFull && kCand), "candidate rows are ragged");
+  static_assert(!(kAligned && (kFull || kCand)), "kAligned: ragged rows of 16-byte aligned scores");
   __shared__ __align__(16) uint32_t lds[kLdsRegWords];
   uint32_t* lv = lds + kLdsVal;
   uint32_t* lp = lds + kLdsPos;
@@ -566,6 +572,9 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
   // 16-byte aligned, so the loads are straight-line.
   float v[kChunks][4];
   const int g_full = nv >> 2;
+  // The chunks the sample reads (every kSampleStep-th; with 8 chunks the even ones).
+  constexpr int kSampleChunks = kChunks == 8 ? 4 : kChunks;
+  constexpr int kSampleStep = kChunks / kSampleChunks;
   if constexpr (kCand) {
 #pragma unroll
     for (int c = 0; c < kChunks; ++c)
@@ -584,27 +593,19 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
       const f32x4 t = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(xr) + tid + c * kTopkThreads);
       v[c][0] = t[0]; v[c][1] = t[1]; v[c][2] = t[2]; v[c][3] = t[3];
     }
-  } else if ((reinterpret_cast<uintptr_t>(xr) & 15) == 0) {  // block-uniform
-    // Whole groups of 4 with 16-byte loads; the one partial group at the end by element.
-    const f32x4 ninf4 = {-__builtin_huge_valf(), -__builtin_huge_valf(), -__builtin_huge_valf(), -__builtin_huge_valf()};
+  } else if constexpr (kAligned) {
+    // Every row 16-byte aligned (checked on the host): whole groups of 4 with 16-byte
+    // loads in the order above, unconditional -- a group past the row's last whole one
+    // reads four absent scores from kTopkAbsent4 -- so that the sample's wait can be
+    // counted; the one partial group at the end is filled in after the sample.
 #pragma unroll
-    for (int c = 0; c < kChunks; ++c) {
+    for (int i = 0; i < kChunks; ++i) {
+      const int c = kChunks == 8 ? 2 * (i & 3) + (i >> 2) : i;
+      if (kChunks == 8 && i == 4) __builtin_amdgcn_sched_barrier(0);
       const int g = tid + c * kTopkThreads;
-      f32x4 t = ninf4;
-      if (g < g_full) t = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(xr) + g);
+      const f32x4* src = g < g_full ? reinterpret_cast<const f32x4*>(xr) + g : reinterpret_cast<const f32x4*>(kTopkAbsent4);
+      const f32x4 t = __builtin_nontemporal_load(src);
       v[c][0] = t[0]; v[c][1] = t[1]; v[c][2] = t[2]; v[c][3] = t[3];
-    }
-    if (nv & 3) {
-      const int g = g_full;  // its owner: thread g % 1024, chunk g / 1024
-      if (tid == (g & (kTopkThreads - 1))) {
-#pragma unroll
-        for (int c = 0; c < kChunks; ++c)
-          if (c == g / kTopkThreads) {
-#pragma unroll
-            for (int j = 0; j < 3; ++j)
-              if (4 * g + j < nv) v[c][j] = xr[4 * g + j];
-          }
-      }
     }
   } else {
 #pragma unroll
@@ -625,8 +626,6 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
   // row: each sample then stands for the same number of positions, the odd
   // chunk beside it taken to look alike.  (A separate, earlier sample load costs
   // more than it saves: the row loads fetched its lines from HBM a second time.)
-  constexpr int kSampleChunks = kChunks == 8 ? 4 : kChunks;
-  constexpr int kSampleStep = kChunks / kSampleChunks;
   float s = v[0][0];
 #pragma unroll
   for (int c = 0; c < kChunks; c += kSampleStep)
@@ -642,6 +641,20 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
   if (lane == 0) red[kRedPresent + wave] = wave_present;
   __syncthreads();
   const int s_present = (int)row0_sum(lane < kTopkWaves ? red[kRedPresent + lane] : 0u);
+  if constexpr (kAligned) {  // the partial group left from the loads
+    if (nv & 3) {
+      const int g = g_full;  // its owner: thread g % 1024, chunk g / 1024
+      if (tid == (g & (kTopkThreads - 1))) {
+#pragma unroll
+        for (int c = 0; c < kChunks; ++c)
+          if (c == g / kTopkThreads) {
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+              if (4 * g + j < nv) v[c][j] = xr[4 * g + j];
+          }
+      }
+    }
+  }
 
   // 3. Threshold and candidate compaction.  Sample rank r aims at
   // (k + kCandCap) / 2 candidates; r > s_present admits every present score.
@@ -852,14 +865,14 @@ static hipError_t launch_reg(const float* x, int64_t ld, int64_t rows, int64_t n
                              hipStream_t stream) {
   const dim3 grid((unsigned)rows), block(kTopkThreads);
   const int chunks = seg_len <= 4 * kTopkThreads ? 1 : seg_len <= 8 * kTopkThreads ? 2 : seg_len <= 16 * kTopkThreads ? 4 : 8;
-  // Every row (segment) whole and 16-byte aligned: the straight-line load path.
-  const bool full = row_len == nullptr && seg_len == 4 * kTopkThreads * chunks && n == nseg * seg_len &&
-                    (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (ld & 3) == 0;
-#define DSA_REG(C, F)                                                                                         \
-  hipLaunchKernelGGL((topk_reg_kernel<C, F>), grid, block, 0, stream, x, ld, (int)n, (int)k, row_len, out_idx, \
-                     out_val, nseg, (int)seg_len, idx_map, CandSegments{})
+  // Every row (segment) starts 16-byte aligned: 16-byte loads; and whole besides: no masks.
+  const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (ld & 3) == 0 && (seg_len & 3) == 0;
+  const bool full = aligned && row_len == nullptr && seg_len == 4 * kTopkThreads * chunks && n == nseg * seg_len;
+#define DSA_REG(C, F, A)                                                                                               \
+  hipLaunchKernelGGL((topk_reg_kernel<C, F, false, A>), grid, block, 0, stream, x, ld, (int)n, (int)k, row_len, \
+                     out_idx, out_val, nseg, (int)seg_len, idx_map, CandSegments{})
 #define DSA_REG2(C) \
-  if (full) DSA_REG(C, true); else DSA_REG(C, false)
+  if (full) DSA_REG(C, true, false); else if (aligned) DSA_REG(C, false, true); else DSA_REG(C, false, false)
   if (chunks == 1) DSA_REG2(1);
   else if (chunks == 2) DSA_REG2(2);
   else if (chunks == 4) DSA_REG2(4);
