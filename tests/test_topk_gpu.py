@@ -118,6 +118,24 @@ def test_mixed_fast_and_exact_rows(dsa, dev):
     _check(dsa, dev, x, 100, sorted=False)
 
 
+@pytest.mark.parametrize("N", [4096, 32768])
+def test_whole_rows_exact_in_place(dsa, dev, N):
+    """Whole 16-byte aligned rows (4096 * chunks scores, no lengths): the rows the register path
+    cannot bound take the exact select inside the same workgroup, with no pass behind."""
+    g = torch.Generator().manual_seed(N + 11)
+    x = torch.randn(10, N, generator=g)
+    x[1] = 0.5                                                 # one value throughout
+    x[3] = torch.randint(0, 3, (N,), generator=g).float()      # three values
+    x[5, 123] = 3.0e38                                         # outliers
+    x[5, N // 2] = -3.0e38
+    x[7, :] = float("-inf")
+    x[7, 17] = 1.0                                             # a single present score
+    x[8, ::2] = 2.0                                            # ties on every other position
+    _check(dsa, dev, x, 2048)
+    _check(dsa, dev, x, 1, sorted=False)
+    _check(dsa, dev, x, 4096)
+
+
 # Rows longer than 32768 scores: segments, then a top-k over the segments' candidates.
 @pytest.mark.parametrize("N,K", [(131072, 2048), (50001, 100), (40000, 4096)])
 def test_long_rows_two_stage(dsa, dev, N, K):

@@ -73,13 +73,14 @@ __device__ __forceinline__ uint32_t load_key(const float* __restrict__ xr, const
   return float_key(xr[i]);
 }
 
-// One row by the whole workgroup (every thread calls it, with the same row).
+// One row by the whole workgroup (every thread calls it, with the same row), in
+// `lds`: (kHistBins + kRedWords) words, kpad * 8 bytes when sorted, then the
+// row's keys when kCached.
 template <bool kCached>
 __device__ __forceinline__ void radix_row(const int row, const float* __restrict__ x, int64_t ld, int n, int k,
                                           const int32_t* __restrict__ row_len, int sorted, int kpad,
                                           int32_t* __restrict__ out_idx, float* __restrict__ out_val,
-                                          int only_flagged, const int32_t* __restrict__ idx_map) {
-  extern __shared__ __align__(16) uint32_t lds[];
+                                          int only_flagged, const int32_t* __restrict__ idx_map, uint32_t* lds) {
   uint32_t* hist = lds;                                     // kHistBins
   uint32_t* red = hist + kHistBins;                         // kRedWords
   uint64_t* sbuf = reinterpret_cast<uint64_t*>(red + kRedWords);  // kpad (sorted only)
@@ -251,9 +252,10 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(
     int sorted, int kpad, int32_t* __restrict__ out_idx, float* __restrict__ out_val, int only_flagged,
     const int32_t* __restrict__ idx_map, int rows, const int32_t* __restrict__ gate) {
   typedef const __attribute__((address_space(4))) int32_t const_i32;
+  extern __shared__ __align__(16) uint32_t rows_lds[];  // after the static `flagged` masks
   if (only_flagged && gate && *(const_i32*)gate == 0) return;  // block-uniform
   if (!only_flagged) {
-    radix_row<kCached>(blockIdx.x, x, ld, n, k, row_len, sorted, kpad, out_idx, out_val, 0, idx_map);
+    radix_row<kCached>(blockIdx.x, x, ld, n, k, row_len, sorted, kpad, out_idx, out_val, 0, idx_map, rows_lds);
     return;
   }
   __shared__ uint64_t flagged[kTopkWaves];
@@ -272,7 +274,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(
         const int b = __builtin_ctzll(mw);
         mw &= mw - 1;
         radix_row<kCached>((int)(r0 + (int64_t)(w * kWave + b) * G), x, ld, n, k, row_len, sorted, kpad, out_idx,
-                           out_val, 1, idx_map);
+                           out_val, 1, idx_map, rows_lds);
         __syncthreads();  // the row's LDS is free before the next one
       }
     }
@@ -567,6 +569,29 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
     }
   }
 
+  // A row this path cannot bound (block-uniform): a whole row (kFull, one
+  // segment) takes the exact radix select right here, in the same LDS, so the
+  // launch needs no pass behind; other rows are flagged for the exact pass, and
+  // candidate rows also copied out packed for it.  (Inlined into the ragged
+  // variants, the select's registers made their main path spill.)
+  auto hand_over = [&]() {
+    if constexpr (kCand) {
+      if (tid == 0) oi[0] = kFallbackFlag;
+      cand_spill(cs, crow, soff, row, nv);
+    } else if constexpr (kFull) {
+      if (nseg == 1) {  // block-uniform
+        const int kp = k < 2 ? 2 : k;
+        radix_row<false>(row, x, ld, n, k, row_len, 1, 1 << (32 - __builtin_clz(kp - 1)), out_idx, out_val, 0,
+                         nullptr, lds);
+      } else if (tid == 0) {
+        oi[0] = kFallbackFlag;
+      }
+    } else if (tid == 0) {
+      oi[0] = kFallbackFlag;
+    }
+  };
+  static_assert((kHistBins + kRedWords) + 2 * kListCap <= kLdsRegWords, "the exact select fits the register path's LDS");
+
   // 1. Load: thread t holds positions 4*(t + c*1024) .. +3 of chunk c.  kFull:
   // the host has checked that every row is whole (4096 * kChunks scores) and
   // 16-byte aligned, so the loads are straight-line.
@@ -666,7 +691,7 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
   const uint32_t e4 = kCand ? (uint32_t)tid : 4u * (uint32_t)tid;
   const uint32_t wreg = (uint32_t)wave * kWaveCap;
   uint32_t total = 0, held = 0;
-  bool all_present = false, dense = false;
+  bool all_present = false, dense = false, handed = false;
   float t = floor_t;
   for (int tries = 0;; ++tries) {
     all_present = r > s_present;
@@ -714,14 +739,13 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
     }
     if (over) hi = r;
     else lo = r;
-    if (hi - lo <= 1 || tries + 1 == kMaxTries) {
-      if (tid == 0) oi[0] = kFallbackFlag;
-      if constexpr (kCand) cand_spill(cs, crow, soff, row, nv);
-      return;  // block-uniform
+    if (hi - lo <= 1 || tries + 1 == kMaxTries) {  // block-uniform: nothing selected; handed over at the end
+      handed = true;
+      break;
     }
     r = (lo + hi + 1) / 2;
   }
-  const int kk = all_present ? min((int)total, k) : k;
+  const int kk = handed ? 0 : all_present ? min((int)total, k) : k;
   if (dense) {  // block-uniform
     uint32_t cw = lane < kTopkWaves ? red[kRedCount + lane] : 0u;
     const uint32_t own = cw;
@@ -846,11 +870,9 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
   }
   if (kk > 0) {
     __syncthreads();
-    if (red[kRedFlag]) {  // block-uniform
-      if (tid == 0) oi[0] = kFallbackFlag;
-      if constexpr (kCand) cand_spill(cs, crow, soff, row, nv);
-    }
+    handed = red[kRedFlag] != 0;  // block-uniform
   }
+  if (handed) hand_over();  // the one call site: the exact select is inlined once
 }
 
 static int next_pow2(int v) {
@@ -859,15 +881,30 @@ static int next_pow2(int v) {
   return p;
 }
 
+static int reg_chunks(int64_t seg_len) {
+  return seg_len <= 4 * kTopkThreads ? 1 : seg_len <= 8 * kTopkThreads ? 2 : seg_len <= 16 * kTopkThreads ? 4 : 8;
+}
+
+// Every row (segment) starts 16-byte aligned: 16-byte loads.
+static bool reg_aligned(const float* x, int64_t ld, int64_t seg_len) {
+  return (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (ld & 3) == 0 && (seg_len & 3) == 0;
+}
+
+// Aligned and whole besides (no row lengths, 4096 * chunks scores a segment): no masks,
+// and with one segment the rows it cannot bound are finished in place.
+static bool reg_full(const float* x, int64_t ld, const int32_t* row_len, int64_t n, int nseg, int64_t seg_len) {
+  return reg_aligned(x, ld, seg_len) && row_len == nullptr && seg_len == 4 * kTopkThreads * reg_chunks(seg_len) &&
+         n == nseg * seg_len;
+}
+
 // Launch on `stream`: `rows` output rows (rows / nseg input rows of nseg segments of seg_len).
 static hipError_t launch_reg(const float* x, int64_t ld, int64_t rows, int64_t n, int64_t k, const int32_t* row_len,
                              int32_t* out_idx, float* out_val, int nseg, int64_t seg_len, const int32_t* idx_map,
                              hipStream_t stream) {
   const dim3 grid((unsigned)rows), block(kTopkThreads);
-  const int chunks = seg_len <= 4 * kTopkThreads ? 1 : seg_len <= 8 * kTopkThreads ? 2 : seg_len <= 16 * kTopkThreads ? 4 : 8;
-  // Every row (segment) starts 16-byte aligned: 16-byte loads; and whole besides: no masks.
-  const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (ld & 3) == 0 && (seg_len & 3) == 0;
-  const bool full = aligned && row_len == nullptr && seg_len == 4 * kTopkThreads * chunks && n == nseg * seg_len;
+  const int chunks = reg_chunks(seg_len);
+  const bool aligned = reg_aligned(x, ld, seg_len);
+  const bool full = reg_full(x, ld, row_len, n, nseg, seg_len);
 #define DSA_REG(C, F, A)                                                                                               \
   hipLaunchKernelGGL((topk_reg_kernel<C, F, false, A>), grid, block, 0, stream, x, ld, (int)n, (int)k, row_len, \
                      out_idx, out_val, nseg, (int)seg_len, idx_map, CandSegments{})
@@ -926,7 +963,7 @@ hipError_t launch_topk(const float* x, int64_t ld, int64_t rows, int64_t n, int6
   const int nseg = workspace ? long_row_segments(rows, n, k) : 0;
   if (n <= kRegMax && k <= kListCap) {
     hipError_t e = launch_reg(x, ld, rows, n, k, row_len, out_idx, out_val, 1, n, nullptr, stream);
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess || reg_full(x, ld, row_len, n, 1, n)) return e;  // whole rows: finished in place
     only_flagged = 1;
     sorted = 1;
   } else if (nseg > 0) {
