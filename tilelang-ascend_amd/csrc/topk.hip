@@ -424,8 +424,9 @@ __device__ __align__(16) float kTopkAbsent4[4] = {-__builtin_huge_valf(), -__bui
 
 // Ballot compaction of the scores >= t among a thread's registers into
 // lv/lp from index `base` on (wave-uniform), registers in the order the row's
-// loads are issued (with 8 chunks the even ones first); returns the wave's count.  Position of register (c, j): e4 + 4096 c + j, or with
-// kLaneMajor e4 + 1024 (4 c + j).
+// loads are issued (with 8 chunks the even ones first); returns the wave's
+// count.  Position of register (c, j): e4 + 4096 c + j, or with kLaneMajor
+// e4 + 1024 (4 c + j).
 template <int kChunks, bool kLaneMajor = false>
 __device__ __forceinline__ uint32_t compact_scores(const float (&v)[kChunks][4], float t, uint32_t base, uint32_t e4,
                                                    uint32_t* lv, uint32_t* lp) {
@@ -590,7 +591,8 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
       oi[0] = kFallbackFlag;
     }
   };
-  static_assert((kHistBins + kRedWords) + 2 * kListCap <= kLdsRegWords, "the exact select fits the register path's LDS");
+  static_assert((kHistBins + kRedWords) + 2 * kListCap <= kLdsRegWords,
+                "the exact select fits the register path's LDS");
 
   // 1. Load: thread t holds positions 4*(t + c*1024) .. +3 of chunk c.  kFull:
   // the host has checked that every row is whole (4096 * kChunks scores) and
@@ -628,7 +630,8 @@ __global__ __launch_bounds__(kTopkThreads) __attribute__((amdgpu_waves_per_eu(8,
       const int c = kChunks == 8 ? 2 * (i & 3) + (i >> 2) : i;
       if (kChunks == 8 && i == 4) __builtin_amdgcn_sched_barrier(0);
       const int g = tid + c * kTopkThreads;
-      const f32x4* src = g < g_full ? reinterpret_cast<const f32x4*>(xr) + g : reinterpret_cast<const f32x4*>(kTopkAbsent4);
+      const f32x4* src =
+          g < g_full ? reinterpret_cast<const f32x4*>(xr) + g : reinterpret_cast<const f32x4*>(kTopkAbsent4);
       const f32x4 t = __builtin_nontemporal_load(src);
       v[c][0] = t[0]; v[c][1] = t[1]; v[c][2] = t[2]; v[c][3] = t[3];
     }
